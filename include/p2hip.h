@@ -1,0 +1,138 @@
+/*  p2hip.h – the device-pointer C ABI of the MI355X five-value GEMM (libp2hip.so).
+ *
+ *  The thin layer the C host library (libphonon2_gemm.so, include/p2_blas.h) calls, and the entry points a caller
+ *  with device-resident data uses directly. Plain C types only; streams are hipStream_t passed as void*, NULL means
+ *  the calling thread's default stream of this library. Every kernel entry is asynchronous on its stream.
+ *
+ *  Errors: entries return 0 on success and a negative P2H_E_* code otherwise; p2h_last_error() gives the message
+ *  (per thread). Nothing here falls back to the CPU: without a usable gfx950 device p2h_init fails.
+ *
+ *  Modes follow the reference's numbering (blas.c:1030): P2H_INT8 = 0 (A quantised, weights exact as two
+ *  {-1,0,+1} planes), P2H_EXACT = 1 (fp32 expansion), P2H_INT8W = 2 (A and weights int8, the default).
+ */
+#ifndef P2HIP_H
+#define P2HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { P2H_INT8 = 0, P2H_EXACT = 1, P2H_INT8W = 2 };
+
+enum {
+    P2H_OK = 0,
+    P2H_E_ARG = -1,       /* a shape, stride, alignment or mode the entry does not accept */
+    P2H_E_DEVICE = -2,    /* no usable gfx950 device, or a HIP call failed */
+    P2H_E_NOMEM = -3,     /* device or pinned host allocation failed */
+    P2H_E_WORKSPACE = -4  /* workspace missing or smaller than p2h_*_workspace_bytes */
+};
+
+/* Row padding of quantised activations: Q rows hold K int8 values, zero-filled up to a multiple of this. */
+#define P2H_Q_KALIGN 128
+
+/* ── runtime ────────────────────────────────────────────────────────────────────────────────────────────────── */
+
+int         p2h_init(void);                 /* device 0 must be gfx950; idempotent, thread-safe */
+const char *p2h_last_error(void);
+const char *p2h_device_name(void);          /* gcnArchName of the device in use */
+int         p2h_device_cu_count(void);
+
+void *p2h_stream_create(void);              /* a default-priority stream; NULL on failure */
+int   p2h_stream_destroy(void *stream);
+int   p2h_stream_sync(void *stream);
+void *p2h_thread_stream(void);              /* this thread's stream (created on first use) */
+
+void *p2h_malloc(size_t bytes);             /* device memory; NULL on failure */
+int   p2h_free(void *dptr);
+void *p2h_host_malloc(size_t bytes);        /* pinned host memory */
+int   p2h_host_free(void *hptr);
+int   p2h_memset(void *dptr, int value, size_t bytes, void *stream);
+int   p2h_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int   p2h_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int   p2h_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+/* Row-strided copies: `rows` rows of `row_bytes`, source and destination pitches in bytes. */
+int   p2h_memcpy2d_h2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t row_bytes, size_t rows,
+                       void *stream);
+int   p2h_memcpy2d_d2h(void *dst, size_t dpitch, const void *src, size_t spitch, size_t row_bytes, size_t rows,
+                       void *stream);
+
+void *p2h_event_create(void);
+int   p2h_event_destroy(void *event);
+int   p2h_event_record(void *event, void *stream);
+int   p2h_event_sync(void *event);
+float p2h_event_elapsed_ms(void *start, void *stop);   /* < 0 on error */
+
+/* ── five-value weights ─────────────────────────────────────────────────────────────────────────────────────────
+ *  A device-resident five-value weight [K, N] (blas.h:38-45 FiveValueB; phonon2.h:116-126 Weight): the sign and
+ *  flag planes byte for byte as the reference stores them (signs [K][N/4], flags [K][N/8]), lo[N], hi[N], and the
+ *  per-column epilogue tables derived from them on the device: clo[n] (blas.c:1319-1326), hi[n]/127
+ *  (blas.c:1327-1328), lo[n] and hi[n]-lo[n] (blas.c:1329-1333). N % 16 == 0. */
+typedef struct P2hWeight P2hWeight;
+
+/* Upload from host memory (an mmap of weights.bin, weights.c:300-312). Synchronous. NULL on failure. */
+P2hWeight *p2h_fv_weight_upload(const unsigned char *signs, const unsigned char *flags, const float *lo,
+                                const float *hi, int K, int N);
+/* Wrap planes already in device memory (not copied; they must outlive the handle). Synchronous. */
+P2hWeight *p2h_fv_weight_wrap(const void *d_signs, const void *d_flags, const float *d_lo, const float *d_hi,
+                              int K, int N);
+void   p2h_weight_free(P2hWeight *w);
+int    p2h_weight_shape(const P2hWeight *w, int *K, int *N);
+size_t p2h_weight_device_bytes(const P2hWeight *w);   /* bytes this handle allocated */
+
+/* The int8w codes in the reference's kernel layout [N/16][K/4][16][4] (p2_fv_pack_codes, blas.c:1372-1400) into
+ * d_codes (K·N bytes). K % 4 == 0. */
+int p2h_fv_pack_codes(const P2hWeight *w, signed char *d_codes, void *stream);
+
+/* ── activations ─────────────────────────────────────────────────────────────────────────────────────────────── */
+
+/* Per-row int8 quantisation (blas.c:1114-1145): scale = amax/127 (1 for a zero row), q = round-half-even(x/scale
+ * as x·(1/scale)) saturated, the K % 16 tail as lrintf(x/scale) clamped to ±127. Q is [M][ldq] int8 with
+ * ldq % 16 == 0 and ldq >= roundup(K, P2H_Q_KALIGN); columns K..roundup(K, P2H_Q_KALIGN)-1 are written as 0.
+ * K % 4 == 0. */
+int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int ldq, float *dScales, void *stream);
+int p2h_q_ld(int K);   /* the smallest valid ldq for K */
+
+/* ── the five-value GEMM ─────────────────────────────────────────────────────────────────────────────────────── */
+
+/* C = alpha · A · W + beta · C on quantised A (p2_sgemm_fvb_q8a, blas.c:1430-1437, and sgemm_i8_run,
+ * blas.c:1296-1370): mode P2H_INT8W or P2H_INT8; beta 0 stores, 1 accumulates, any other value pre-scales C.
+ * The int32 sums run over K blocks of 1024 rows and each block is folded into C in fp32 as the reference does. */
+int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                     const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *stream);
+
+/* C = alpha · A · W + beta · C on fp32 A (p2_sgemm_fvb, blas.c:1481-1499): the int8 modes quantise A into the
+ * workspace and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output
+ * fmaf chain over k = 0..K-1 is the reference's exact kernel (blas.c:155-186, 929-987). */
+int    p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
+                    float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream);
+size_t p2h_fvb_workspace_bytes(int mode, int M, int K);
+
+/* The raw int32 accumulators sum_k q[m][k]·B[k][n] over all K of the int8 kernel (blas.c:1256-1282): for
+ * P2H_INT8W B is the codes plane into dAcc; for P2H_INT8 the S plane into dAcc and the T plane into dAcc2. */
+int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ldq, const P2hWeight *w,
+                    int32_t *dAcc, int32_t *dAcc2, int ldacc, void *stream);
+
+/* C = beta · C (scale_c, blas.c:60-70), the alpha == 0 case. */
+int p2h_scale_c(int M, int N, float beta, float *dC, int ldc, void *stream);
+
+/* ── int8-table weights (p2_sgemm_q8b / p2_sgemm_q8b_q8a, blas.c:1439-1479) ────────────────────────────────────
+ *  B int8 [K][ldb] in device memory with one fp32 scale per column. N % 16 == 0. */
+int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, int ldq, const float *dScales,
+                     const signed char *dB, int ldb, const float *dBscales, float beta, float *dC, int ldc,
+                     void *stream);
+int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const signed char *dB,
+                 int ldb, const float *dBscales, float beta, float *dC, int ldc, void *workspace,
+                 size_t workspace_bytes, void *stream);
+
+/* ── fp32 GEMM (p2_sgemm, blas.h:25-29): C = alpha · op(A) · op(B) + beta · C, row-major, trans 0/1 ──────── */
+int p2h_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
+              const float *dB, int ldb, float beta, float *dC, int ldc, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* P2HIP_H */

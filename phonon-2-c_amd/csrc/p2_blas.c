@@ -1,0 +1,477 @@
+/*  p2_blas.c – the reference's GEMM API (csrc/blas.h) over the MI355X kernels (include/p2_blas.h).
+ *
+ *  Host code in C: operand staging, the device weight cache, the mode latch and the reference's argument
+ *  conventions. Every product is computed by libp2hip.so on the GPU; this file does no arithmetic on operands.
+ */
+#include "p2_blas.h"
+#include "p2hip.h"
+
+#include <pthread.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ── failure ───────────────────────────────────────────────────────────────────────────────────────────────── */
+
+static void die(const char *who, const char *what)
+{
+    fprintf(stderr, "%s: %s\n", who, what);
+    abort();
+}
+
+static void check(int rc, const char *who)
+{
+    if (rc != 0) die(who, p2h_last_error());
+}
+
+/* blas.c:989-995 */
+static void require_panel_aligned(int N, const char *who)
+{
+    if (N % 16 != 0) {
+        fprintf(stderr, "%s: N = %d is not a multiple of %d\n", who, N, 16);
+        abort();
+    }
+}
+
+/* ── the mode latch (blas.c:1027-1066) ─────────────────────────────────────────────────────────────────────── */
+
+static int gemm_mode = -1;
+static pthread_once_t gemm_mode_once = PTHREAD_ONCE_INIT;
+
+/* P2_GEMM = int8 | int8w | exact, P2_EXACT non-"0" forces exact. The GPU always has int8 dot products, so the
+ * reference's "no dot-product extension → exact" clause (blas.c:1043-1045) never applies. */
+static void gemm_mode_init(void)
+{
+    const char *e = getenv("P2_EXACT");
+    const char *g = getenv("P2_GEMM");
+    int mode = P2H_INT8W;
+    if (g && strcmp(g, "exact") == 0) mode = P2H_EXACT;
+    else if (g && strcmp(g, "int8") == 0) mode = P2H_INT8;
+    else if (g && strcmp(g, "int8w") == 0) mode = P2H_INT8W;
+    if (e && e[0] && e[0] != '0') mode = P2H_EXACT;
+    gemm_mode = mode;
+}
+
+static int current_mode(void)
+{
+    pthread_once(&gemm_mode_once, gemm_mode_init);
+    return gemm_mode;
+}
+
+int p2_gemm_exact(void) { return current_mode() == P2H_EXACT; }
+
+const char *p2_gemm_mode(void)
+{
+    switch (current_mode()) {
+    case P2H_INT8:  return "int8 dot products, exact weights";
+    case P2H_INT8W: return "int8 dot products, int8 weights";
+    default:        return "fp32 expansion (exact)";
+    }
+}
+
+/* ── device start-up ───────────────────────────────────────────────────────────────────────────────────────── */
+
+static pthread_once_t dev_once = PTHREAD_ONCE_INIT;
+
+static void dev_init(void) { check(p2h_init(), "phonon2 GPU GEMM"); }
+
+/* ── per-thread staging ────────────────────────────────────────────────────────────────────────────────────── */
+
+typedef struct {
+    void *stream;
+    void *dA;  size_t capA;     /* activations (fp32) */
+    void *dB;  size_t capB;     /* fp32 B of p2_sgemm */
+    void *dC;  size_t capC;     /* output */
+    void *dW;  size_t capW;     /* quantisation workspace */
+    float *hq; size_t capq;     /* pinned host rows of the QuantA handed out by p2_quant_prepare */
+    float *hs; size_t caps;     /* its scales array (never read: the GPU quantises) */
+} Ctx;
+
+static pthread_key_t ctx_key;
+static pthread_once_t ctx_once = PTHREAD_ONCE_INIT;
+
+static void ctx_free(void *p)
+{
+    Ctx *c = (Ctx *)p;
+    if (!c) return;
+    p2h_free(c->dA); p2h_free(c->dB); p2h_free(c->dC); p2h_free(c->dW);
+    p2h_host_free(c->hq);
+    free(c->hs);
+    p2h_stream_destroy(c->stream);
+    free(c);
+}
+
+static void ctx_key_init(void) { pthread_key_create(&ctx_key, ctx_free); }
+
+static Ctx *ctx(void)
+{
+    pthread_once(&dev_once, dev_init);
+    pthread_once(&ctx_once, ctx_key_init);
+    Ctx *c = (Ctx *)pthread_getspecific(ctx_key);
+    if (!c) {
+        c = (Ctx *)calloc(1, sizeof *c);
+        if (!c) die("phonon2 GPU GEMM", "out of memory");
+        c->stream = p2h_stream_create();
+        if (!c->stream) die("phonon2 GPU GEMM", p2h_last_error());
+        pthread_setspecific(ctx_key, c);
+    }
+    return c;
+}
+
+static void *dgrow(void **p, size_t *cap, size_t need, const char *who)
+{
+    if (need > *cap || !*p) {
+        p2h_free(*p);
+        size_t n = need < 4096 ? 4096 : need + need / 4;
+        *p = p2h_malloc(n);
+        if (!*p) die(who, p2h_last_error());
+        *cap = n;
+    }
+    return *p;
+}
+
+/* ── the device weight cache ───────────────────────────────────────────────────────────────────────────────── */
+
+typedef struct Entry {
+    const void *a, *b, *c, *d;   /* signs, flags, lo, hi  /  q8, scales */
+    int K, N, ld, kind;
+    uint64_t fp;
+    P2hWeight *w;                /* five-value */
+    void *dq8; float *dsc;       /* int8 table: [K][N] int8, [N] scales */
+    struct Entry *next;
+} Entry;
+
+#define CACHE_BUCKETS 1024
+static Entry *cache[CACHE_BUCKETS];
+static pthread_mutex_t cache_mu = PTHREAD_MUTEX_INITIALIZER;
+
+static uint64_t fnv(uint64_t h, const void *p, size_t n)
+{
+    const unsigned char *s = (const unsigned char *)p;
+    for (size_t i = 0; i < n; i++) { h ^= s[i]; h *= 0x100000001B3ull; }
+    return h;
+}
+
+/* lo/hi (or scales) in full, and the first and last 64 bytes of each plane */
+static uint64_t fingerprint(const void *p1, size_t n1, const void *p2, size_t n2, const void *v1, const void *v2,
+                            size_t nv)
+{
+    uint64_t h = 0xCBF29CE484222325ull;
+    size_t e1 = n1 < 64 ? n1 : 64, e2 = n2 < 64 ? n2 : 64;
+    h = fnv(h, p1, e1); h = fnv(h, (const char *)p1 + n1 - e1, e1);
+    if (p2) { h = fnv(h, p2, e2); h = fnv(h, (const char *)p2 + n2 - e2, e2); }
+    h = fnv(h, v1, nv);
+    if (v2) h = fnv(h, v2, nv);
+    return h;
+}
+
+static size_t bucket(const void *a, int K, int N)
+{
+    uint64_t x = (uint64_t)(uintptr_t)a ^ ((uint64_t)K << 32) ^ (uint64_t)N;
+    x ^= x >> 29; x *= 0xBF58476D1CE4E5B9ull; x ^= x >> 32;
+    return (size_t)(x % CACHE_BUCKETS);
+}
+
+static void entry_release(Entry *e)
+{
+    p2h_weight_free(e->w);
+    p2h_free(e->dq8);
+    p2h_free(e->dsc);
+    free(e);
+}
+
+static const P2hWeight *fv_weight(const FiveValueB *B, int K, int N)
+{
+    size_t kn = (size_t)K * N;
+    uint64_t fp = fingerprint(B->signs, kn / 4 ? kn / 4 : 1, B->flags, kn / 8 ? kn / 8 : 1, B->lo, B->hi,
+                              (size_t)N * sizeof(float));
+    size_t h = bucket(B->signs, K, N);
+    pthread_mutex_lock(&cache_mu);
+    Entry **pe = &cache[h];
+    for (; *pe; pe = &(*pe)->next) {
+        Entry *e = *pe;
+        if (e->kind == 0 && e->a == B->signs && e->b == B->flags && e->c == B->lo && e->d == B->hi && e->K == K &&
+            e->N == N) {
+            if (e->fp == fp) {
+                pthread_mutex_unlock(&cache_mu);
+                return e->w;
+            }
+            *pe = e->next;   /* same addresses, new contents: drop the stale copy */
+            entry_release(e);
+            break;
+        }
+    }
+    Entry *e = (Entry *)calloc(1, sizeof *e);
+    if (!e) die("p2_sgemm_fvb", "out of memory");
+    e->w = p2h_fv_weight_upload(B->signs, B->flags, B->lo, B->hi, K, N);
+    if (!e->w) die("p2_sgemm_fvb: weight upload", p2h_last_error());
+    e->a = B->signs; e->b = B->flags; e->c = B->lo; e->d = B->hi;
+    e->K = K; e->N = N; e->kind = 0; e->fp = fp;
+    e->next = cache[h];
+    cache[h] = e;
+    pthread_mutex_unlock(&cache_mu);
+    return e->w;
+}
+
+static const Entry *q8_weight(const signed char *B, const float *scales, int ldb, int K, int N, void *stream)
+{
+    size_t rows_bytes = K > 0 ? (size_t)(K - 1) * ldb + N : 1;
+    uint64_t fp = fingerprint(B, rows_bytes, NULL, 0, scales, NULL, (size_t)N * sizeof(float));
+    size_t h = bucket(B, K, N);
+    pthread_mutex_lock(&cache_mu);
+    Entry **pe = &cache[h];
+    for (; *pe; pe = &(*pe)->next) {
+        Entry *e = *pe;
+        if (e->kind == 1 && e->a == B && e->c == scales && e->K == K && e->N == N && e->ld == ldb) {
+            if (e->fp == fp) {
+                pthread_mutex_unlock(&cache_mu);
+                return e;
+            }
+            *pe = e->next;
+            entry_release(e);
+            break;
+        }
+    }
+    Entry *e = (Entry *)calloc(1, sizeof *e);
+    if (!e) die("p2_sgemm_q8b", "out of memory");
+    e->dq8 = p2h_malloc((size_t)K * N + 16);
+    e->dsc = (float *)p2h_malloc((size_t)N * sizeof(float));
+    if (!e->dq8 || !e->dsc) die("p2_sgemm_q8b: weight upload", p2h_last_error());
+    check(p2h_memcpy2d_h2d(e->dq8, (size_t)N, B, (size_t)ldb, (size_t)N, (size_t)K, stream), "p2_sgemm_q8b");
+    check(p2h_memcpy_h2d(e->dsc, scales, (size_t)N * sizeof(float), stream), "p2_sgemm_q8b");
+    check(p2h_stream_sync(stream), "p2_sgemm_q8b");
+    e->a = B; e->c = scales; e->K = K; e->N = N; e->ld = ldb; e->kind = 1; e->fp = fp;
+    e->next = cache[h];
+    cache[h] = e;
+    pthread_mutex_unlock(&cache_mu);
+    return e;
+}
+
+void p2_gpu_weight_cache_clear(void)
+{
+    pthread_mutex_lock(&cache_mu);
+    for (int i = 0; i < CACHE_BUCKETS; i++) {
+        Entry *e = cache[i];
+        while (e) {
+            Entry *n = e->next;
+            entry_release(e);
+            e = n;
+        }
+        cache[i] = NULL;
+    }
+    pthread_mutex_unlock(&cache_mu);
+}
+
+/* ── operand staging ───────────────────────────────────────────────────────────────────────────────────────── */
+
+/* rows × cols fp32 from host (pitch ld) into the thread's buffer *slot, packed (pitch cols). */
+static float *upload_f32(Ctx *c, void **slot, size_t *cap, const float *h, int rows, int cols, int ld,
+                         const char *who)
+{
+    size_t bytes = (size_t)rows * cols * sizeof(float);
+    float *d = (float *)dgrow(slot, cap, bytes ? bytes : 4, who);
+    if (bytes)
+        check(p2h_memcpy2d_h2d(d, (size_t)cols * 4, h, (size_t)ld * 4, (size_t)cols * 4, (size_t)rows, c->stream),
+              who);
+    return d;
+}
+
+static float *stage_c(Ctx *c, const float *C, int M, int N, int ldc, int need_old, const char *who)
+{
+    float *d = (float *)dgrow(&c->dC, &c->capC, (size_t)M * N * sizeof(float) + 16, who);
+    if (need_old)
+        check(p2h_memcpy2d_h2d(d, (size_t)N * 4, C, (size_t)ldc * 4, (size_t)N * 4, (size_t)M, c->stream), who);
+    return d;
+}
+
+static void finish_c(Ctx *c, float *C, const float *dC, int M, int N, int ldc, const char *who)
+{
+    check(p2h_memcpy2d_d2h(C, (size_t)ldc * 4, dC, (size_t)N * 4, (size_t)N * 4, (size_t)M, c->stream), who);
+    check(p2h_stream_sync(c->stream), who);
+}
+
+static void *workspace(Ctx *c, int M, int K, size_t *bytes, const char *who)
+{
+    size_t need = p2h_fvb_workspace_bytes(P2H_INT8W, M, K);
+    *bytes = need;
+    if (need == 0) return NULL;
+    size_t cap0 = c->capW;
+    void *w = dgrow(&c->dW, &c->capW, need, who);
+    (void)cap0;
+    *bytes = c->capW;
+    return w;
+}
+
+/* C = beta · C for alpha == 0 (blas.c:1434-1435, 1488 and 748-749). */
+static void scale_only(Ctx *c, float *C, int M, int N, int ldc, float beta, const char *who)
+{
+    if (beta == 1.0f || M <= 0 || N <= 0) return;
+    float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
+    check(p2h_scale_c(M, N, beta, dC, N, c->stream), who);
+    finish_c(c, C, dC, M, N, ldc, who);
+}
+
+/* ── the five-value GEMMs ──────────────────────────────────────────────────────────────────────────────────── */
+
+void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, const FiveValueB *B, float beta,
+                  float *C, int ldc)
+{
+    static const char who[] = "p2_sgemm_fvb";
+    require_panel_aligned(N, who);
+    Ctx *c = ctx();
+    if (M <= 0 || N <= 0) return;
+    if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
+    const P2hWeight *w = fv_weight(B, K, N);
+    int mode = current_mode();
+    float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
+    float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
+    size_t wsb = 0;
+    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, M, K, &wsb, who) : NULL;
+    check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, w, beta, dC, N, ws, wsb, c->stream), who);
+    finish_c(c, C, dC, M, N, ldc, who);
+}
+
+int p2_quant_prepare(QuantA *qa, int M, int K)
+{
+    if (current_mode() == P2H_EXACT || K % 4 != 0 || M < 0) return -1;   /* blas.c:1175 */
+    Ctx *c = ctx();
+    size_t need = (size_t)(M > 0 ? M : 1) * (K > 0 ? K : 1) * sizeof(float);
+    if (need > c->capq || !c->hq) {
+        p2h_host_free(c->hq);
+        c->hq = (float *)p2h_host_malloc(need);
+        if (!c->hq) { c->capq = 0; return -1; }
+        c->capq = need;
+    }
+    size_t sneed = (size_t)(M > 0 ? M : 1) * sizeof(float);
+    if (sneed > c->caps || !c->hs) {
+        free(c->hs);
+        c->hs = (float *)calloc(1, sneed);
+        if (!c->hs) { c->caps = 0; return -1; }
+        c->caps = sneed;
+    }
+    qa->q = (signed char *)c->hq;
+    qa->scales = c->hs;
+    qa->M = M;
+    qa->K = K;
+    return 0;
+}
+
+void p2_quant_row(const QuantA *qa, int m, const float *row)
+{
+    memcpy((float *)(void *)qa->q + (size_t)m * qa->K, row, (size_t)qa->K * sizeof(float));
+}
+
+void p2_sgemm_fvb_q8a(int M, int N, int K, float alpha, const QuantA *A, const FiveValueB *B, float beta, float *C,
+                      int ldc)
+{
+    static const char who[] = "p2_sgemm_fvb_q8a";
+    require_panel_aligned(N, who);
+    Ctx *c = ctx();
+    if (M <= 0 || N <= 0) return;
+    if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
+    if (K % 4 != 0) die(who, "K is not a multiple of 4 (p2_quant_prepare refuses such K)");
+    /* the reference reads the codes plane in int8w mode and the two planes otherwise (blas.c:1408) */
+    int mode = current_mode() == P2H_INT8W ? P2H_INT8W : P2H_INT8;
+    const P2hWeight *w = fv_weight(B, K, N);
+    float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
+    float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
+    size_t wsb = 0;
+    void *ws = workspace(c, M, K, &wsb, who);
+    check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, w, beta, dC, N, ws, wsb, c->stream), who);
+    finish_c(c, C, dC, M, N, ldc, who);
+}
+
+signed char *p2_fv_pack_codes(const FiveValueB *b, int K, int N)
+{
+    if (K % 4 != 0 || N % 16 != 0 || K <= 0 || N <= 0) return NULL;   /* blas.c:1393 */
+    Ctx *c = ctx();
+    const P2hWeight *w = fv_weight(b, K, N);
+    size_t bytes = (size_t)K * N;
+    signed char *host = (signed char *)malloc(bytes);
+    void *d = p2h_malloc(bytes);
+    if (!host || !d) {
+        free(host);
+        p2h_free(d);
+        return NULL;
+    }
+    int rc = p2h_fv_pack_codes(w, (signed char *)d, c->stream);
+    if (rc == 0) rc = p2h_memcpy_d2h(host, d, bytes, c->stream);
+    if (rc == 0) rc = p2h_stream_sync(c->stream);
+    p2h_free(d);
+    if (rc != 0) {
+        free(host);
+        return NULL;
+    }
+    return host;
+}
+
+/* ── int8-table GEMMs ──────────────────────────────────────────────────────────────────────────────────────── */
+
+void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, const signed char *B,
+                  const float *scales, int ldb, float beta, float *C, int ldc)
+{
+    static const char who[] = "p2_sgemm_q8b";
+    require_panel_aligned(N, who);
+    Ctx *c = ctx();
+    if (M <= 0 || N <= 0) return;
+    if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
+    const Entry *e = q8_weight(B, scales, ldb, K, N, c->stream);
+    int mode = current_mode();
+    float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
+    float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
+    size_t wsb = 0;
+    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, M, K, &wsb, who) : NULL;
+    check(p2h_q8b_gemm(mode, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws, wsb,
+                       c->stream), who);
+    finish_c(c, C, dC, M, N, ldc, who);
+}
+
+void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const signed char *B, const float *scales,
+                      int ldb, float beta, float *C, int ldc)
+{
+    static const char who[] = "p2_sgemm_q8b_q8a";
+    require_panel_aligned(N, who);
+    Ctx *c = ctx();
+    if (M <= 0 || N <= 0) return;
+    if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
+    if (K % 4 != 0) die(who, "K is not a multiple of 4 (p2_quant_prepare refuses such K)");
+    const Entry *e = q8_weight(B, scales, ldb, K, N, c->stream);
+    float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
+    float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
+    size_t wsb = 0;
+    void *ws = workspace(c, M, K, &wsb, who);
+    check(p2h_q8b_gemm(P2H_INT8W, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws,
+                       wsb, c->stream), who);
+    finish_c(c, C, dC, M, N, ldc, who);
+}
+
+/* ── fp32 GEMM ─────────────────────────────────────────────────────────────────────────────────────────────── */
+
+static void sgemm_any(const char *who, P2Trans transA, P2Trans transB, int M, int N, int K, float alpha,
+                      const float *A, int lda, const float *B, int ldb, float beta, float *C, int ldc)
+{
+    Ctx *c = ctx();
+    if (M <= 0 || N <= 0) return;
+    if (alpha == 0.0f || K <= 0) { scale_only(c, C, M, N, ldc, beta, who); return; }   /* blas.c:748-749 */
+    int tA = transA == P2_TRANS, tB = transB == P2_TRANS;
+    float *dA = tA ? upload_f32(c, &c->dA, &c->capA, A, K, M, lda, who)
+                   : upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
+    float *dB = tB ? upload_f32(c, &c->dB, &c->capB, B, N, K, ldb, who)
+                   : upload_f32(c, &c->dB, &c->capB, B, K, N, ldb, who);
+    float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
+    check(p2h_sgemm(tA, tB, M, N, K, alpha, dA, tA ? M : K, dB, tB ? K : N, beta, dC, N, c->stream), who);
+    finish_c(c, C, dC, M, N, ldc, who);
+}
+
+void p2_sgemm(P2Trans transA, P2Trans transB, int M, int N, int K, float alpha, const float *A, int lda,
+              const float *B, int ldb, float beta, float *C, int ldc)
+{
+    sgemm_any("p2_sgemm", transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+}
+
+void p2_sgemm_st(P2Trans transA, P2Trans transB, int M, int N, int K, float alpha, const float *A, int lda,
+                 const float *B, int ldb, float beta, float *C, int ldc)
+{
+    sgemm_any("p2_sgemm_st", transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+}

@@ -1,0 +1,677 @@
+/*  p2hip.hip – the device-pointer C ABI (include/p2hip.h) over the gfx950 kernels in p2hip_kernels.h.
+ *
+ *  Checks every shape, stride and alignment the kernels assume before launching, so a kernel never sees an operand
+ *  it would index out of bounds.
+ */
+#include "p2hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "p2hip_kernels.h"
+
+namespace {
+
+thread_local char t_err[512];
+thread_local hipStream_t t_stream = nullptr;
+
+std::once_flag g_init_once;
+int g_init_rc = P2H_E_DEVICE;
+char g_init_err[512];
+char g_arch[64];
+int g_cus = 0;
+
+int fail(int rc, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof t_err, fmt, ap);
+    va_end(ap);
+    return rc;
+}
+
+#define HIPCHK(call)                                                                                            \
+    do {                                                                                                        \
+        hipError_t e_ = (call);                                                                                 \
+        if (e_ != hipSuccess) return fail(P2H_E_DEVICE, "%s: %s", #call, hipGetErrorString(e_));              \
+    } while (0)
+
+void do_init()
+{
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n < 1) {
+        snprintf(g_init_err, sizeof g_init_err, "p2h_init: no HIP device (%s)", hipGetErrorString(e));
+        return;
+    }
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, 0);
+    if (e != hipSuccess) {
+        snprintf(g_init_err, sizeof g_init_err, "p2h_init: hipGetDeviceProperties: %s", hipGetErrorString(e));
+        return;
+    }
+    snprintf(g_arch, sizeof g_arch, "%s", prop.gcnArchName);
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        snprintf(g_init_err, sizeof g_init_err, "p2h_init: device 0 is %s, this library is built for gfx950 only",
+                 prop.gcnArchName);
+        return;
+    }
+    g_cus = prop.multiProcessorCount;
+    e = hipSetDevice(0);
+    if (e != hipSuccess) {
+        snprintf(g_init_err, sizeof g_init_err, "p2h_init: hipSetDevice: %s", hipGetErrorString(e));
+        return;
+    }
+    g_init_rc = P2H_OK;
+}
+
+int ensure_init()
+{
+    std::call_once(g_init_once, do_init);
+    if (g_init_rc != P2H_OK) return fail(g_init_rc, "%s", g_init_err);
+    return P2H_OK;
+}
+
+hipStream_t stream_of(void *s)
+{
+    if (s) return (hipStream_t)s;
+    return (hipStream_t)p2h_thread_stream();
+}
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+struct P2hWeight {
+    int K, N;
+    const uint8_t *signs, *flags;
+    const float *lo, *hi;
+    uint8_t *clo;
+    float *c1w, *c2;
+    void *own;        /* the one device allocation this handle made */
+    size_t own_bytes;
+};
+
+extern "C" {
+
+/* ── runtime ────────────────────────────────────────────────────────────────────────────────────────────────── */
+
+int p2h_init(void) { return ensure_init(); }
+
+const char *p2h_last_error(void) { return t_err; }
+
+const char *p2h_device_name(void)
+{
+    ensure_init();
+    return g_arch;
+}
+
+int p2h_device_cu_count(void)
+{
+    ensure_init();
+    return g_cus;
+}
+
+void *p2h_stream_create(void)
+{
+    if (ensure_init()) return nullptr;
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+        fail(P2H_E_DEVICE, "hipStreamCreate failed");
+        return nullptr;
+    }
+    return s;
+}
+
+int p2h_stream_destroy(void *stream)
+{
+    if (!stream) return P2H_OK;
+    HIPCHK(hipStreamDestroy((hipStream_t)stream));
+    return P2H_OK;
+}
+
+int p2h_stream_sync(void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    HIPCHK(hipStreamSynchronize(stream_of(stream)));
+    return P2H_OK;
+}
+
+void *p2h_thread_stream(void)
+{
+    if (!t_stream) {
+        if (ensure_init()) return nullptr;
+        if (hipStreamCreateWithFlags(&t_stream, hipStreamNonBlocking) != hipSuccess) {
+            t_stream = nullptr;
+            fail(P2H_E_DEVICE, "hipStreamCreate failed");
+        }
+    }
+    return t_stream;
+}
+
+void *p2h_malloc(size_t bytes)
+{
+    if (ensure_init()) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+        fail(P2H_E_NOMEM, "hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int p2h_free(void *dptr)
+{
+    if (!dptr) return P2H_OK;
+    HIPCHK(hipFree(dptr));
+    return P2H_OK;
+}
+
+void *p2h_host_malloc(size_t bytes)
+{
+    if (ensure_init()) return nullptr;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault) != hipSuccess) {
+        fail(P2H_E_NOMEM, "hipHostMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+int p2h_host_free(void *hptr)
+{
+    if (!hptr) return P2H_OK;
+    HIPCHK(hipHostFree(hptr));
+    return P2H_OK;
+}
+
+int p2h_memset(void *dptr, int value, size_t bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    HIPCHK(hipMemsetAsync(dptr, value, bytes, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_memcpy2d_h2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t row_bytes, size_t rows,
+                     void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (rows == 0 || row_bytes == 0) return P2H_OK;
+    HIPCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, row_bytes, rows, hipMemcpyHostToDevice, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_memcpy2d_d2h(void *dst, size_t dpitch, const void *src, size_t spitch, size_t row_bytes, size_t rows,
+                     void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (rows == 0 || row_bytes == 0) return P2H_OK;
+    HIPCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, row_bytes, rows, hipMemcpyDeviceToHost, stream_of(stream)));
+    return P2H_OK;
+}
+
+void *p2h_event_create(void)
+{
+    if (ensure_init()) return nullptr;
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        fail(P2H_E_DEVICE, "hipEventCreate failed");
+        return nullptr;
+    }
+    return e;
+}
+
+int p2h_event_destroy(void *event)
+{
+    if (!event) return P2H_OK;
+    HIPCHK(hipEventDestroy((hipEvent_t)event));
+    return P2H_OK;
+}
+
+int p2h_event_record(void *event, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    HIPCHK(hipEventRecord((hipEvent_t)event, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_event_sync(void *event)
+{
+    HIPCHK(hipEventSynchronize((hipEvent_t)event));
+    return P2H_OK;
+}
+
+float p2h_event_elapsed_ms(void *start, void *stop)
+{
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop) != hipSuccess) return -1.0f;
+    return ms;
+}
+
+/* ── weights ────────────────────────────────────────────────────────────────────────────────────────────────── */
+
+static P2hWeight *weight_new(int K, int N, bool copy_planes)
+{
+    if (K < 0 || N <= 0 || N % 16 != 0) {
+        fail(P2H_E_ARG, "five-value weight: N = %d must be a positive multiple of 16 (K = %d)", N, K);
+        return nullptr;
+    }
+    size_t kn = (size_t)K * N;
+    size_t off_signs = 0, off_flags = 0, off_lo = 0, off_hi = 0, off = 0;
+    if (copy_planes) {
+        off_signs = off; off += align_up(kn / 4 ? kn / 4 : 1, 256);
+        off_flags = off; off += align_up(kn / 8 ? kn / 8 : 1, 256);
+        off_lo = off; off += align_up((size_t)N * 4, 256);
+        off_hi = off; off += align_up((size_t)N * 4, 256);
+    }
+    size_t off_clo = off; off += align_up((size_t)N, 256);
+    size_t off_c1 = off; off += align_up((size_t)N * 4, 256);
+    size_t off_c2 = off; off += align_up((size_t)N * 4, 256);
+    void *base = nullptr;
+    if (hipMalloc(&base, off) != hipSuccess) {
+        fail(P2H_E_NOMEM, "five-value weight: hipMalloc(%zu) failed", off);
+        return nullptr;
+    }
+    P2hWeight *w = new P2hWeight();
+    w->K = K; w->N = N;
+    uint8_t *b = (uint8_t *)base;
+    if (copy_planes) {
+        w->signs = b + off_signs;
+        w->flags = b + off_flags;
+        w->lo = (const float *)(b + off_lo);
+        w->hi = (const float *)(b + off_hi);
+    }
+    w->clo = b + off_clo;
+    w->c1w = (float *)(b + off_c1);
+    w->c2 = (float *)(b + off_c2);
+    w->own = base;
+    w->own_bytes = off;
+    return w;
+}
+
+static int weight_tables(P2hWeight *w)
+{
+    hipStream_t s = stream_of(nullptr);
+    hipLaunchKernelGGL(p2k::fv_tables, dim3((w->N + 255) / 256), dim3(256), 0, s, w->N, w->lo, w->hi, w->clo,
+                       w->c1w, w->c2);
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipStreamSynchronize(s));
+    return P2H_OK;
+}
+
+P2hWeight *p2h_fv_weight_upload(const unsigned char *signs, const unsigned char *flags, const float *lo,
+                                const float *hi, int K, int N)
+{
+    if (ensure_init()) return nullptr;
+    if (!signs || !flags || !lo || !hi) {
+        fail(P2H_E_ARG, "p2h_fv_weight_upload: NULL plane");
+        return nullptr;
+    }
+    P2hWeight *w = weight_new(K, N, true);
+    if (!w) return nullptr;
+    size_t kn = (size_t)K * N;
+    hipStream_t s = stream_of(nullptr);
+    bool ok = hipMemcpyAsync((void *)w->signs, signs, kn / 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+              hipMemcpyAsync((void *)w->flags, flags, kn / 8, hipMemcpyHostToDevice, s) == hipSuccess &&
+              hipMemcpyAsync((void *)w->lo, lo, (size_t)N * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
+              hipMemcpyAsync((void *)w->hi, hi, (size_t)N * 4, hipMemcpyHostToDevice, s) == hipSuccess;
+    if (!ok || weight_tables(w) != P2H_OK) {
+        if (!ok) fail(P2H_E_DEVICE, "p2h_fv_weight_upload: copy failed");
+        p2h_weight_free(w);
+        return nullptr;
+    }
+    return w;
+}
+
+P2hWeight *p2h_fv_weight_wrap(const void *d_signs, const void *d_flags, const float *d_lo, const float *d_hi,
+                              int K, int N)
+{
+    if (ensure_init()) return nullptr;
+    if (!d_signs || !d_flags || !d_lo || !d_hi || !aligned(d_signs, 4) || !aligned(d_flags, 2) ||
+        !aligned(d_lo, 4) || !aligned(d_hi, 4)) {
+        fail(P2H_E_ARG, "p2h_fv_weight_wrap: planes must be non-NULL, signs 4-byte and flags 2-byte aligned");
+        return nullptr;
+    }
+    P2hWeight *w = weight_new(K, N, false);
+    if (!w) return nullptr;
+    w->signs = (const uint8_t *)d_signs;
+    w->flags = (const uint8_t *)d_flags;
+    w->lo = d_lo;
+    w->hi = d_hi;
+    if (weight_tables(w) != P2H_OK) {
+        p2h_weight_free(w);
+        return nullptr;
+    }
+    return w;
+}
+
+void p2h_weight_free(P2hWeight *w)
+{
+    if (!w) return;
+    if (w->own) (void)hipFree(w->own);
+    delete w;
+}
+
+int p2h_weight_shape(const P2hWeight *w, int *K, int *N)
+{
+    if (!w) return fail(P2H_E_ARG, "NULL weight");
+    if (K) *K = w->K;
+    if (N) *N = w->N;
+    return P2H_OK;
+}
+
+size_t p2h_weight_device_bytes(const P2hWeight *w) { return w ? w->own_bytes : 0; }
+
+int p2h_fv_pack_codes(const P2hWeight *w, signed char *d_codes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (!w || !d_codes) return fail(P2H_E_ARG, "p2h_fv_pack_codes: NULL argument");
+    if (w->K % 4 != 0) return fail(P2H_E_ARG, "p2h_fv_pack_codes: K = %d is not a multiple of 4", w->K);
+    if (!aligned(d_codes, 4)) return fail(P2H_E_ARG, "p2h_fv_pack_codes: output must be 4-byte aligned");
+    size_t total = (size_t)(w->N / 16) * (w->K / 4) * 16;
+    if (total == 0) return P2H_OK;
+    hipLaunchKernelGGL(p2k::fv_pack_codes, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream_of(stream),
+                       w->K, w->N, w->signs, w->flags, w->clo, (uint32_t *)d_codes);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+/* ── activations ────────────────────────────────────────────────────────────────────────────────────────────── */
+
+int p2h_q_ld(int K) { return (int)align_up((size_t)(K > 0 ? K : 0), P2H_Q_KALIGN); }
+
+int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int ldq, float *dScales, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (M < 0 || K < 0 || K % 4 != 0) return fail(P2H_E_ARG, "p2h_quant_rows: K = %d must be a multiple of 4", K);
+    if (M == 0) return P2H_OK;
+    if (!dA || !dQ || !dScales || lda < K) return fail(P2H_E_ARG, "p2h_quant_rows: bad pointer or lda");
+    if (ldq < p2h_q_ld(K) || ldq % 16 != 0 || !aligned(dQ, 16))
+        return fail(P2H_E_ARG, "p2h_quant_rows: ldq = %d must be >= %d, a multiple of 16, Q 16-byte aligned", ldq,
+                    p2h_q_ld(K));
+    int vec_ok = (lda % 4 == 0) && aligned(dA, 16);
+    hipLaunchKernelGGL(p2k::quant_rows, dim3((M + 3) / 4), dim3(256), 0, stream_of(stream), M, K, p2h_q_ld(K), dA,
+                       lda, vec_ok, (int8_t *)dQ, ldq, dScales);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+/* ── GEMMs ──────────────────────────────────────────────────────────────────────────────────────────────────── */
+
+int p2h_scale_c(int M, int N, float beta, float *dC, int ldc, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (M < 0 || N < 0 || (M > 0 && N > 0 && (!dC || ldc < N))) return fail(P2H_E_ARG, "p2h_scale_c: bad shape");
+    if (beta == 1.0f || M == 0 || N == 0) return P2H_OK;
+    size_t total = (size_t)M * N;
+    hipLaunchKernelGGL(p2k::scale_c, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream_of(stream), M, N,
+                       beta, dC, ldc);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+static int check_q(const char *who, int M, int K, const signed char *dQ, int ldq, const float *dScales)
+{
+    if (M < 0 || K < 0 || K % 4 != 0) return fail(P2H_E_ARG, "%s: K = %d must be a multiple of 4", who, K);
+    if (M > 0 && (!dQ || !dScales)) return fail(P2H_E_ARG, "%s: NULL activations", who);
+    if (M > 0 && (ldq < p2h_q_ld(K) || ldq % 16 != 0 || !aligned(dQ, 16)))
+        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d and a multiple of 16, Q 16-byte aligned", who, ldq,
+                    p2h_q_ld(K));
+    return P2H_OK;
+}
+
+static p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const signed char *dQ, int ldq,
+                               const float *dScales, float *dC, int ldc)
+{
+    p2k::GemmArgs g;
+    memset(&g, 0, sizeof g);
+    g.M = M; g.N = N; g.K = K;
+    g.alpha = alpha; g.beta = beta;
+    g.Q = (const int8_t *)dQ; g.ldq = ldq; g.a_scales = dScales;
+    g.C = dC; g.ldc = ldc;
+    g.c_vec4 = dC && (ldc % 4 == 0) && aligned(dC, 16);
+    g.tiles_n = (N + p2k::BN - 1) / p2k::BN;
+    return g;
+}
+
+static dim3 gemm_grid(int M, int N)
+{
+    size_t tn = (N + p2k::BN - 1) / p2k::BN, tm = (M + p2k::BM - 1) / p2k::BM;
+    return dim3((unsigned)(tn * tm));
+}
+
+int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                     const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a: mode %d is not an int8 mode", mode);
+    if (!w || w->N != N || w->K != K)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a: weight is [%d, %d], call asks [%d, %d]", w ? w->K : -1,
+                    w ? w->N : -1, K, N);
+    if (int rc = check_q("p2h_fvb_gemm_q8a", M, K, dQ, ldq, dScales)) return rc;
+    if (M > 0 && (!dC || ldc < N)) return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a: C or ldc invalid");
+    hipStream_t s = stream_of(stream);
+    if (M == 0) return P2H_OK;
+    if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);            /* blas.c:1434 */
+    if (K == 0) return (beta != 0.0f) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;   /* no K block runs */
+    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc);
+    g.signs = w->signs; g.flags = w->flags; g.clo = w->clo;
+    const bool multi = K > p2k::kFoldRows;
+    if (mode == P2H_INT8W) {
+        g.c1 = w->c1w;
+        if (multi)
+            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8W, p2k::OUT_F32, true>), gemm_grid(M, N), dim3(256), 0, s, g);
+        else
+            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8W, p2k::OUT_F32, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+    } else {
+        g.c1 = w->lo; g.c2 = w->c2;
+        if (multi)
+            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8, p2k::OUT_F32, true>), gemm_grid(M, N), dim3(256), 0, s, g);
+        else
+            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8, p2k::OUT_F32, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+    }
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ldq, const P2hWeight *w,
+                    int32_t *dAcc, int32_t *dAcc2, int ldacc, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8) return fail(P2H_E_ARG, "p2h_fvb_acc_i32: mode %d", mode);
+    if (!w || w->N != N || w->K != K) return fail(P2H_E_ARG, "p2h_fvb_acc_i32: weight shape mismatch");
+    if (M > 0 && !dQ) return fail(P2H_E_ARG, "p2h_fvb_acc_i32: NULL activations");
+    if (int rc = check_q("p2h_fvb_acc_i32", M, K, dQ, ldq, (const float *)dAcc)) return rc;
+    if (M > 0 && (!dAcc || ldacc < N || ldacc % 4 != 0 || !aligned(dAcc, 16) ||
+                  (mode == P2H_INT8 && (!dAcc2 || !aligned(dAcc2, 16)))))
+        return fail(P2H_E_ARG, "p2h_fvb_acc_i32: accumulators must be 16-byte aligned with ldacc %% 4 == 0");
+    if (M == 0) return P2H_OK;
+    p2k::GemmArgs g = gemm_args(M, N, K, 1.0f, 0.0f, dQ, ldq, nullptr, nullptr, 0);
+    g.signs = w->signs; g.flags = w->flags; g.clo = w->clo;
+    g.acc1 = dAcc; g.acc2 = dAcc2; g.ldacc = ldacc;
+    hipStream_t s = stream_of(stream);
+    if (mode == P2H_INT8W)
+        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8W, p2k::OUT_ACC, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8, p2k::OUT_ACC, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
+{
+    p2k::ExactArgs g = g0;
+    g.tiles_n = (g.N + p2k::EBN - 1) / p2k::EBN;
+    size_t tiles = (size_t)g.tiles_n * ((g.M + p2k::EBM - 1) / p2k::EBM);
+    if (tiles == 0) return P2H_OK;
+    if (bkind == p2k::EXB_FV)
+        hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_FV>, dim3((unsigned)tiles), dim3(256), 0, s, g);
+    else if (bkind == p2k::EXB_Q8)
+        hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_Q8>, dim3((unsigned)tiles), dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_F32>, dim3((unsigned)tiles), dim3(256), 0, s, g);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+size_t p2h_fvb_workspace_bytes(int mode, int M, int K)
+{
+    if (mode == P2H_EXACT || M <= 0 || K <= 0 || K % 4 != 0) return 0;
+    return align_up((size_t)M * p2h_q_ld(K), 256) + align_up((size_t)M * 4, 256);
+}
+
+static int quant_into_workspace(const char *who, int M, int K, const float *dA, int lda, void *workspace,
+                                size_t workspace_bytes, signed char **dQ, float **dS, hipStream_t s)
+{
+    size_t need = p2h_fvb_workspace_bytes(P2H_INT8W, M, K);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
+        return fail(P2H_E_WORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", who, need,
+                    workspace_bytes);
+    *dQ = (signed char *)workspace;
+    *dS = (float *)((char *)workspace + align_up((size_t)M * p2h_q_ld(K), 256));
+    return p2h_quant_rows(M, K, dA, lda, *dQ, p2h_q_ld(K), *dS, s);
+}
+
+int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
+                 float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm: unknown mode %d", mode);
+    if (!w || w->N != N || w->K != K)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm: weight is [%d, %d], call asks [%d, %d]", w ? w->K : -1,
+                    w ? w->N : -1, K, N);
+    if (M < 0 || K < 0) return fail(P2H_E_ARG, "p2h_fvb_gemm: negative shape");
+    if (M > 0 && (!dC || ldc < N || (K > 0 && (!dA || lda < K)))) return fail(P2H_E_ARG, "p2h_fvb_gemm: bad A/C");
+    hipStream_t s = stream_of(stream);
+    if (M == 0) return P2H_OK;
+    if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);   /* blas.c:1488 */
+    if (mode != P2H_EXACT && K % 4 == 0) {                            /* blas.c:1490-1493 */
+        if (beta != 0.0f && beta != 1.0f) {
+            if (int rc = p2h_scale_c(M, N, beta, dC, ldc, s)) return rc;
+            beta = 1.0f;
+        }
+        if (K == 0) return P2H_OK;
+        signed char *dQ;
+        float *dS;
+        if (int rc = quant_into_workspace("p2h_fvb_gemm", M, K, dA, lda, workspace, workspace_bytes, &dQ, &dS, s))
+            return rc;
+        return p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, p2h_q_ld(K), dS, w, beta, dC, ldc, s);
+    }
+    p2k::ExactArgs g;
+    memset(&g, 0, sizeof g);
+    g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
+    g.A = dA; g.lda = lda;
+    g.signs = w->signs; g.flags = w->flags; g.lo = w->lo; g.hi = w->hi;
+    g.C = dC; g.ldc = ldc;
+    return launch_exact(p2k::EXB_FV, g, s);
+}
+
+int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, int ldq, const float *dScales,
+                     const signed char *dB, int ldb, const float *dBscales, float beta, float *dC, int ldc,
+                     void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (N < 0 || N % 16 != 0) return fail(P2H_E_ARG, "p2h_q8b_gemm_q8a: N = %d is not a multiple of 16", N);
+    if (int rc = check_q("p2h_q8b_gemm_q8a", M, K, dQ, ldq, dScales)) return rc;
+    if (M > 0 && K > 0 && (!dB || !dBscales || ldb < N || ldb % 16 != 0 || !aligned(dB, 16)))
+        return fail(P2H_E_ARG, "p2h_q8b_gemm_q8a: B must be 16-byte aligned with ldb %% 16 == 0 and ldb >= N");
+    if (M > 0 && (!dC || ldc < N)) return fail(P2H_E_ARG, "p2h_q8b_gemm_q8a: C or ldc invalid");
+    hipStream_t s = stream_of(stream);
+    if (M == 0 || N == 0) return P2H_OK;
+    if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);
+    if (K == 0) return (beta != 0.0f) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;
+    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc);
+    g.B8 = (const int8_t *)dB; g.ldb = ldb; g.c1 = dBscales;
+    if (K > p2k::kFoldRows)
+        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_Q8B, p2k::OUT_F32, true>), gemm_grid(M, N), dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_Q8B, p2k::OUT_F32, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const signed char *dB,
+                 int ldb, const float *dBscales, float beta, float *dC, int ldc, void *workspace,
+                 size_t workspace_bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
+        return fail(P2H_E_ARG, "p2h_q8b_gemm: unknown mode %d", mode);
+    if (N < 0 || N % 16 != 0) return fail(P2H_E_ARG, "p2h_q8b_gemm: N = %d is not a multiple of 16", N);
+    if (M < 0 || K < 0) return fail(P2H_E_ARG, "p2h_q8b_gemm: negative shape");
+    if (M > 0 && (!dC || ldc < N || (K > 0 && (!dA || lda < K || !dB || !dBscales || ldb < N))))
+        return fail(P2H_E_ARG, "p2h_q8b_gemm: bad A/B/C");
+    hipStream_t s = stream_of(stream);
+    if (M == 0 || N == 0) return P2H_OK;
+    if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);
+    if (mode != P2H_EXACT && K % 4 == 0) {   /* blas.c:1453-1457 */
+        if (beta != 0.0f && beta != 1.0f) {
+            if (int rc = p2h_scale_c(M, N, beta, dC, ldc, s)) return rc;
+            beta = 1.0f;
+        }
+        if (K == 0) return P2H_OK;
+        signed char *dQ;
+        float *dS;
+        if (int rc = quant_into_workspace("p2h_q8b_gemm", M, K, dA, lda, workspace, workspace_bytes, &dQ, &dS, s))
+            return rc;
+        return p2h_q8b_gemm_q8a(M, N, K, alpha, dQ, p2h_q_ld(K), dS, dB, ldb, dBscales, beta, dC, ldc, s);
+    }
+    p2k::ExactArgs g;
+    memset(&g, 0, sizeof g);
+    g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
+    g.A = dA; g.lda = lda;
+    g.B8 = (const int8_t *)dB; g.ldb = ldb; g.bscales = dBscales;
+    g.C = dC; g.ldc = ldc;
+    return launch_exact(p2k::EXB_Q8, g, s);
+}
+
+int p2h_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
+              const float *dB, int ldb, float beta, float *dC, int ldc, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (M < 0 || N < 0 || K < 0) return fail(P2H_E_ARG, "p2h_sgemm: negative shape");
+    if (M > 0 && N > 0 && (!dC || ldc < N)) return fail(P2H_E_ARG, "p2h_sgemm: bad C");
+    if (M > 0 && N > 0 && K > 0 &&
+        (!dA || !dB || lda < (transA ? M : K) || ldb < (transB ? K : N)))
+        return fail(P2H_E_ARG, "p2h_sgemm: bad A/B");
+    hipStream_t s = stream_of(stream);
+    if (M == 0 || N == 0) return P2H_OK;
+    if (alpha == 0.0f || K == 0) return p2h_scale_c(M, N, beta, dC, ldc, s);   /* blas.c:748-749 */
+    p2k::ExactArgs g;
+    memset(&g, 0, sizeof g);
+    g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
+    g.A = dA; g.lda = lda; g.transA = transA ? 1 : 0;
+    g.Bf = dB; g.ldbf = ldb; g.transB = transB ? 1 : 0;
+    g.C = dC; g.ldc = ldc;
+    return launch_exact(p2k::EXB_F32, g, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,397 @@
+"""ctypes binding of the MI355X five-value GEMM (lib/libp2hip.so, include/p2hip.h) and the input generator
+(lib/libp2gen.so, include/p2gen.h), with numpy host arrays.
+
+Device memory, copies, streams and events all go through libp2hip.so itself, so a process that uses this module
+holds exactly one HIP runtime. Every call raises P2Error when the library reports an error; nothing here computes
+a product on the CPU.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBDIR = os.path.join(HERE, "lib")
+HIP_SO = os.path.join(LIBDIR, "libp2hip.so")
+GEN_SO = os.path.join(LIBDIR, "libp2gen.so")
+BLAS_SO = os.path.join(LIBDIR, "libphonon2_gemm.so")
+
+INT8, EXACT, INT8W = 0, 1, 2
+MODES = {"int8": INT8, "exact": EXACT, "int8w": INT8W}
+Q_KALIGN = 128
+
+
+class P2Error(RuntimeError):
+    pass
+
+
+_vp, _sz, _i, _f = C.c_void_p, C.c_size_t, C.c_int, C.c_float
+
+_HIP_SIG = {
+    "p2h_init": (_i, []),
+    "p2h_last_error": (C.c_char_p, []),
+    "p2h_device_name": (C.c_char_p, []),
+    "p2h_device_cu_count": (_i, []),
+    "p2h_stream_create": (_vp, []),
+    "p2h_stream_destroy": (_i, [_vp]),
+    "p2h_stream_sync": (_i, [_vp]),
+    "p2h_thread_stream": (_vp, []),
+    "p2h_malloc": (_vp, [_sz]),
+    "p2h_free": (_i, [_vp]),
+    "p2h_host_malloc": (_vp, [_sz]),
+    "p2h_host_free": (_i, [_vp]),
+    "p2h_memset": (_i, [_vp, _i, _sz, _vp]),
+    "p2h_memcpy_h2d": (_i, [_vp, _vp, _sz, _vp]),
+    "p2h_memcpy_d2h": (_i, [_vp, _vp, _sz, _vp]),
+    "p2h_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
+    "p2h_memcpy2d_h2d": (_i, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
+    "p2h_memcpy2d_d2h": (_i, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
+    "p2h_event_create": (_vp, []),
+    "p2h_event_destroy": (_i, [_vp]),
+    "p2h_event_record": (_i, [_vp, _vp]),
+    "p2h_event_sync": (_i, [_vp]),
+    "p2h_event_elapsed_ms": (_f, [_vp, _vp]),
+    "p2h_fv_weight_upload": (_vp, [_vp, _vp, _vp, _vp, _i, _i]),
+    "p2h_fv_weight_wrap": (_vp, [_vp, _vp, _vp, _vp, _i, _i]),
+    "p2h_weight_free": (None, [_vp]),
+    "p2h_weight_shape": (_i, [_vp, C.POINTER(_i), C.POINTER(_i)]),
+    "p2h_weight_device_bytes": (_sz, [_vp]),
+    "p2h_fv_pack_codes": (_i, [_vp, _vp, _vp]),
+    "p2h_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
+    "p2h_q_ld": (_i, [_i]),
+    "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp]),
+    "p2h_fvb_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
+    "p2h_fvb_workspace_bytes": (_sz, [_i, _i, _i]),
+    "p2h_fvb_acc_i32": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp]),
+    "p2h_scale_c": (_i, [_i, _i, _f, _vp, _i, _vp]),
+    "p2h_q8b_gemm_q8a": (_i, [_i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _vp, _f, _vp, _i, _vp]),
+    "p2h_q8b_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
+    "p2h_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
+}
+
+_hip = None
+_gen = None
+
+
+def hip():
+    """libp2hip.so with its prototypes declared; raises if the library is missing (no CPU fallback exists)."""
+    global _hip
+    if _hip is None:
+        if not os.path.exists(HIP_SO):
+            raise P2Error(f"{HIP_SO} is not built: run __graft_entry__.build() or make -C phonon-2-c_amd")
+        L = C.CDLL(HIP_SO)
+        for name, (res, args) in _HIP_SIG.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _hip = L
+    return _hip
+
+
+def last_error():
+    return hip().p2h_last_error().decode(errors="replace")
+
+
+def _ok(rc, what):
+    if rc != 0:
+        raise P2Error(f"{what}: {last_error()} (rc {rc})")
+
+
+def init():
+    _ok(hip().p2h_init(), "p2h_init")
+    return hip().p2h_device_name().decode()
+
+
+def device_cu_count():
+    return hip().p2h_device_cu_count()
+
+
+# ── device memory ───────────────────────────────────────────────────────────────────────────────────────────────
+
+class DeviceBuffer:
+    """A device allocation; .ptr is the device address."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = hip().p2h_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise P2Error(f"p2h_malloc({self.nbytes}): {last_error()}")
+
+    def free(self):
+        if self.ptr:
+            hip().p2h_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def upload(self, arr, stream=None, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes, "upload beyond the buffer"
+        _ok(hip().p2h_memcpy_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes, stream), "h2d")
+        sync(stream)
+        return self
+
+    def download(self, shape, dtype, stream=None, offset=0):
+        out = np.empty(shape, dtype)
+        assert offset + out.nbytes <= self.nbytes, "download beyond the buffer"
+        sync(stream)
+        _ok(hip().p2h_memcpy_d2h(out.ctypes.data, self.ptr + offset, out.nbytes, stream), "d2h")
+        sync(stream)
+        return out
+
+    def zero(self, stream=None):
+        _ok(hip().p2h_memset(self.ptr, 0, self.nbytes, stream), "memset")
+        return self
+
+
+def to_device(arr, stream=None, pad=0):
+    arr = np.ascontiguousarray(arr)
+    b = DeviceBuffer(arr.nbytes + pad)
+    if pad:
+        b.zero(stream)
+    return b.upload(arr, stream)
+
+
+def sync(stream=None):
+    _ok(hip().p2h_stream_sync(stream), "stream sync")
+
+
+class Stream:
+    def __init__(self):
+        self.ptr = hip().p2h_stream_create()
+        if not self.ptr:
+            raise P2Error(last_error())
+
+    def sync(self):
+        sync(self.ptr)
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                hip().p2h_stream_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        self.ptr = hip().p2h_event_create()
+        if not self.ptr:
+            raise P2Error(last_error())
+
+    def record(self, stream=None):
+        _ok(hip().p2h_event_record(self.ptr, stream), "event record")
+
+    def sync(self):
+        _ok(hip().p2h_event_sync(self.ptr), "event sync")
+
+    def elapsed_ms(self, end):
+        ms = hip().p2h_event_elapsed_ms(self.ptr, end.ptr)
+        if ms < 0:
+            raise P2Error("hipEventElapsedTime failed")
+        return ms
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                hip().p2h_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+# ── weights ─────────────────────────────────────────────────────────────────────────────────────────────────────
+
+class FvWeight:
+    """A device-resident five-value weight [K, N] uploaded from host planes."""
+
+    def __init__(self, signs, flags, lo, hi, K, N):
+        s = np.ascontiguousarray(signs, np.uint8)
+        f = np.ascontiguousarray(flags, np.uint8)
+        l = np.ascontiguousarray(lo, np.float32)
+        h = np.ascontiguousarray(hi, np.float32)
+        assert s.size == K * N // 4 and f.size == K * N // 8 and l.size == N and h.size == N
+        self.K, self.N = K, N
+        self.ptr = hip().p2h_fv_weight_upload(s.ctypes.data, f.ctypes.data, l.ctypes.data, h.ctypes.data, K, N)
+        if not self.ptr:
+            raise P2Error(f"p2h_fv_weight_upload: {last_error()}")
+
+    def device_bytes(self):
+        return hip().p2h_weight_device_bytes(self.ptr)
+
+    def free(self):
+        if self.ptr:
+            hip().p2h_weight_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def q_ld(K):
+    return hip().p2h_q_ld(K)
+
+
+def workspace_bytes(mode, M, K):
+    return hip().p2h_fvb_workspace_bytes(MODES.get(mode, mode), M, K)
+
+
+# ── device-pointer entry points (asynchronous on `stream`) ───────────────────────────────────────────────────────
+
+def quant_rows_dev(M, K, dA, lda, dQ, ldq, dS, stream=None):
+    _ok(hip().p2h_quant_rows(M, K, dA, lda, dQ, ldq, dS, stream), "p2h_quant_rows")
+
+
+def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, stream=None):
+    _ok(hip().p2h_fvb_gemm_q8a(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, stream),
+        "p2h_fvb_gemm_q8a")
+
+
+def fvb_gemm_dev(mode, M, N, K, alpha, dA, lda, w, beta, dC, ldc, ws, ws_bytes, stream=None):
+    _ok(hip().p2h_fvb_gemm(MODES.get(mode, mode), M, N, K, alpha, dA, lda, w.ptr, beta, dC, ldc, ws, ws_bytes,
+                           stream), "p2h_fvb_gemm")
+
+
+# ── host-array conveniences (upload, run, download, synchronise) ─────────────────────────────────────────────────
+
+def quant_rows(A, K=None):
+    A = np.ascontiguousarray(A, np.float32)
+    M, lda = A.shape
+    K = lda if K is None else K
+    ldq = q_ld(K)
+    dA = to_device(A)
+    dQ = DeviceBuffer(max(M, 1) * max(ldq, 16))
+    dS = DeviceBuffer(max(M, 1) * 4)
+    quant_rows_dev(M, K, dA.ptr, lda, dQ.ptr, ldq, dS.ptr)
+    q = dQ.download((M, ldq), np.int8)
+    s = dS.download((M,), np.float32)
+    return q, s
+
+
+def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None):
+    """p2h_fvb_gemm on host arrays: A [M, lda] (first K columns used), C0 [M, ldc] (ldc >= N) or None."""
+    A = np.ascontiguousarray(A, np.float32)
+    M, lda = A.shape
+    K = w.K if K is None else K
+    N = w.N
+    C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
+    ldc = C0.shape[1]
+    dA = to_device(A)
+    dC = to_device(C0)
+    wsb = workspace_bytes(mode, M, K)
+    ws = DeviceBuffer(max(wsb, 256))
+    fvb_gemm_dev(mode, M, N, K, alpha, dA.ptr, lda, w, beta, dC.ptr, ldc, ws.ptr, max(wsb, 256))
+    return dC.download((M, ldc), np.float32)
+
+
+def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None):
+    """p2h_fvb_gemm_q8a on a quantised host matrix q [M, K] (re-padded to the library's ldq)."""
+    q = np.ascontiguousarray(q, np.int8)
+    M, K = q.shape
+    N = w.N
+    ldq = q_ld(K)
+    qp = np.zeros((M, ldq), np.int8)
+    qp[:, :K] = q
+    C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
+    dQ, dS, dC = to_device(qp), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
+    fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ.ptr, ldq, dS.ptr, w, beta, dC.ptr, C0.shape[1])
+    return dC.download(C0.shape, np.float32)
+
+
+def fvb_acc_i32(mode, q, w):
+    """The raw int32 sums of the int8 kernel over all K: one matrix (int8w) or the S and T sums (int8)."""
+    q = np.ascontiguousarray(q, np.int8)
+    M, K = q.shape
+    N = w.N
+    ldq = q_ld(K)
+    qp = np.zeros((M, ldq), np.int8)
+    qp[:, :K] = q
+    dQ = to_device(qp)
+    d1 = DeviceBuffer(M * N * 4)
+    d2 = DeviceBuffer(M * N * 4)
+    m = MODES.get(mode, mode)
+    _ok(hip().p2h_fvb_acc_i32(m, M, N, K, dQ.ptr, ldq, w.ptr, d1.ptr, d2.ptr if m == INT8 else None, N, None),
+        "p2h_fvb_acc_i32")
+    a1 = d1.download((M, N), np.int32)
+    return (a1, d2.download((M, N), np.int32)) if m == INT8 else a1
+
+
+def fv_pack_codes(w):
+    d = DeviceBuffer(w.K * w.N)
+    _ok(hip().p2h_fv_pack_codes(w.ptr, d.ptr, None), "p2h_fv_pack_codes")
+    return d.download((w.K * w.N,), np.int8)
+
+
+def q8b_gemm(mode, A, B, scales, alpha=1.0, beta=0.0, C0=None):
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.int8)
+    M, K = A.shape
+    N = B.shape[1]
+    C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
+    dA, dB, dS, dC = to_device(A), to_device(B), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
+    wsb = workspace_bytes(mode, M, K)
+    ws = DeviceBuffer(max(wsb, 256))
+    _ok(hip().p2h_q8b_gemm(MODES.get(mode, mode), M, N, K, alpha, dA.ptr, K, dB.ptr, N, dS.ptr, beta, dC.ptr,
+                           C0.shape[1], ws.ptr, max(wsb, 256), None), "p2h_q8b_gemm")
+    return dC.download(C0.shape, np.float32)
+
+
+def sgemm(A, B, transA=False, transB=False, alpha=1.0, beta=0.0, C0=None):
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M = A.shape[1] if transA else A.shape[0]
+    K = A.shape[0] if transA else A.shape[1]
+    N = B.shape[0] if transB else B.shape[1]
+    C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
+    dA, dB, dC = to_device(A), to_device(B), to_device(C0)
+    _ok(hip().p2h_sgemm(int(transA), int(transB), M, N, K, alpha, dA.ptr, A.shape[1], dB.ptr, B.shape[1], beta,
+                        dC.ptr, C0.shape[1], None), "p2h_sgemm")
+    return dC.download(C0.shape, np.float32)
+
+
+# ── the generator ───────────────────────────────────────────────────────────────────────────────────────────────
+
+def gen():
+    global _gen
+    if _gen is None:
+        if not os.path.exists(GEN_SO):
+            raise P2Error(f"{GEN_SO} is not built")
+        L = C.CDLL(GEN_SO)
+        u64 = C.c_uint64
+        L.p2g_activations.argtypes = [u64, u64, _i, _i, _vp]
+        L.p2g_fv_weight.argtypes = [u64, u64, _i, _i, _vp, _vp, _vp, _vp]
+        L.p2g_i8_weight.argtypes = [u64, u64, _i, _i, _vp, _vp]
+        L.p2g_round_fp16.argtypes = [C.c_double]
+        L.p2g_round_fp16.restype = C.c_float
+        for n in ("p2g_activations", "p2g_fv_weight", "p2g_i8_weight"):
+            getattr(L, n).restype = None
+        _gen = L
+    return _gen
+
+
+def gen_activations(seed, tensor_id, M, K):
+    A = np.empty((M, K), np.float32)
+    gen().p2g_activations(seed, tensor_id, M, K, A.ctypes.data)
+    return A
+
+
+def gen_fv_weight(seed, tensor_id, K, N):
+    signs = np.empty((K, N // 4), np.uint8)
+    flags = np.empty((K, N // 8), np.uint8)
+    lo = np.empty(N, np.float32)
+    hi = np.empty(N, np.float32)
+    gen().p2g_fv_weight(seed, tensor_id, K, N, signs.ctypes.data, flags.ctypes.data, lo.ctypes.data, hi.ctypes.data)
+    return signs, flags, lo, hi
+
+
+def gen_i8_weight(seed, tensor_id, K, N):
+    q8 = np.empty((K, N), np.int8)
+    sc = np.empty(N, np.float32)
+    gen().p2g_i8_weight(seed, tensor_id, K, N, q8.ctypes.data, sc.ctypes.data)
+    return q8, sc

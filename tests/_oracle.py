@@ -1,0 +1,221 @@
+"""ctypes wrapper over the CPU oracle (oracle/liboracle.so) and the reference build (oracle/_ref/libp2ref.so).
+
+Test infrastructure: the checker for the HIP path. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libp2ref.so")
+
+INT8, EXACT, INT8W = 0, 1, 2
+MODES = {"int8": INT8, "exact": EXACT, "int8w": INT8W}
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i, _f = C.c_int, C.c_float
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"{ORACLE_SO} missing: run `make -C oracle`")
+        L = C.CDLL(ORACLE_SO)
+        sig = {
+            "p2o_pack_planes": [_i8p, _u8p, _i, _i, _u8p, _u8p],
+            "p2o_unpack_planes": [_u8p, _u8p, _i, _i, _u8p, _u8p],
+            "p2o_expand_exact": [_u8p, _u8p, _f32p, _f32p, _i, _i, _f32p],
+            "p2o_sgemm_fvb_exact": [_i, _i, _i, _f, _f32p, _i, _u8p, _u8p, _f32p, _f32p, _f, _f32p, _i],
+            "p2o_quant_rows": [_f32p, _i, _i, _i, _i8p, _f32p],
+            "p2o_clo": [_f32p, _f32p, _i, _u8p],
+            "p2o_codes_i8w": [_u8p, _u8p, _f32p, _f32p, _i, _i, _i8p],
+            "p2o_fv_pack_codes": [_u8p, _u8p, _f32p, _f32p, _i, _i, _i8p],
+            "p2o_planes_i8": [_u8p, _u8p, _i, _i, _i8p, _i8p],
+            "p2o_acc_i32": [_i8p, _i, _i, _i8p, _i, _i, _i, _i32p],
+            "p2o_gemm_i8_run": [_i, _i, _i, _i, _f, _i8p, _f32p, _u8p, _u8p, _f32p, _f32p, _i, _f32p, _i],
+            "p2o_gemm_q8b_run": [_i, _i, _i, _f, _i8p, _f32p, _i8p, _i, _f32p, _i, _f32p, _i],
+            "p2o_sgemm_fvb": [_i, _i, _i, _i, _f, _f32p, _i, _u8p, _u8p, _f32p, _f32p, _f, _f32p, _i],
+            "p2o_sgemm_q8b": [_i, _i, _i, _i, _f, _f32p, _i, _i8p, _f32p, _i, _f, _f32p, _i],
+            "p2o_mode_from_env": [C.c_char_p, C.c_char_p],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = C.c_int if name == "p2o_mode_from_env" else None
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def pack_planes(sign, is_hi):
+    K, N = sign.shape
+    s = np.zeros((K, N // 4), np.uint8)
+    f = np.zeros((K, N // 8), np.uint8)
+    lib().p2o_pack_planes(_c(sign, np.int8), _c(is_hi, np.uint8), K, N, s, f)
+    return s, f
+
+
+def unpack_planes(signs, flags, K, N):
+    code = np.zeros((K, N), np.uint8)
+    flag = np.zeros((K, N), np.uint8)
+    lib().p2o_unpack_planes(_c(signs, np.uint8), _c(flags, np.uint8), K, N, code, flag)
+    return code, flag
+
+
+def expand_exact(signs, flags, lo, hi, K, N):
+    W = np.zeros((K, N), np.float32)
+    lib().p2o_expand_exact(_c(signs, np.uint8), _c(flags, np.uint8), _c(lo, np.float32), _c(hi, np.float32), K, N, W)
+    return W
+
+
+def quant_rows(A, K=None):
+    A = _c(A, np.float32)
+    M, lda = A.shape
+    K = lda if K is None else K
+    q = np.zeros((M, K), np.int8)
+    sc = np.zeros(max(M, 1), np.float32)
+    lib().p2o_quant_rows(A, M, K, lda, q, sc)
+    return q, sc[:M]
+
+
+def clo(lo, hi):
+    N = len(lo)
+    out = np.zeros(N, np.uint8)
+    lib().p2o_clo(_c(lo, np.float32), _c(hi, np.float32), N, out)
+    return out
+
+
+def codes_i8w(signs, flags, lo, hi, K, N):
+    out = np.zeros((K, N), np.int8)
+    lib().p2o_codes_i8w(_c(signs, np.uint8), _c(flags, np.uint8), _c(lo, np.float32), _c(hi, np.float32), K, N, out)
+    return out
+
+
+def fv_pack_codes(signs, flags, lo, hi, K, N):
+    out = np.zeros(K * N, np.int8)
+    lib().p2o_fv_pack_codes(_c(signs, np.uint8), _c(flags, np.uint8), _c(lo, np.float32), _c(hi, np.float32),
+                            K, N, out)
+    return out
+
+
+def planes_i8(signs, flags, K, N):
+    S = np.zeros((K, N), np.int8)
+    T = np.zeros((K, N), np.int8)
+    lib().p2o_planes_i8(_c(signs, np.uint8), _c(flags, np.uint8), K, N, S, T)
+    return S, T
+
+
+def acc_i32(q, B, k0=0, k1=None):
+    q = _c(q, np.int8)
+    B = _c(B, np.int8)
+    M, K = q.shape
+    N = B.shape[1]
+    k1 = K if k1 is None else k1
+    acc = np.zeros((M, N), np.int32)
+    lib().p2o_acc_i32(q, M, K, B, N, k0, k1, acc)
+    return acc
+
+
+def gemm_i8_run(mode, q, a_scales, signs, flags, lo, hi, N, alpha=1.0, C0=None, beta_zero=True):
+    q = _c(q, np.int8)
+    M, K = q.shape
+    C = np.zeros((M, N), np.float32) if C0 is None else _c(C0, np.float32).copy()
+    lib().p2o_gemm_i8_run(MODES[mode] if isinstance(mode, str) else mode, M, N, K, alpha, q,
+                          _c(a_scales, np.float32), _c(signs, np.uint8), _c(flags, np.uint8),
+                          _c(lo, np.float32), _c(hi, np.float32), 1 if beta_zero else 0, C, C.shape[1])
+    return C
+
+
+def sgemm_fvb(mode, A, signs, flags, lo, hi, N, alpha=1.0, beta=0.0, C0=None, K=None, ldc=None):
+    """p2_sgemm_fvb in `mode`; A is [M, lda] with the first K columns used; C0 is [M, ldc]."""
+    A = _c(A, np.float32)
+    M, lda = A.shape
+    K = lda if K is None else K
+    if C0 is None:
+        C = np.zeros((M, N if ldc is None else ldc), np.float32)
+    else:
+        C = _c(C0, np.float32).copy()
+    lib().p2o_sgemm_fvb(MODES[mode] if isinstance(mode, str) else mode, M, N, K, alpha, A, lda,
+                        _c(signs, np.uint8), _c(flags, np.uint8), _c(lo, np.float32), _c(hi, np.float32),
+                        beta, C, C.shape[1])
+    return C
+
+
+def sgemm_q8b(mode, A, B, scales, N, alpha=1.0, beta=0.0, C0=None, K=None):
+    A = _c(A, np.float32)
+    B = _c(B, np.int8)
+    M, lda = A.shape
+    K = lda if K is None else K
+    C = np.zeros((M, N), np.float32) if C0 is None else _c(C0, np.float32).copy()
+    lib().p2o_sgemm_q8b(MODES[mode] if isinstance(mode, str) else mode, M, N, K, alpha, A, lda, B,
+                        _c(scales, np.float32), B.shape[1], beta, C, C.shape[1])
+    return C
+
+
+def mode_from_env(p2_gemm, p2_exact):
+    enc = lambda s: None if s is None else s.encode()
+    return lib().p2o_mode_from_env(enc(p2_gemm), enc(p2_exact))
+
+
+# ── the reference's own library, built from its C sources by oracle/Makefile ─────────────────────────────────
+
+class FiveValueB(C.Structure):
+    """The reference's FiveValueB (blas.h:39-45)."""
+    _fields_ = [("signs", C.c_void_p), ("flags", C.c_void_p), ("lo", C.c_void_p), ("hi", C.c_void_p),
+                ("codes", C.c_void_p)]
+
+
+_ref = None
+
+
+def ref_available():
+    return os.path.exists(REF_SO)
+
+
+def ref():
+    """The reference's p2_sgemm_fvb / p2_sgemm_q8b (x86: the exact fp32 AVX2 route, blas.c:1043-1045)."""
+    global _ref
+    if _ref is None:
+        L = C.CDLL(REF_SO)
+        L.p2_sgemm_fvb.argtypes = [_i, _i, _i, _f, C.c_void_p, _i, C.POINTER(FiveValueB), _f, C.c_void_p, _i]
+        L.p2_sgemm_fvb.restype = None
+        L.p2_sgemm_q8b.argtypes = [_i, _i, _i, _f, C.c_void_p, _i, C.c_void_p, C.c_void_p, _i, _f, C.c_void_p, _i]
+        L.p2_sgemm_q8b.restype = None
+        L.p2_gemm_mode.restype = C.c_char_p
+        _ref = L
+    return _ref
+
+
+def ref_sgemm_fvb(A, signs, flags, lo, hi, N, alpha, beta, C0, K=None):
+    A = _c(A, np.float32)
+    M, lda = A.shape
+    K = lda if K is None else K
+    out = _c(C0, np.float32).copy()
+    s, f, l, h = _c(signs, np.uint8), _c(flags, np.uint8), _c(lo, np.float32), _c(hi, np.float32)
+    b = FiveValueB(s.ctypes.data, f.ctypes.data, l.ctypes.data, h.ctypes.data, None)
+    ref().p2_sgemm_fvb(M, N, K, alpha, A.ctypes.data, lda, C.byref(b), beta, out.ctypes.data, out.shape[1])
+    return out
+
+
+def ref_sgemm_q8b(A, B, scales, N, alpha, beta, C0, K=None):
+    A = _c(A, np.float32)
+    B = _c(B, np.int8)
+    M, lda = A.shape
+    K = lda if K is None else K
+    out = _c(C0, np.float32).copy()
+    sc = _c(scales, np.float32)
+    ref().p2_sgemm_q8b(M, N, K, alpha, A.ctypes.data, lda, B.ctypes.data, sc.ctypes.data, B.shape[1],
+                       beta, out.ctypes.data, out.shape[1])
+    return out

@@ -1,0 +1,22 @@
+"""The blas.h drop-in (libphonon2_gemm.so) in each mode, one child process per mode because the mode is latched
+once per process (blas.c:1049-1053)."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+CHILD = os.path.join(os.path.dirname(__file__), "dropin_child.py")
+
+
+@pytest.mark.parametrize("env", [{}, {"P2_GEMM": "int8"}, {"P2_GEMM": "exact"}, {"P2_GEMM": "int8", "P2_EXACT": "1"}])
+def test_dropin_mode(env):
+    e = dict(os.environ)
+    e.pop("P2_GEMM", None)
+    e.pop("P2_EXACT", None)
+    e.update(env)
+    print(f"drop-in child with {env}", flush=True)
+    r = subprocess.run([sys.executable, CHILD], env=e, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr

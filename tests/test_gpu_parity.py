@@ -1,0 +1,215 @@
+"""Parity of the HIP path (libp2hip.so, through its C ABI) with the oracle, on the GPU.
+
+Bars: int32 accumulators, quantised activations, codes and every exact-mode output bit-exact; int8 / int8w fp32
+outputs within 1e-5 relative (|gpu − ref| <= 1e-5 · max(|ref|, rms of the reference row)) – and, because the
+kernel folds its int32 sums per 1024-row K block with the reference's own fp32 operations, also bit-exact.
+Full-size shapes compare a sample of rows: the GEMM is row-independent, so rows of C depend only on the same rows
+of A.
+"""
+import numpy as np
+import pytest
+
+import _oracle as O
+import p2gemm as P
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261201
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    name = P.init()
+    assert name.startswith("gfx950"), name
+    return name
+
+
+def _weight(K, N, tid, code3=False):
+    signs, flags, lo, hi = P.gen_fv_weight(SEED, tid, K, N)
+    if code3:
+        rng = np.random.default_rng(tid)
+        flat = signs.reshape(-1)
+        for i in rng.choice(flat.size, size=max(2, flat.size // 50), replace=False):
+            flat[i] |= np.uint8(3 << (2 * int(rng.integers(0, 4))))
+    return signs, flags, lo, hi
+
+
+def _assert_fp32(got, ref, bit_exact=True):
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2, axis=1, keepdims=True))
+    tol = 1e-5 * np.maximum(np.abs(ref), rms)
+    bad = np.abs(got.astype(np.float64) - ref) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside 1e-5 relative; first at {np.argwhere(bad)[0]}"
+    if bit_exact:
+        neq = got.view(np.uint32) != ref.view(np.uint32)
+        assert not neq.any(), f"{neq.sum()} of {neq.size} not bit-exact; first at {np.argwhere(neq)[0]}"
+
+
+def _bits_equal(a, b):
+    return np.array_equal(np.ascontiguousarray(a).view(np.uint32), np.ascontiguousarray(b).view(np.uint32))
+
+
+# ── activation quantisation ─────────────────────────────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("M,K", [(64, 1024), (7, 20), (300, 4096), (5, 4), (129, 1028)])
+def test_quant_rows_bit_exact(M, K):
+    A = P.gen_activations(SEED, 100 + K, M, K)
+    if M > 3:
+        A[2] = 0.0   # a zero row: scale 1, q 0
+    q_gpu, s_gpu = P.quant_rows(A)
+    q_ref, s_ref = O.quant_rows(A)
+    assert _bits_equal(s_gpu, s_ref)
+    assert np.array_equal(q_gpu[:, :K], q_ref)
+    assert (q_gpu[:, K:] == 0).all(), "padding columns must be zero"
+
+
+def test_quant_rows_strided_unaligned():
+    A = P.gen_activations(SEED, 7, 9, 303)
+    q_gpu, s_gpu = P.quant_rows(A, K=300)   # lda 303: rows are not 16-byte aligned
+    q_ref, s_ref = O.quant_rows(A, K=300)
+    assert _bits_equal(s_gpu, s_ref) and np.array_equal(q_gpu[:, :300], q_ref)
+
+
+# ── int32 accumulators ──────────────────────────────────────────────────────────────────────────────────────────
+
+ACC_SHAPES = [(1, 64, 16), (37, 1024, 64), (130, 1100, 272), (200, 4096, 144), (375, 1024, 1024)]
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+@pytest.mark.parametrize("M,K,N", ACC_SHAPES)
+def test_acc_i32_bit_exact(mode, M, K, N):
+    signs, flags, lo, hi = _weight(K, N, 200 + N, code3=(K == 1100))
+    A = P.gen_activations(SEED, 300 + M, M, K)
+    q, _ = O.quant_rows(A)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    got = P.fvb_acc_i32(mode, q, w)
+    if mode == "int8w":
+        ref = O.acc_i32(q, O.codes_i8w(signs, flags, lo, hi, K, N))
+        assert np.array_equal(got, ref)
+    else:
+        S, T = O.planes_i8(signs, flags, K, N)
+        assert np.array_equal(got[0], O.acc_i32(q, S))
+        assert np.array_equal(got[1], O.acc_i32(q, T))
+
+
+# ── the whole GEMM on fp32 activations ──────────────────────────────────────────────────────────────────────────
+
+GEMM_CASES = [
+    # M, K, N, alpha, beta
+    (1, 64, 16, 1.0, 0.0),
+    (37, 1024, 64, 1.0, 0.0),
+    (38, 1024, 4096, 1.0, 0.0),
+    (38, 4096, 1024, 0.5, 1.0),
+    (130, 1028, 272, -1.5, 0.3),
+    (375, 1024, 1024, 1.0, 0.0),
+    (9, 100, 32, 1.0, 1.0),
+    (200, 2052, 144, 0.7, 0.0),
+]
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8", "exact"])
+@pytest.mark.parametrize("M,K,N,alpha,beta", GEMM_CASES)
+def test_fvb_gemm_parity(mode, M, K, N, alpha, beta):
+    signs, flags, lo, hi = _weight(K, N, 400 + K + N)
+    A = P.gen_activations(SEED, 500 + M, M, K)
+    C0 = P.gen_activations(SEED, 600 + N, M, N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    got = P.fvb_gemm(mode, A, w, alpha=alpha, beta=beta, C0=C0)
+    ref = O.sgemm_fvb(mode, A, signs, flags, lo, hi, N, alpha=alpha, beta=beta, C0=C0)
+    _assert_fp32(got, ref)
+
+
+def test_fvb_gemm_strides_and_alpha_zero():
+    K, N, M = 256, 48, 11
+    signs, flags, lo, hi = _weight(K, N, 11)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 12, M, K + 5)
+    C0 = P.gen_activations(SEED, 13, M, N + 3)
+    for mode in ("int8w", "int8", "exact"):
+        got = P.fvb_gemm(mode, A, w, alpha=1.25, beta=1.0, C0=C0, K=K)
+        ref = O.sgemm_fvb(mode, A, signs, flags, lo, hi, N, alpha=1.25, beta=1.0, C0=C0, K=K)
+        _assert_fp32(got, ref)
+        got0 = P.fvb_gemm(mode, A, w, alpha=0.0, beta=0.5, C0=C0, K=K)
+        ref0 = O.sgemm_fvb(mode, A, signs, flags, lo, hi, N, alpha=0.0, beta=0.5, C0=C0, K=K)
+        assert _bits_equal(got0, ref0)
+
+
+def test_fvb_gemm_q8a_matches_fp32_entry():
+    K, N, M = 1024, 4096, 375
+    signs, flags, lo, hi = _weight(K, N, 21)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 22, M, K)
+    q, sc = O.quant_rows(A)
+    got = P.fvb_gemm_q8a("int8w", q, sc, w)
+    ref = O.gemm_i8_run("int8w", q, sc, signs, flags, lo, hi, N)
+    _assert_fp32(got, ref)
+
+
+def test_code3_int8w_and_exact():
+    K, N, M = 128, 64, 20
+    signs, flags, lo, hi = _weight(K, N, 31, code3=True)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 32, M, K)
+    for mode in ("int8w", "int8", "exact"):
+        _assert_fp32(P.fvb_gemm(mode, A, w), O.sgemm_fvb(mode, A, signs, flags, lo, hi, N))
+
+
+@pytest.mark.parametrize("name", sorted({k.split("/")[0] for k in np.load(
+    __import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "ref_exact_gemm.npz")).files
+    if k.startswith("fvb")}))
+def test_exact_against_reference_golden(name):
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_exact_gemm.npz"))
+    g = lambda f: z[f"{name}/{f}"]
+    M, K, N = (int(x) for x in g("dims"))
+    alpha, beta = (float(x) for x in g("ab"))
+    w = P.FvWeight(g("signs"), g("flags"), g("lo"), g("hi"), K, N)
+    got = P.fvb_gemm("exact", g("A"), w, alpha=alpha, beta=beta, C0=g("C0"), K=K)
+    assert _bits_equal(got, g("C"))
+
+
+# ── codes, int8 tables, fp32 GEMM ───────────────────────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("K,N", [(64, 16), (1024, 1024), (4096, 1024)])
+def test_pack_codes_bit_exact(K, N):
+    signs, flags, lo, hi = _weight(K, N, 41, code3=(K == 64))
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    assert np.array_equal(P.fv_pack_codes(w), O.fv_pack_codes(signs, flags, lo, hi, K, N))
+
+
+@pytest.mark.parametrize("mode", ["int8w", "exact"])
+@pytest.mark.parametrize("M,K,N,beta", [(11, 96, 32, 0.0), (375, 4096, 1024, 1.0), (3, 1030, 48, 0.0)])
+def test_q8b_parity(mode, M, K, N, beta):
+    B, sc = P.gen_i8_weight(SEED, 51, K, N)
+    A = P.gen_activations(SEED, 52, M, K)
+    C0 = P.gen_activations(SEED, 53, M, N)
+    got = P.q8b_gemm(mode, A, B, sc, alpha=0.75, beta=beta, C0=C0)
+    ref = O.sgemm_q8b(mode, A, B, sc, N, alpha=0.75, beta=beta, C0=C0)
+    _assert_fp32(got, ref)
+
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+def test_sgemm_fp32(tA, tB):
+    rng = np.random.default_rng(61)
+    M, K, N = 45, 77, 50
+    A = rng.standard_normal((K, M) if tA else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tB else (K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    got = P.sgemm(A, B, tA, tB, alpha=0.5, beta=0.25, C0=C0)
+    ref = 0.5 * ((A.T if tA else A).astype(np.float64) @ (B.T if tB else B).astype(np.float64)) + 0.25 * C0
+    assert np.allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+# ── full-size shapes, sampled rows ──────────────────────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024), (749, 1024, 1024), (375, 1024, 3072)])
+def test_full_size_sampled_rows(M, K, N):
+    signs, flags, lo, hi = _weight(K, N, 700 + K + N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 800 + M, M, K)
+    got = P.fvb_gemm("int8w", A, w)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 48, replace=False)]))
+    ref = O.sgemm_fvb("int8w", A[rows], signs, flags, lo, hi, N)
+    _assert_fp32(got[rows], ref)
+    # a size-independent property over every row: rows scaled by 2^j give outputs scaled by exactly 2^j
+    got2 = P.fvb_gemm("int8w", A * np.float32(4.0), w)
+    assert _bits_equal(got2, (got * np.float32(4.0)).astype(np.float32))
