@@ -54,7 +54,10 @@ def main():
             failures.append(what)
 
     expect(L.p2_gemm_exact() == (mode_env == O.EXACT), "p2_gemm_exact")
-    expect(("exact" in L.p2_gemm_mode().decode()) == (mode_env == O.EXACT), "p2_gemm_mode string")
+    # blas.c:1060-1064
+    names = {O.INT8: "int8 dot products, exact weights", O.INT8W: "int8 dot products, int8 weights",
+             O.EXACT: "fp32 expansion (exact)"}
+    expect(L.p2_gemm_mode().decode() == names[mode_env], "p2_gemm_mode string")
 
     seed = 7
     for (M, K, N, alpha, beta) in [(375, 1024, 1024, 1.0, 0.0), (38, 4096, 1024, 0.5, 1.0), (38, 1024, 1024, 1.0, 0.3),
