@@ -1,0 +1,330 @@
+#!/usr/bin/env python3
+"""Throughput of the five-value int8 GEMM on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload ffn375|m6000|m38|sweep|exact375] [--no-cpu-baseline]
+
+Default workload (`ffn375`): the macaron FFN pair of one 30 s window, M = 375 rows: up-projection K=1024 → N=4096,
+then down-projection K=4096 → N=1024, int8w. A step is one pass: quantise A (fp32, resident in HBM) per row,
+five-value GEMM up, quantise the fp32 up output, five-value GEMM down. All operands are device-resident before the
+timed region; the step is replayed from a HIP graph. Synthetic data from the seeded generator (include/p2gen.h).
+
+Prints ONE JSON line. `value` is int8 TOPS (2·M·N·K per GEMM), `roofline` is the dominant kernel's achieved
+algorithmic bandwidth against 8 TB/s, measured live with HIP events on the stream the kernels run on, and
+`cpu_baseline` is the reference's own p2_sgemm_fvb (built from its C sources into oracle/_ref/) timed on this
+host's cores on a bounded sample of the same workload. `extra` carries the other configurations of the workload
+set, each measured the same way.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "phonon-2-c_amd"))
+
+import p2gemm as P  # noqa: E402
+
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOPS
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32
+SEED = 20261201
+
+
+def gemm_ops(M, N, K):
+    return 2.0 * M * N * K
+
+
+def gemm_bytes(M, N, K, a_bytes_per_elem, beta1=False):
+    """Algorithmic HBM bytes of one five-value GEMM: packed planes K·N·3/8, lo/hi 8N, activations, fp32 C."""
+    return K * N * 3 / 8 + 8 * N + a_bytes_per_elem * M * K + (4 * M if a_bytes_per_elem == 1 else 0) \
+        + 4 * M * N * (2 if beta1 else 1)
+
+
+def quant_bytes(M, K):
+    return 4 * M * K + M * K + 4 * M
+
+
+class Linear:
+    """One device-resident five-value linear [K, N] with its output buffer."""
+
+    def __init__(self, tid, K, N, M):
+        signs, flags, lo, hi = P.gen_fv_weight(SEED, tid, K, N)
+        self.K, self.N, self.M = K, N, M
+        self.w = P.FvWeight(signs, flags, lo, hi, K, N)
+        ew2 = float(np.mean(0.4 * lo.astype(np.float64) ** 2 + 0.2 * hi.astype(np.float64) ** 2))
+        self.alpha = float(np.float32(1.0 / np.sqrt(K * ew2)))   # keeps a chain of layers at unit variance
+        self.out = P.DeviceBuffer(M * N * 4)
+
+
+class Scratch:
+    """Quantised rows, their scales, and the split-K workspace shared by a chain of linears (stream-ordered)."""
+
+    def __init__(self, M, K, split_bytes):
+        self.ldq = P.q_ld(K)
+        self.q = P.DeviceBuffer(M * self.ldq)
+        self.s = P.DeviceBuffer(M * 4)
+        self.ws = P.Workspace(split_bytes)
+
+
+def run_linear(lin, dA, lda, ws, stream, alpha=None, events=None):
+    """quantise A, then the q8a GEMM; events (e0, e1, e2) bracket the two kernels when given."""
+    a = lin.alpha if alpha is None else alpha
+    if events:
+        events[0].record(stream.ptr)
+    P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ws.ldq, ws.s.ptr, stream.ptr)
+    if events:
+        events[1].record(stream.ptr)
+    P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, a, ws.q.ptr, ws.ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr,
+                       lin.N, ws.ws.ptr, ws.ws.nbytes, stream.ptr)
+    if events:
+        events[2].record(stream.ptr)
+
+
+def time_graph(graph, stream, steps, warmup):
+    for _ in range(warmup):
+        graph.launch()
+    stream.sync()
+    e0, e1 = P.Event(), P.Event()
+    e0.record(stream.ptr)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.launch()
+    e1.record(stream.ptr)
+    e1.sync()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_ms(e1) / steps, wall
+
+
+def kernel_times(linears, inputs, ws, stream, reps):
+    """Average duration (ms) of each linear's quantise and GEMM kernels, from HIP events on their stream."""
+    ev = [[P.Event() for _ in range(3)] for _ in linears]
+    q = np.zeros(len(linears))
+    g = np.zeros(len(linears))
+    for _ in range(reps):
+        for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
+            run_linear(lin, dA, lda, ws, stream, events=ev[i])
+        stream.sync()
+        for i in range(len(linears)):
+            q[i] += ev[i][0].elapsed_ms(ev[i][1])
+            g[i] += ev[i][1].elapsed_ms(ev[i][2])
+    return q / reps, g / reps
+
+
+# ── workloads ──────────────────────────────────────────────────────────────────────────────────────────────────
+
+def build_chain(spec, M_default):
+    """spec: list of (tid, K, N, M, input) with input an index into the chain's outputs or 'x' for the fresh
+    activation buffer of width K. Returns linears, their input pointers, and the workspace."""
+    linears, inputs, fresh = [], [], {}
+    for tid, K, N, M, src in spec:
+        lin = Linear(tid, K, N, M)
+        if src == "x":
+            if (M, K) not in fresh:
+                fresh[(M, K)] = P.to_device(P.gen_activations(SEED, 10_000 + K + M, M, K))
+            inputs.append((fresh[(M, K)].ptr, K))
+        else:
+            inputs.append((linears[src].out.ptr, linears[src].N))
+        linears.append(lin)
+    maxm = max(s[3] for s in spec)
+    maxk = max(s[1] for s in spec)
+    split = max(P.q8a_workspace_bytes("int8w", l.M, l.N, l.K) for l in linears)
+    return linears, inputs, Scratch(maxm, maxk, split), fresh
+
+
+def ffn_spec(M, base=1):
+    return [(base, 1024, 4096, M, "x"), (base + 1, 4096, 1024, M, 0)]
+
+
+def sweep_spec(M=375):
+    """24 FastConformer blocks × 9 five-value linears at their real shapes (weights.c:371-379, encoder.c:333-613):
+    ff1.l1, ff1.l2, qkv, pos (M = 2T−1), out, pw1, pw2, ff2.l1, ff2.l2. The d = 1024 stream chains through
+    ff1 → out → pw2 → ff2; qkv and pw1 read it; pos reads the positional rows."""
+    spec = []
+    for b in range(24):
+        t = 100 + 16 * b
+        i = len(spec)
+        prev = "x" if b == 0 else i - 1          # the previous block's ff2.l2 output
+        spec += [
+            (t + 0, 1024, 4096, M, prev),         # i+0 ff1.linear1
+            (t + 1, 4096, 1024, M, i + 0),        # i+1 ff1.linear2
+            (t + 2, 1024, 3072, M, i + 1),        # i+2 qkv
+            (t + 3, 1024, 1024, 2 * M - 1, "x"),  # i+3 pos
+            (t + 4, 1024, 1024, M, i + 1),        # i+4 out
+            (t + 5, 1024, 2048, M, i + 4),        # i+5 pw1
+            (t + 6, 1024, 1024, M, i + 4),        # i+6 pw2
+            (t + 7, 1024, 4096, M, i + 6),        # i+7 ff2.linear1
+            (t + 8, 4096, 1024, M, i + 7),        # i+8 ff2.linear2
+        ]
+    return spec
+
+
+def measure_chain(spec, stream, steps, warmup, kreps):
+    linears, inputs, ws, keep = build_chain(spec, None)
+    with P.Graph(stream) as graph:
+        for lin, (dA, lda) in zip(linears, inputs):
+            run_linear(lin, dA, lda, ws, stream)
+    ms, wall = time_graph(graph, stream, steps, warmup)
+    qt, gt = kernel_times(linears, inputs, ws, stream, kreps)
+    return linears, ms, wall, qt, gt
+
+
+def summarize(linears, ms, qt, gt):
+    ops = sum(gemm_ops(l.M, l.N, l.K) for l in linears)
+    planes = sum(l.K * l.N * 3 / 8 + 8 * l.N for l in linears)
+    gbytes = [gemm_bytes(l.M, l.N, l.K, 1) for l in linears]
+    return {
+        "ms_per_step": ms,
+        "tops": ops / (ms * 1e-3) / 1e12,
+        "pct_int8_peak": 100.0 * ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
+        "planes_gbs": planes / (ms * 1e-3) / 1e9,
+        "gemm_kernels_ms": [round(float(x), 5) for x in gt],
+        "quant_kernels_ms": [round(float(x), 5) for x in qt],
+        "gemm_kernel_gbs": [round(b / (t * 1e-3) / 1e9, 1) for b, t in zip(gbytes, gt)],
+        "gemm_kernel_tops": [round(gemm_ops(l.M, l.N, l.K) / (t * 1e-3) / 1e12, 1) for l, t in zip(linears, gt)],
+    }
+
+
+def cpu_baseline(M, shapes, seconds=8.0):
+    """The reference's p2_sgemm_fvb (oracle/_ref/libp2ref.so: exact fp32 AVX2 route; int8w compiles only for
+    AArch64, blas.c:1021-1023) on this host's cores, over the same shapes, repeated for about `seconds`."""
+    so = os.path.join(ROOT, "oracle", "_ref", "libp2ref.so")
+    if not os.path.exists(so):
+        return None
+    cores = os.cpu_count() or 1
+    os.environ["P2_THREADS"] = str(cores)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _oracle as O
+    data = []
+    for i, (K, N) in enumerate(shapes):
+        signs, flags, lo, hi = P.gen_fv_weight(SEED, 900 + i, K, N)
+        A = P.gen_activations(SEED, 950 + i, M, K)
+        data.append((A, signs, flags, lo, hi, N, np.zeros((M, N), np.float32)))
+    for d in data:   # warm-up: builds the pool and touches the buffers
+        O.ref_sgemm_fvb(d[0], *d[1:5], d[5], 1.0, 0.0, d[6])
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for d in data:
+            O.ref_sgemm_fvb(d[0], *d[1:5], d[5], 1.0, 0.0, d[6])
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    ops = sum(gemm_ops(M, N, K) for K, N in shapes)
+    return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": cores, "kind": "reference",
+            "sample": f"{reps} passes of the same GEMMs (M={M}, " + ", ".join(f"{K}->{N}" for K, N in shapes)
+            + ") through the reference's p2_sgemm_fvb, exact fp32 AVX2 route (the only one x86 compiles), "
+            f"P2_THREADS={cores}; {dt * 1e3:.2f} ms per pass"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="ffn375", choices=["ffn375", "m6000", "m38", "sweep", "exact375"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: the five-value GEMM path has no multi-GPU form in this build "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    dev = P.init()
+    stream = P.Stream()
+    print(f"# device {dev}, {P.device_cu_count()} CUs", file=sys.stderr, flush=True)
+
+    results = {}
+
+    def run(name, spec, steps, warmup, kreps):
+        lins, ms, wall, qt, gt = measure_chain(spec, stream, steps, warmup, kreps)
+        r = summarize(lins, ms, qt, gt)
+        r["wall_s"] = round(wall, 3)
+        results[name] = (lins, r)
+        print(f"# {name}: {ms * 1e3:.2f} us/step, {r['tops']:.1f} TOPS", file=sys.stderr, flush=True)
+        return lins, r
+
+    main_wl = args.workload
+    specs = {
+        "ffn375": lambda: ffn_spec(375),
+        "m6000": lambda: ffn_spec(6000, base=3),
+        "m38": lambda: ffn_spec(38, base=5),
+        "sweep": lambda: sweep_spec(375),
+    }
+    if main_wl == "exact375":
+        raise SystemExit("exact375 is reported under extra; pick an int8 workload for the headline")
+    lins, r = run(main_wl, specs[main_wl](), args.steps, args.warmup, 20)
+
+    extra = {}
+    if not args.no_extra:
+        for name in ("m6000", "m38", "sweep"):
+            if name == main_wl:
+                continue
+            steps = {"m6000": 200, "m38": 2000, "sweep": 50}[name]
+            _, rr = run(name, specs[name](), steps, 20, 5 if name == "sweep" else 20)
+            extra[name] = rr
+        extra["sweep_ms_per_30s_window"] = (results["sweep"][1]["ms_per_step"] if "sweep" in results else None)
+        extra["exact375"] = exact_config(stream)
+
+    # dominant kernel of the headline workload: the GEMM with the largest share of the step
+    gt = r["gemm_kernels_ms"]
+    i = int(np.argmax(gt))
+    L = lins[i]
+    alg = gemm_bytes(L.M, L.N, L.K, 1)
+    achieved = alg / (gt[i] * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": f"gemm_i8<int8w> M={L.M} K={L.K} N={L.N}", "algorithmic_bytes": int(alg),
+                "avg_ms": gt[i]}
+
+    ops = sum(gemm_ops(l.M, l.N, l.K) for l in lins)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(lins[0].M, [(l.K, l.N) for l in lins])
+
+    line = {
+        "metric": "five-value int8 GEMM TOPS + % int8 MFMA peak; encoder linears ms per 30 s",
+        "value": round(r["tops"], 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded generator: N(0,1) activations with 0.1% x20 outliers; five-value weights "
+                "P(0)=0.4, P(lo)=0.4, P(hi)=0.2, fp16 lo/hi)",
+        "config": {"workload": {"ffn375": "FFN pair M=375: 1024->4096 then 4096->1024, int8w, fp32 A in HBM",
+                                "m6000": "FFN pair M=6000: 1024->4096 then 4096->1024, int8w",
+                                "m38": "FFN pair M=38: 1024->4096 then 4096->1024, int8w",
+                                "sweep": "216 encoder linears of one 30 s window (M=375, pos M=749), int8w"}[main_wl],
+                   "M": lins[0].M, "gemm_ops_per_step": ops, "graph": True},
+        "pct_int8_peak": round(r["pct_int8_peak"], 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": {"gemm_ms": r["gemm_kernels_ms"], "quant_ms": r["quant_kernels_ms"],
+                    "gemm_gbs": r["gemm_kernel_gbs"], "gemm_tops": r["gemm_kernel_tops"]},
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def exact_config(stream):
+    """Config: one exact-mode five-value GEMM, M=375, K=1024, N=1024 (bench_gemm.c's route)."""
+    M, K, N = 375, 1024, 1024
+    signs, flags, lo, hi = P.gen_fv_weight(SEED, 77, K, N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    dA = P.to_device(P.gen_activations(SEED, 78, M, K))
+    dC = P.DeviceBuffer(M * N * 4)
+    with P.Graph(stream) as g:
+        P.fvb_gemm_dev("exact", M, N, K, 1.0, dA.ptr, K, w, 0.0, dC.ptr, N, None, 0, stream.ptr)
+    ms, _ = time_graph(g, stream, 200, 20)
+    tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 5), "tflops": round(tf, 2), "pct_fp32_peak": round(100 * tf / PEAK_FP32_TFLOPS, 2)}
+
+
+if __name__ == "__main__":
+    main()

@@ -59,6 +59,13 @@ int   p2h_memcpy2d_h2d(void *dst, size_t dpitch, const void *src, size_t spitch,
 int   p2h_memcpy2d_d2h(void *dst, size_t dpitch, const void *src, size_t spitch, size_t row_bytes, size_t rows,
                        void *stream);
 
+/* Stream capture into a HIP graph, for launch-bound chains of these entry points (every kernel entry here is
+ * capturable: none allocates, synchronises or records a memset). end returns an executable graph. */
+int   p2h_capture_begin(void *stream);
+int   p2h_capture_end(void *stream, void **graph_exec);
+int   p2h_graph_launch(void *graph_exec, void *stream);
+int   p2h_graph_destroy(void *graph_exec);
+
 void *p2h_event_create(void);
 int   p2h_event_destroy(void *event);
 int   p2h_event_record(void *event, void *stream);
@@ -101,14 +108,23 @@ int p2h_q_ld(int K);   /* the smallest valid ldq for K */
  * blas.c:1296-1370): mode P2H_INT8W or P2H_INT8; beta 0 stores, 1 accumulates, any other value pre-scales C.
  * The int32 sums run over K blocks of 1024 rows and each block is folded into C in fp32 as the reference does. */
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
-                     const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *stream);
+                     const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
+                     size_t workspace_bytes, void *stream);
+/* Bytes of workspace that let p2h_fvb_gemm_q8a split K across workgroups (0 when the call would not split). With
+ * workspace NULL the call runs unsplit. Split K adds the int32 partial sums of one 1024-row block exactly and folds
+ * the blocks in order, so results do not depend on the split. */
+size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K);
+
+/* A workspace must be zero-filled once before its first use (its tile counters start at zero and every call leaves
+ * them at zero). A kernel, not a memset, so it may be captured. Calls sharing a workspace must be stream-ordered. */
+int p2h_workspace_init(void *workspace, size_t bytes, void *stream);
 
 /* C = alpha · A · W + beta · C on fp32 A (p2_sgemm_fvb, blas.c:1481-1499): the int8 modes quantise A into the
  * workspace and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output
  * fmaf chain over k = 0..K-1 is the reference's exact kernel (blas.c:155-186, 929-987). */
 int    p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
                     float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream);
-size_t p2h_fvb_workspace_bytes(int mode, int M, int K);
+size_t p2h_fvb_workspace_bytes(int mode, int M, int N, int K);
 
 /* The raw int32 accumulators sum_k q[m][k]·B[k][n] over all K of the int8 kernel (blas.c:1256-1282): for
  * P2H_INT8W B is the codes plane into dAcc; for P2H_INT8 the S plane into dAcc and the T plane into dAcc2. */

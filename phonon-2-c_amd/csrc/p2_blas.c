@@ -291,16 +291,17 @@ static void finish_c(Ctx *c, float *C, const float *dC, int M, int N, int ldc, c
     check(p2h_stream_sync(c->stream), who);
 }
 
-static void *workspace(Ctx *c, int M, int K, size_t *bytes, const char *who)
+static void *workspace(Ctx *c, int mode, int M, int N, int K, size_t *bytes, const char *who)
 {
-    size_t need = p2h_fvb_workspace_bytes(P2H_INT8W, M, K);
+    size_t need = p2h_fvb_workspace_bytes(mode, M, N, K);
     *bytes = need;
     if (need == 0) return NULL;
-    size_t cap0 = c->capW;
-    void *w = dgrow(&c->dW, &c->capW, need, who);
-    (void)cap0;
+    if (need > c->capW || !c->dW) {
+        dgrow(&c->dW, &c->capW, need, who);
+        check(p2h_workspace_init(c->dW, c->capW, c->stream), who);   /* split counters start at zero */
+    }
     *bytes = c->capW;
-    return w;
+    return c->dW;
 }
 
 /* C = beta · C for alpha == 0 (blas.c:1434-1435, 1488 and 748-749). */
@@ -327,7 +328,7 @@ void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, con
     float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
-    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, M, K, &wsb, who) : NULL;
+    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, mode, M, N, K, &wsb, who) : NULL;
     check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, w, beta, dC, N, ws, wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
 }
@@ -377,7 +378,7 @@ void p2_sgemm_fvb_q8a(int M, int N, int K, float alpha, const QuantA *A, const F
     float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
-    void *ws = workspace(c, M, K, &wsb, who);
+    void *ws = workspace(c, mode, M, N, K, &wsb, who);
     check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, w, beta, dC, N, ws, wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
 }
@@ -421,7 +422,7 @@ void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, con
     float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
-    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, M, K, &wsb, who) : NULL;
+    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, P2H_INT8W, M, N, K, &wsb, who) : NULL;
     check(p2h_q8b_gemm(mode, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws, wsb,
                        c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
@@ -440,7 +441,7 @@ void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const s
     float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
-    void *ws = workspace(c, M, K, &wsb, who);
+    void *ws = workspace(c, P2H_INT8W, M, N, K, &wsb, who);
     check(p2h_q8b_gemm(P2H_INT8W, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws,
                        wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);

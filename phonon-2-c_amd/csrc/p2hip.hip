@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
 #include <mutex>
 
 #include "p2hip_kernels.h"
@@ -236,6 +237,41 @@ int p2h_memcpy2d_d2h(void *dst, size_t dpitch, const void *src, size_t spitch, s
     return P2H_OK;
 }
 
+int p2h_capture_begin(void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (!stream) return fail(P2H_E_ARG, "p2h_capture_begin: capture needs an explicit stream");
+    HIPCHK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return P2H_OK;
+}
+
+int p2h_capture_end(void *stream, void **graph_exec)
+{
+    if (!stream || !graph_exec) return fail(P2H_E_ARG, "p2h_capture_end: NULL argument");
+    hipGraph_t graph = nullptr;
+    HIPCHK(hipStreamEndCapture((hipStream_t)stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(P2H_E_DEVICE, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    *graph_exec = exec;
+    return P2H_OK;
+}
+
+int p2h_graph_launch(void *graph_exec, void *stream)
+{
+    if (!graph_exec) return fail(P2H_E_ARG, "p2h_graph_launch: NULL graph");
+    HIPCHK(hipGraphLaunch((hipGraphExec_t)graph_exec, stream_of(stream)));
+    return P2H_OK;
+}
+
+int p2h_graph_destroy(void *graph_exec)
+{
+    if (!graph_exec) return P2H_OK;
+    HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return P2H_OK;
+}
+
 void *p2h_event_create(void)
 {
     if (ensure_init()) return nullptr;
@@ -446,8 +482,67 @@ static int check_q(const char *who, int M, int K, const signed char *dQ, int ldq
     return P2H_OK;
 }
 
-static p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const signed char *dQ, int ldq,
-                               const float *dScales, float *dC, int ldc)
+/* ── the int8 GEMM: plan and launch ──────────────────────────────────────────────────────────────────────────── */
+
+}  // extern "C"
+
+namespace {
+
+using G64 = p2k::Geo<64, 64, 2, 2>;
+using G128 = p2k::Geo<128, 128, 2, 2>;
+using G256x128 = p2k::Geo<256, 128, 2, 2>;   /* 256 activation rows × 128 weight columns */
+using G128x256 = p2k::Geo<128, 256, 2, 2>;
+
+enum { CFG_64 = 0, CFG_128 = 1, CFG_256x128 = 2, CFG_128x256 = 3, CFG_COUNT = 4 };
+const int kCfgBM[CFG_COUNT] = {64, 128, 256, 128};
+const int kCfgBN[CFG_COUNT] = {64, 128, 128, 256};
+
+struct Plan {
+    int cfg, splits, split_rows, tiles_m, tiles_n;
+    size_t part_bytes, sem_bytes;
+};
+
+int env_int(const char *name, int dflt)
+{
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+/* Tile and K split for one call. Splits divide a 1024-row fold block (so each lies in one block) and only run when
+ * the output tiles alone leave the CUs short of work; P2H_TILE and P2H_SPLIT_ROWS override the choice (tuning). */
+Plan make_plan(int mode, int M, int N, int K, bool can_split)
+{
+    Plan p;
+    int cfg = M <= 64 ? CFG_64 : CFG_128;
+    if (mode != P2H_INT8W && cfg > CFG_128) cfg = CFG_128;
+    cfg = env_int("P2H_TILE", cfg);
+    if (cfg < 0 || cfg >= CFG_COUNT || (mode != P2H_INT8W && cfg > CFG_128)) cfg = CFG_128;
+    p.cfg = cfg;
+    p.tiles_m = (M + kCfgBM[cfg] - 1) / kCfgBM[cfg];
+    p.tiles_n = (N + kCfgBN[cfg] - 1) / kCfgBN[cfg];
+    const int tiles = p.tiles_m * p.tiles_n;
+    int rows = K > p2k::kFoldRows ? p2k::kFoldRows : (int)align_up((size_t)K, p2k::BK);
+    if (can_split) {
+        const int want = 2 * (g_cus > 0 ? g_cus : 256);
+        while (rows > p2k::BK && (long)tiles * ((K + rows - 1) / rows) < want) rows /= 2;
+    }
+    int forced = env_int("P2H_SPLIT_ROWS", 0);
+    if (can_split && forced >= p2k::BK && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
+    p.split_rows = rows;
+    p.splits = (K + rows - 1) / rows;
+    const bool split = p.splits > 1 && K > 0;
+    if (!split) {   /* one split: K blocks fold in registers */
+        p.splits = 1;
+        p.split_rows = K > 0 ? K : 1;
+    }
+    const size_t planes = mode == P2H_INT8 ? 2 : 1;
+    p.part_bytes = split ? align_up(planes * p.splits * (size_t)M * N * 4, 256) : 0;
+    p.sem_bytes = split ? align_up((size_t)tiles * 4, 256) : 0;
+    return p;
+}
+
+p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const signed char *dQ, int ldq,
+                        const float *dScales, float *dC, int ldc, const Plan &p, void *split_ws)
 {
     p2k::GemmArgs g;
     memset(&g, 0, sizeof g);
@@ -456,18 +551,72 @@ static p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, con
     g.Q = (const int8_t *)dQ; g.ldq = ldq; g.a_scales = dScales;
     g.C = dC; g.ldc = ldc;
     g.c_vec4 = dC && (ldc % 4 == 0) && aligned(dC, 16);
-    g.tiles_n = (N + p2k::BN - 1) / p2k::BN;
+    g.tiles_n = p.tiles_n; g.tiles_m = p.tiles_m;
+    g.splits = p.splits; g.split_rows = p.split_rows;
+    if (p.splits > 1) {
+        g.part = (int32_t *)split_ws;
+        g.sem = (unsigned *)((char *)split_ws + p.part_bytes);
+    }
     return g;
 }
 
-static dim3 gemm_grid(int M, int N)
+template <class G, int MODE>
+void launch_f32(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
-    size_t tn = (N + p2k::BN - 1) / p2k::BN, tm = (M + p2k::BM - 1) / p2k::BM;
-    return dim3((unsigned)(tn * tm));
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n * p.splits)), block(G::NT);
+    if (p.splits > 1)
+        hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, false, true>), grid, block, 0, s, g);
+    else if (g.K > p2k::kFoldRows)
+        hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, true, false>), grid, block, 0, s, g);
+    else
+        hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, false, false>), grid, block, 0, s, g);
+}
+
+template <int MODE>
+void launch_f32_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
+{
+    switch (p.cfg) {
+    case CFG_64: launch_f32<G64, MODE>(g, p, s); break;
+    case CFG_256x128: if (MODE == p2k::MODE_INT8W) launch_f32<G256x128, p2k::MODE_INT8W>(g, p, s); break;
+    case CFG_128x256: if (MODE == p2k::MODE_INT8W) launch_f32<G128x256, p2k::MODE_INT8W>(g, p, s); break;
+    default: launch_f32<G128, MODE>(g, p, s); break;
+    }
+}
+
+int check_split_ws(const char *who, const Plan &p, void *ws, size_t ws_bytes)
+{
+    if (p.splits <= 1) return P2H_OK;
+    if (!ws || ws_bytes < p.part_bytes + p.sem_bytes || !aligned(ws, 256))
+        return fail(P2H_E_WORKSPACE, "%s: split workspace of %zu bytes needed", who, p.part_bytes + p.sem_bytes);
+    return P2H_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int p2h_workspace_init(void *workspace, size_t bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (!workspace || bytes == 0) return P2H_OK;
+    if (!aligned(workspace, 4)) return fail(P2H_E_ARG, "p2h_workspace_init: workspace must be 4-byte aligned");
+    size_t words = bytes / 4;
+    hipLaunchKernelGGL(p2k::fill_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream_of(stream),
+                       (uint32_t *)workspace, words, 0u);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K)
+{
+    if (ensure_init() || M <= 0 || N <= 0 || K <= 0 || (mode != P2H_INT8W && mode != P2H_INT8)) return 0;
+    Plan p = make_plan(mode, M, N, K, true);
+    return p.part_bytes + p.sem_bytes;
 }
 
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
-                     const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *stream)
+                     const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
+                     size_t workspace_bytes, void *stream)
 {
     if (int rc = ensure_init()) return rc;
     if (mode != P2H_INT8W && mode != P2H_INT8)
@@ -481,21 +630,16 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
     if (M == 0) return P2H_OK;
     if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);            /* blas.c:1434 */
     if (K == 0) return (beta != 0.0f) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;   /* no K block runs */
-    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc);
+    Plan p = make_plan(mode, M, N, K, workspace != nullptr);
+    if (int rc = check_split_ws("p2h_fvb_gemm_q8a", p, workspace, workspace_bytes)) return rc;
+    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
     g.signs = w->signs; g.flags = w->flags; g.clo = w->clo;
-    const bool multi = K > p2k::kFoldRows;
     if (mode == P2H_INT8W) {
         g.c1 = w->c1w;
-        if (multi)
-            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8W, p2k::OUT_F32, true>), gemm_grid(M, N), dim3(256), 0, s, g);
-        else
-            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8W, p2k::OUT_F32, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+        launch_f32_cfg<p2k::MODE_INT8W>(g, p, s);
     } else {
         g.c1 = w->lo; g.c2 = w->c2;
-        if (multi)
-            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8, p2k::OUT_F32, true>), gemm_grid(M, N), dim3(256), 0, s, g);
-        else
-            hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8, p2k::OUT_F32, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+        launch_f32_cfg<p2k::MODE_INT8>(g, p, s);
     }
     HIPCHK(hipGetLastError());
     return P2H_OK;
@@ -513,14 +657,19 @@ int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ld
                   (mode == P2H_INT8 && (!dAcc2 || !aligned(dAcc2, 16)))))
         return fail(P2H_E_ARG, "p2h_fvb_acc_i32: accumulators must be 16-byte aligned with ldacc %% 4 == 0");
     if (M == 0) return P2H_OK;
-    p2k::GemmArgs g = gemm_args(M, N, K, 1.0f, 0.0f, dQ, ldq, nullptr, nullptr, 0);
+    Plan p = make_plan(mode, M, N, K, false);
+    p.cfg = CFG_128;
+    p.tiles_m = (M + 127) / 128;
+    p.tiles_n = (N + 127) / 128;
+    p2k::GemmArgs g = gemm_args(M, N, K, 1.0f, 0.0f, dQ, ldq, nullptr, nullptr, 0, p, nullptr);
     g.signs = w->signs; g.flags = w->flags; g.clo = w->clo;
     g.acc1 = dAcc; g.acc2 = dAcc2; g.ldacc = ldacc;
     hipStream_t s = stream_of(stream);
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G128::NT);
     if (mode == P2H_INT8W)
-        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8W, p2k::OUT_ACC, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_INT8W, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
     else
-        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_INT8, p2k::OUT_ACC, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_INT8, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -541,21 +690,27 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
     return P2H_OK;
 }
 
-size_t p2h_fvb_workspace_bytes(int mode, int M, int K)
+static size_t quant_area(int M, int K) { return align_up((size_t)M * p2h_q_ld(K), 256) + align_up((size_t)M * 4, 256); }
+
+size_t p2h_fvb_workspace_bytes(int mode, int M, int N, int K)
 {
     if (mode == P2H_EXACT || M <= 0 || K <= 0 || K % 4 != 0) return 0;
-    return align_up((size_t)M * p2h_q_ld(K), 256) + align_up((size_t)M * 4, 256);
+    return quant_area(M, K) + p2h_fvb_q8a_workspace_bytes(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K);
 }
 
-static int quant_into_workspace(const char *who, int M, int K, const float *dA, int lda, void *workspace,
-                                size_t workspace_bytes, signed char **dQ, float **dS, hipStream_t s)
+static int quant_into_workspace(const char *who, int M, int N, int K, const float *dA, int lda, void *workspace,
+                                size_t workspace_bytes, signed char **dQ, float **dS, void **rest,
+                                size_t *rest_bytes, hipStream_t s)
 {
-    size_t need = p2h_fvb_workspace_bytes(P2H_INT8W, M, K);
+    size_t need = quant_area(M, K);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
         return fail(P2H_E_WORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", who, need,
                     workspace_bytes);
+    (void)N;
     *dQ = (signed char *)workspace;
     *dS = (float *)((char *)workspace + align_up((size_t)M * p2h_q_ld(K), 256));
+    *rest = workspace_bytes > need ? (char *)workspace + need : nullptr;
+    *rest_bytes = workspace_bytes > need ? workspace_bytes - need : 0;
     return p2h_quant_rows(M, K, dA, lda, *dQ, p2h_q_ld(K), *dS, s);
 }
 
@@ -581,9 +736,14 @@ int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
         if (K == 0) return P2H_OK;
         signed char *dQ;
         float *dS;
-        if (int rc = quant_into_workspace("p2h_fvb_gemm", M, K, dA, lda, workspace, workspace_bytes, &dQ, &dS, s))
+        void *rest;
+        size_t rest_bytes;
+        if (int rc = quant_into_workspace("p2h_fvb_gemm", M, N, K, dA, lda, workspace, workspace_bytes, &dQ, &dS,
+                                          &rest, &rest_bytes, s))
             return rc;
-        return p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, p2h_q_ld(K), dS, w, beta, dC, ldc, s);
+        Plan p = make_plan(mode, M, N, K, true);
+        if (rest_bytes < p.part_bytes + p.sem_bytes) rest = nullptr;   /* too small for the split: run without */
+        return p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, p2h_q_ld(K), dS, w, beta, dC, ldc, rest, rest_bytes, s);
     }
     p2k::ExactArgs g;
     memset(&g, 0, sizeof g);
@@ -608,12 +768,10 @@ int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, in
     if (M == 0 || N == 0) return P2H_OK;
     if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);
     if (K == 0) return (beta != 0.0f) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;
-    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc);
+    Plan p = make_plan(P2H_INT8, M, N, K, false);
+    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, nullptr);
     g.B8 = (const int8_t *)dB; g.ldb = ldb; g.c1 = dBscales;
-    if (K > p2k::kFoldRows)
-        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_Q8B, p2k::OUT_F32, true>), gemm_grid(M, N), dim3(256), 0, s, g);
-    else
-        hipLaunchKernelGGL((p2k::gemm_i8<p2k::MODE_Q8B, p2k::OUT_F32, false>), gemm_grid(M, N), dim3(256), 0, s, g);
+    launch_f32_cfg<p2k::MODE_Q8B>(g, p, s);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -640,7 +798,10 @@ int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
         if (K == 0) return P2H_OK;
         signed char *dQ;
         float *dS;
-        if (int rc = quant_into_workspace("p2h_q8b_gemm", M, K, dA, lda, workspace, workspace_bytes, &dQ, &dS, s))
+        void *rest;
+        size_t rest_bytes;
+        if (int rc = quant_into_workspace("p2h_q8b_gemm", M, N, K, dA, lda, workspace, workspace_bytes, &dQ, &dS,
+                                          &rest, &rest_bytes, s))
             return rc;
         return p2h_q8b_gemm_q8a(M, N, K, alpha, dQ, p2h_q_ld(K), dS, dB, ldb, dBscales, beta, dC, ldc, s);
     }

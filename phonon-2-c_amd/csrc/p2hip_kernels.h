@@ -113,16 +113,34 @@ struct GemmArgs {
     const int8_t *B8; int ldb;                            /* int8 table [K][ldb] (MODE_Q8B) */
     float *C; int ldc; int c_vec4;                        /* fp32 output; c_vec4: ldc % 4 == 0 and C 16-B aligned */
     int32_t *acc1; int32_t *acc2; int ldacc;              /* OUT_ACC: raw sums */
-    int tiles_n;                                          /* column tiles of the grid */
+    int tiles_n, tiles_m;                                 /* output tiles of the grid */
+    int splits, split_rows;                               /* K splits; rows per split (divides 1024) */
+    int32_t *part;                                        /* split partials [planes][splits][M][N] */
+    unsigned *sem;                                        /* per-tile arrival counters, zero between calls */
 };
 
-/* Tile geometry. Weight columns n play the MFMA "row" role and activation rows m the "column" role, so each lane's
- * four accumulators are four consecutive n of one output row (a 16-byte store). */
-constexpr int BN = 128;          /* weight columns per workgroup */
-constexpr int BM = 128;          /* activation rows per workgroup */
 constexpr int BK = 128;          /* K rows per LDS stage */
 constexpr int SB = BK + 16;      /* LDS row pitch in bytes: 9 × 16 B, so 8 consecutive rows hit 8 bank groups */
-constexpr int TILE_BYTES = 128 * SB;
+
+/* Tile geometry. Weight columns n play the MFMA "row" role and activation rows m the "column" role, so each lane's
+ * four accumulators are four consecutive n of one output row (a 16-byte store). WN × WM waves; each wave owns
+ * FN × FM MFMA tiles of 16 × 16. */
+template <int BM_, int BN_, int WM_, int WN_>
+struct Geo {
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+    static constexpr int NT = 64 * WM * WN;
+    static constexpr int FN = BN / WN / 16, FM = BM / WM / 16;
+    static constexpr int A_CHUNKS = BM * (BK / 16);      /* 16-byte chunks of an activation stage */
+    static constexpr int A_PER = A_CHUNKS / NT;
+    static constexpr int CGS = BN / 16;                   /* 16-column groups */
+    static constexpr int B_UNITS = (BK / 4) * CGS;        /* (4-row quad, column group) units of a weight stage */
+    static constexpr int B_PER = (B_UNITS + NT - 1) / NT;
+    static constexpr int A_BYTES = BM * SB, B_BYTES = BN * SB;
+    static constexpr int LDS_ONE = 2 * A_BYTES + 2 * B_BYTES;   /* single-plane modes */
+    static_assert(A_CHUNKS % NT == 0, "activation chunks must divide among the threads");
+    static_assert(NT % CGS == 0, "a thread's column group must not change between its units");
+    static_assert(FN >= 1 && FM >= 1, "wave tile");
+};
 
 /* byte permute: result byte i = byte sel_i of the 8-byte value {hi:lo}, selectors 0-3 from lo, 4-7 from hi */
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
@@ -152,8 +170,8 @@ __device__ __forceinline__ uint32_t i8w_lo_table(uint32_t clo)
 constexpr uint32_t kI8wHiTable = 0xFE7F0081u;
 constexpr uint32_t kPlaneS = 0x020100FFu;   /* [−1, 0, 1, 2] */
 
-/* Rows k0..k0+3 (rq-th quad of the stage) × columns 16·cg..16·cg+15 of a five-value tile into the code tile(s):
- * column n, rows 4rq..4rq+3 land as one dword at row n, 16-byte chunk (rq/4) ^ (n/16 mod 8), dword rq mod 4. */
+/* Rows 4rq..4rq+3 of a stage × columns 16·cg..16·cg+15 of a five-value tile into the code tile(s): column n,
+ * rows 4rq..4rq+3 land as one dword at LDS row n, 16-byte chunk (rq/4) ^ (n/16 mod 8), dword rq mod 4. */
 template <int MODE>
 __device__ __forceinline__ void store_fv_codes(const uint32_t s[4], const uint32_t f[4], const uint32_t lo_tab[16],
                                                int8_t *tileB, int8_t *tileT, int cg, int rq)
@@ -196,144 +214,167 @@ __device__ __forceinline__ void store_q8_codes(const uint4 r[4], int8_t *tileB, 
     }
 }
 
-/* 256 threads, 4 waves as 2 (n) × 2 (m); each wave owns a 64 n × 64 m block: 4 × 4 MFMA tiles of 16 × 16.
- * Stage loop: global loads of stage t+1 are issued before the MFMAs of stage t and stored to the other LDS buffer
- * after them, one barrier per stage. MULTI (K > 1024) keeps an fp32 running sum per output across the 1024-row
- * folds; with K <= 1024 the single fold stores straight to C. */
-template <int MODE, int OUT, bool MULTI>
-__global__ __launch_bounds__(256, ((MODE == MODE_INT8 || MULTI) ? 1 : 2)) void gemm_i8(GemmArgs g)
+/* Workgroup → (output tile, K split). Workgroups are dealt to the 8 XCDs round-robin; when the count divides by 8
+ * the index is remapped so each XCD runs one contiguous range of logical tiles – the splits of a tile and the
+ * column tiles of a row band share that XCD's L2. */
+__device__ __forceinline__ void tile_of(const GemmArgs &g, int &tile_n, int &tile_m, int &split)
+{
+    const int nb = (int)gridDim.x;
+    int b = (int)blockIdx.x;
+    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
+    split = b % g.splits;
+    const int t = b / g.splits;
+    tile_n = t % g.tiles_n;
+    tile_m = t / g.tiles_n;
+}
+
+/* The int8 five-value GEMM (sgemm_i8_worker, blas.c:1296-1370) for one output tile and one K split.
+ *  Stage loop: branch-free global loads of stage t+1 (addresses clamped in bounds, out-of-range values replaced
+ *  afterwards) are issued before the MFMAs of stage t and written to the other LDS buffer after them.
+ *  Folding the int32 sums into fp32 (blas.c:1355-1366): with one split, per 1024-row block in registers (MULTI keeps
+ *  the running sum when K > 1024); with SPLIT, each workgroup writes its int32 partial sums, and the last of a
+ *  tile's splits to arrive adds them per block (exact in int32) and folds the blocks in order. */
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT>
+__global__ __launch_bounds__(G::NT, ((MODE == MODE_INT8 || MULTI || G::NT > 256 || 2 * G::LDS_ONE > 160 * 1024) ? 1 : 2))
+void gemm_i8(GemmArgs g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
-    __shared__ __attribute__((aligned(16))) int8_t sm[(TWO ? 6 : 4) * TILE_BYTES];
-    /* LDS: activation tiles [2], code tiles [2], and the T-plane code tiles [2] of the two-plane mode */
-    auto smA = [&](int b) { return sm + b * TILE_BYTES; };
-    auto smB = [&](int b) { return sm + (2 + b) * TILE_BYTES; };
-    auto smT = [&](int b) { return sm + ((TWO ? 4 : 2) + b) * TILE_BYTES; };
+    constexpr int FN = G::FN, FM = G::FM;
+    __shared__ __attribute__((aligned(16))) int8_t sm[2 * G::A_BYTES + (TWO ? 4 : 2) * G::B_BYTES];
+    __shared__ int s_last;
+    auto smA = [&](int b) { return sm + b * G::A_BYTES; };
+    auto smB = [&](int b) { return sm + 2 * G::A_BYTES + b * G::B_BYTES; };
+    auto smT = [&](int b) { return sm + 2 * G::A_BYTES + ((TWO ? 2 : 0) + b) * G::B_BYTES; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave & 1, wm = wave >> 1;
-    const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
-    const int n0 = tile_n * BN, m0 = tile_m * BM;
+    const int wn = wave % G::WN, wm = wave / G::WN;
+    int tile_n, tile_m, split;
+    tile_of(g, tile_n, tile_m, split);
+    const int n0 = tile_n * G::BN, m0 = tile_m * G::BM;
     const int M = g.M, N = g.N, K = g.K;
-    const int nk = (K + BK - 1) / BK;
+    const int k_begin = split * g.split_rows;
+    const int k_end = min(K, k_begin + g.split_rows);
+    const int nk = (k_end - k_begin + BK - 1) / BK;
 
-    /* producer roles */
-    const int cg = tid & 7, rq = tid >> 3;          /* B: 16-column group, 4-row quad */
+    /* B producer: column group cg (fixed), quads rq0 + i·(NT/CGS) */
+    const int cg = tid % G::CGS, rq0 = tid / G::CGS;
     const bool col_ok = n0 + 16 * cg < N;
-    const int a_chunk = tid & 7, a_row = tid >> 3;  /* A: 16-byte chunk, rows a_row + 32 i */
+    const int cgc = col_ok ? cg : 0;   /* clamped column group for addressing */
 
     uint32_t lo_tab[16];
     if (MODE == MODE_INT8W) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) lo_tab[j] = col_ok ? i8w_lo_table(g.clo[n0 + 16 * cg + j]) : 0u;
+        for (int j = 0; j < 16; j++) lo_tab[j] = i8w_lo_table(g.clo[n0 + 16 * cgc + j]);
     }
 
-    uint4 ra[4];
-    uint32_t rs[4], rf[4];
-    uint4 rb[4];
+    uint4 ra[G::A_PER];
+    uint32_t rs[G::B_PER][4], rf[G::B_PER][4];
+    uint4 rb[G::B_PER][4];
 
     auto load_stage = [&](int t) {
-        const int k0 = t * BK;
+        const int k0 = k_begin + t * BK;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = m0 + a_row + 32 * i;
-            ra[i] = m < M ? *reinterpret_cast<const uint4 *>(g.Q + (size_t)m * g.ldq + k0 + 16 * a_chunk)
-                          : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < G::A_PER; i++) {
+            const int c = tid + i * G::NT;
+            const int m = m0 + c / (BK / 16);
+            const int mc = min(m, M - 1);
+            uint4 v = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + k0 + 16 * (c % (BK / 16)));
+            ra[i] = m < M ? v : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int k = k0 + 4 * rq + r;
-            const bool ok = col_ok && k < K;
-            if (MODE == MODE_Q8B) {
-                rb[r] = ok ? *reinterpret_cast<const uint4 *>(g.B8 + (size_t)k * g.ldb + n0 + 16 * cg)
-                           : make_uint4(0, 0, 0, 0);
-            } else {
-                rs[r] = ok ? *reinterpret_cast<const uint32_t *>(g.signs + (size_t)k * (N / 4) + n0 / 4 + 4 * cg)
-                           : 0x55555555u;   /* code 1 everywhere: zero weights */
-                rf[r] = ok ? *reinterpret_cast<const uint16_t *>(g.flags + (size_t)k * (N / 8) + n0 / 8 + 2 * cg)
-                           : 0u;
+        for (int u = 0; u < G::B_PER; u++) {
+            const int rq = rq0 + u * (G::NT / G::CGS);
+            if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int k = k0 + 4 * rq + r;
+                const bool ok = col_ok && k < k_end;
+                const int kc = min(k, K - 1);
+                if (MODE == MODE_Q8B) {
+                    uint4 v = *reinterpret_cast<const uint4 *>(g.B8 + (size_t)kc * g.ldb + n0 + 16 * cgc);
+                    rb[u][r] = ok ? v : make_uint4(0, 0, 0, 0);
+                } else {
+                    uint32_t sv = *reinterpret_cast<const uint32_t *>(g.signs + (size_t)kc * (N / 4) + n0 / 4 + 4 * cgc);
+                    uint32_t fv = *reinterpret_cast<const uint16_t *>(g.flags + (size_t)kc * (N / 8) + n0 / 8 + 2 * cgc);
+                    rs[u][r] = ok ? sv : 0x55555555u;   /* code 1 everywhere: zero weights */
+                    rf[u][r] = ok ? fv : 0u;
+                }
             }
         }
     };
     auto store_stage = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            *reinterpret_cast<uint4 *>(smA(buf) + (a_row + 32 * i) * SB + 16 * a_chunk) = ra[i];
-        if (MODE == MODE_Q8B) store_q8_codes(rb, smB(buf), cg, rq);
-        else store_fv_codes<MODE>(rs, rf, lo_tab, smB(buf), smT(buf), cg, rq);
+        for (int i = 0; i < G::A_PER; i++) {
+            const int c = tid + i * G::NT;
+            *reinterpret_cast<uint4 *>(smA(buf) + (c / (BK / 16)) * SB + 16 * (c % (BK / 16))) = ra[i];
+        }
+#pragma unroll
+        for (int u = 0; u < G::B_PER; u++) {
+            const int rq = rq0 + u * (G::NT / G::CGS);
+            if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
+            if (MODE == MODE_Q8B) store_q8_codes(rb[u], smB(buf), cg, rq);
+            else store_fv_codes<MODE>(rs[u], rf[u], lo_tab, smB(buf), smT(buf), cg, rq);
+        }
     };
 
-    v4i acc[4][4], accT[4][4];
-    float run[MULTI ? 4 : 1][MULTI ? 4 : 1][4];
+    v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
+    float run[MULTI ? FN : 1][MULTI ? FM : 1][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < FN; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < FM; j++) {
             acc[i][j] = v4i{0, 0, 0, 0};
-            if (TWO) accT[i][j] = v4i{0, 0, 0, 0};
+            if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
         }
 
     /* epilogue geometry of this lane: outputs (m_lane + 16 j, n_lane + 16 i + r) */
-    const int n_lane = n0 + wn * 64 + 4 * (lane >> 4);
-    const int m_lane = m0 + wm * 64 + (lane & 15);
+    const int n_lane = n0 + wn * (G::BN / G::WN) + 4 * (lane >> 4);
+    const int m_lane = m0 + wm * (G::BM / G::WM) + (lane & 15);
     const bool beta_zero = g.beta == 0.0f;
 
-    /* Fold the int32 sums of one K block into the fp32 result (blas.c:1355-1366): f = (float)acc · c1
-     * (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta == 0) or fmaf(f, as, beta-scaled C), later blocks
-     * fmaf(f, as, running). The last fold stores C. */
-    auto fold = [&](int block, bool last) {
+    /* One fold of a K block: f = (float)accS · c1 (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta 0)
+     * or fmaf(f, as, beta-scaled C); later blocks fmaf(f, as, running). `last` stores C. */
+    auto fold_one = [&](int block, bool last, int i, int j, const v4i &a1, const v4i &a2, float runv[4]) {
+        const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+        const bool ok = n < N && m < M;
+        const int nc = min(n, N - 4), mc = min(m, M - 1);
+        float c1v[4], c2v[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int n = n_lane + 16 * i;
-            const bool n_ok = n < N;
-            float c1v[4] = {0, 0, 0, 0}, c2v[4] = {0, 0, 0, 0};
-            if (n_ok) {
+        for (int r = 0; r < 4; r++) {
+            c1v[r] = g.c1[nc + r];
+            if (TWO) c2v[r] = g.c2[nc + r];
+        }
+        const float as = g.a_scales[mc] * g.alpha;
+        float *cp = g.C + (size_t)m * g.ldc + n;
+        float cold[4] = {0, 0, 0, 0};
+        if (block == 0 && !beta_zero && ok) {
+            if (g.c_vec4) {
+                float4 v = *reinterpret_cast<const float4 *>(cp);
+                cold[0] = v.x; cold[1] = v.y; cold[2] = v.z; cold[3] = v.w;
+            } else {
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    c1v[r] = g.c1[n + r];
-                    if (TWO) c2v[r] = g.c2[n + r];
-                }
+                for (int r = 0; r < 4; r++) cold[r] = cp[r];
             }
+            if (g.beta != 1.0f) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int m = m_lane + 16 * j;
-                const bool ok = n_ok && m < M;
-                const float as = m < M ? g.a_scales[m] * g.alpha : 0.0f;
-                float *cp = g.C + (size_t)m * g.ldc + n;
-                float cold[4] = {0, 0, 0, 0};
-                if (block == 0 && !beta_zero && ok) {
-                    if (g.c_vec4) {
-                        float4 v = *reinterpret_cast<const float4 *>(cp);
-                        cold[0] = v.x; cold[1] = v.y; cold[2] = v.z; cold[3] = v.w;
-                    } else {
+                for (int r = 0; r < 4; r++) cold[r] = cold[r] * g.beta;
+            }
+        }
+        float out[4];
 #pragma unroll
-                        for (int r = 0; r < 4; r++) cold[r] = cp[r];
-                    }
-                    if (g.beta != 1.0f) {
+        for (int r = 0; r < 4; r++) {
+            float f = (float)a1[r] * c1v[r];
+            if (TWO) f = __builtin_fmaf((float)a2[r], c2v[r], f);
+            const float prev = block == 0 ? cold[r] : runv[r];
+            out[r] = (block == 0 && beta_zero) ? f * as : __builtin_fmaf(f, as, prev);
+            runv[r] = out[r];
+        }
+        if (last && ok) {
+            if (g.c_vec4) {
+                *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
+            } else {
 #pragma unroll
-                        for (int r = 0; r < 4; r++) cold[r] = cold[r] * g.beta;
-                    }
-                }
-                float out[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    float f = (float)acc[i][j][r] * c1v[r];
-                    if (TWO) f = __builtin_fmaf((float)accT[i][j][r], c2v[r], f);
-                    float prev = cold[r];
-                    if (MULTI && block > 0) prev = run[MULTI ? i : 0][MULTI ? j : 0][r];
-                    out[r] = (block == 0 && beta_zero) ? f * as : __builtin_fmaf(f, as, prev);
-                    if (MULTI) run[MULTI ? i : 0][MULTI ? j : 0][r] = out[r];
-                }
-                acc[i][j] = v4i{0, 0, 0, 0};
-                if (TWO) accT[i][j] = v4i{0, 0, 0, 0};
-                if (last && ok) {
-                    if (g.c_vec4) {
-                        *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) cp[r] = out[r];
-                    }
-                }
+                for (int r = 0; r < 4; r++) cp[r] = out[r];
             }
         }
     };
@@ -352,34 +393,44 @@ __global__ __launch_bounds__(256, ((MODE == MODE_INT8 || MULTI) ? 1 : 2)) void g
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 64) {
             const int g16 = (kk >> 4) + (lane >> 4);   /* this lane's 16-byte chunk along k */
-            v4i a[4], b[4], bt[4];
+            v4i a[FN], b[FM], bt[TWO ? FN : 1];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int nl = wn * 64 + 16 * i + (lane & 15);
+            for (int i = 0; i < FN; i++) {
+                const int nl = wn * (G::BN / G::WN) + 16 * i + (lane & 15);
                 const int off = nl * SB + 16 * (g16 ^ ((nl >> 4) & 7));
                 a[i] = *reinterpret_cast<const v4i *>(tB + off);
-                if (TWO) bt[i] = *reinterpret_cast<const v4i *>(tT + off);
+                if (TWO) bt[TWO ? i : 0] = *reinterpret_cast<const v4i *>(tT + off);
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int ml = wm * 64 + 16 * j + (lane & 15);
+            for (int j = 0; j < FM; j++) {
+                const int ml = wm * (G::BM / G::WM) + 16 * j + (lane & 15);
                 b[j] = *reinterpret_cast<const v4i *>(tA + ml * SB + 16 * g16);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < FN; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
+                for (int j = 0; j < FM; j++) {
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-                    if (TWO) accT[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bt[i], b[j], accT[i][j], 0, 0, 0);
+                    if (TWO)
+                        accT[TWO ? i : 0][TWO ? j : 0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            bt[TWO ? i : 0], b[j], accT[TWO ? i : 0][TWO ? j : 0], 0, 0, 0);
                 }
         }
         if (t + 1 < nk) store_stage(buf ^ 1);
-        if (OUT == OUT_F32) {
+        if (OUT == OUT_F32 && !SPLIT) {
             const bool last = t + 1 == nk;
-            if (MULTI) {
-                if (((t + 1) * BK) % kFoldRows == 0 || last) fold(block++, last);
-            } else if (last) {
-                fold(0, true);
+            if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
+#pragma unroll
+                for (int i = 0; i < FN; i++)
+#pragma unroll
+                    for (int j = 0; j < FM; j++) {
+                        float tmp[4];
+                        float *rv = MULTI ? run[MULTI ? i : 0][MULTI ? j : 0] : tmp;
+                        fold_one(block, last, i, j, acc[i][j], TWO ? accT[TWO ? i : 0][TWO ? j : 0] : acc[i][j], rv);
+                        acc[i][j] = v4i{0, 0, 0, 0};
+                        if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+                    }
+                block++;
             }
         }
         __syncthreads();
@@ -387,15 +438,58 @@ __global__ __launch_bounds__(256, ((MODE == MODE_INT8 || MULTI) ? 1 : 2)) void g
 
     if (OUT == OUT_ACC) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < FN; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < FM; j++) {
                 const int n = n_lane + 16 * i, m = m_lane + 16 * j;
                 if (m < M && n < N) {
                     *reinterpret_cast<v4i *>(g.acc1 + (size_t)m * g.ldacc + n) = acc[i][j];
-                    if (TWO) *reinterpret_cast<v4i *>(g.acc2 + (size_t)m * g.ldacc + n) = accT[i][j];
+                    if (TWO) *reinterpret_cast<v4i *>(g.acc2 + (size_t)m * g.ldacc + n) = accT[TWO ? i : 0][TWO ? j : 0];
                 }
             }
+        return;
+    }
+
+    if (SPLIT) {
+        const size_t plane = (size_t)g.splits * M * N;
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                if (m < M && n < N) {
+                    int32_t *p = g.part + ((size_t)split * M + m) * N + n;
+                    *reinterpret_cast<v4i *>(p) = acc[i][j];
+                    if (TWO) *reinterpret_cast<v4i *>(p + plane) = accT[TWO ? i : 0][TWO ? j : 0];
+                }
+            }
+        __threadfence();
+        __syncthreads();
+        const int tile = tile_m * g.tiles_n + tile_n;
+        if (tid == 0) s_last = atomicAdd(g.sem + tile, 1u) == (unsigned)(g.splits - 1);
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();
+        const int per_block = kFoldRows / g.split_rows;
+        const int nblocks = (g.splits + per_block - 1) / per_block;
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
+                float runv[4] = {0, 0, 0, 0};
+                for (int b = 0; b < nblocks; b++) {
+                    v4i s1 = v4i{0, 0, 0, 0}, s2 = v4i{0, 0, 0, 0};
+                    const int s_end = min(g.splits, (b + 1) * per_block);
+                    for (int s = b * per_block; s < s_end; s++) {
+                        const int32_t *p = g.part + ((size_t)s * M + m) * N + n;
+                        s1 += *reinterpret_cast<const v4i *>(p);
+                        if (TWO) s2 += *reinterpret_cast<const v4i *>(p + plane);
+                    }
+                    fold_one(b, b + 1 == nblocks, i, j, s1, s2, runv);
+                }
+            }
+        if (tid == 0) g.sem[tile] = 0u;
     }
 }
 
@@ -578,6 +672,13 @@ __global__ void fv_pack_codes(int K, int N, const uint8_t *__restrict__ signs, c
         word |= ((uint32_t)(s * mag) & 0xFFu) << (8 * i);
     }
     out[idx] = word;
+}
+
+/* Fill with a word value (a kernel rather than a memset node, so it may sit inside a captured graph). */
+__global__ void fill_u32(uint32_t *__restrict__ p, size_t words, uint32_t value)
+{
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < words) p[idx] = value;
 }
 
 __global__ void scale_c(int M, int N, float beta, float *__restrict__ C, int ldc)

@@ -46,6 +46,10 @@ _HIP_SIG = {
     "p2h_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
     "p2h_memcpy2d_h2d": (_i, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
     "p2h_memcpy2d_d2h": (_i, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
+    "p2h_capture_begin": (_i, [_vp]),
+    "p2h_capture_end": (_i, [_vp, C.POINTER(_vp)]),
+    "p2h_graph_launch": (_i, [_vp, _vp]),
+    "p2h_graph_destroy": (_i, [_vp]),
     "p2h_event_create": (_vp, []),
     "p2h_event_destroy": (_i, [_vp]),
     "p2h_event_record": (_i, [_vp, _vp]),
@@ -59,9 +63,11 @@ _HIP_SIG = {
     "p2h_fv_pack_codes": (_i, [_vp, _vp, _vp]),
     "p2h_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_q_ld": (_i, [_i]),
-    "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp]),
+    "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
+    "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "p2h_workspace_init": (_i, [_vp, _sz, _vp]),
     "p2h_fvb_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
-    "p2h_fvb_workspace_bytes": (_sz, [_i, _i, _i]),
+    "p2h_fvb_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_acc_i32": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp]),
     "p2h_scale_c": (_i, [_i, _i, _f, _vp, _i, _vp]),
     "p2h_q8b_gemm_q8a": (_i, [_i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _vp, _f, _vp, _i, _vp]),
@@ -177,6 +183,36 @@ class Stream:
             pass
 
 
+class Graph:
+    """Capture the calls made inside `with Graph(stream) as g:` on `stream`, then g.launch() replays them."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.ptr = None
+
+    def __enter__(self):
+        _ok(hip().p2h_capture_begin(self.stream.ptr), "p2h_capture_begin")
+        return self
+
+    def __exit__(self, et, ev, tb):
+        out = C.c_void_p()
+        rc = hip().p2h_capture_end(self.stream.ptr, C.byref(out))
+        if et is None:
+            _ok(rc, "p2h_capture_end")
+            self.ptr = out.value
+        return False
+
+    def launch(self):
+        _ok(hip().p2h_graph_launch(self.ptr, self.stream.ptr), "p2h_graph_launch")
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                hip().p2h_graph_destroy(self.ptr)
+        except Exception:
+            pass
+
+
 class Event:
     def __init__(self):
         self.ptr = hip().p2h_event_create()
@@ -238,8 +274,22 @@ def q_ld(K):
     return hip().p2h_q_ld(K)
 
 
-def workspace_bytes(mode, M, K):
-    return hip().p2h_fvb_workspace_bytes(MODES.get(mode, mode), M, K)
+def workspace_bytes(mode, M, N, K):
+    """Workspace of p2h_fvb_gemm (fp32 activations): quantised rows plus the split-K area."""
+    return hip().p2h_fvb_workspace_bytes(MODES.get(mode, mode), M, N, K)
+
+
+def q8a_workspace_bytes(mode, M, N, K):
+    return hip().p2h_fvb_q8a_workspace_bytes(MODES.get(mode, mode), M, N, K)
+
+
+class Workspace(DeviceBuffer):
+    """A zero-initialised workspace (its split-K tile counters must start at zero)."""
+
+    def __init__(self, nbytes, stream=None):
+        super().__init__(max(int(nbytes), 256))
+        _ok(hip().p2h_workspace_init(self.ptr, self.nbytes, stream), "p2h_workspace_init")
+        sync(stream)
 
 
 # ── device-pointer entry points (asynchronous on `stream`) ───────────────────────────────────────────────────────
@@ -248,9 +298,9 @@ def quant_rows_dev(M, K, dA, lda, dQ, ldq, dS, stream=None):
     _ok(hip().p2h_quant_rows(M, K, dA, lda, dQ, ldq, dS, stream), "p2h_quant_rows")
 
 
-def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, stream=None):
-    _ok(hip().p2h_fvb_gemm_q8a(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, stream),
-        "p2h_fvb_gemm_q8a")
+def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=None, ws_bytes=0, stream=None):
+    _ok(hip().p2h_fvb_gemm_q8a(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, ws,
+                               ws_bytes, stream), "p2h_fvb_gemm_q8a")
 
 
 def fvb_gemm_dev(mode, M, N, K, alpha, dA, lda, w, beta, dC, ldc, ws, ws_bytes, stream=None):
@@ -284,14 +334,14 @@ def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None):
     ldc = C0.shape[1]
     dA = to_device(A)
     dC = to_device(C0)
-    wsb = workspace_bytes(mode, M, K)
-    ws = DeviceBuffer(max(wsb, 256))
-    fvb_gemm_dev(mode, M, N, K, alpha, dA.ptr, lda, w, beta, dC.ptr, ldc, ws.ptr, max(wsb, 256))
+    ws = Workspace(workspace_bytes(mode, M, N, K))
+    fvb_gemm_dev(mode, M, N, K, alpha, dA.ptr, lda, w, beta, dC.ptr, ldc, ws.ptr, ws.nbytes)
     return dC.download((M, ldc), np.float32)
 
 
-def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None):
-    """p2h_fvb_gemm_q8a on a quantised host matrix q [M, K] (re-padded to the library's ldq)."""
+def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None, split=True):
+    """p2h_fvb_gemm_q8a on a quantised host matrix q [M, K] (re-padded to the library's ldq); split=False runs
+    without a workspace (no K split)."""
     q = np.ascontiguousarray(q, np.int8)
     M, K = q.shape
     N = w.N
@@ -300,7 +350,9 @@ def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None):
     qp[:, :K] = q
     C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
     dQ, dS, dC = to_device(qp), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
-    fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ.ptr, ldq, dS.ptr, w, beta, dC.ptr, C0.shape[1])
+    ws = Workspace(q8a_workspace_bytes(mode, M, N, K)) if split else None
+    fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ.ptr, ldq, dS.ptr, w, beta, dC.ptr, C0.shape[1],
+                     ws.ptr if ws else None, ws.nbytes if ws else 0)
     return dC.download(C0.shape, np.float32)
 
 
@@ -335,10 +387,9 @@ def q8b_gemm(mode, A, B, scales, alpha=1.0, beta=0.0, C0=None):
     N = B.shape[1]
     C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
     dA, dB, dS, dC = to_device(A), to_device(B), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
-    wsb = workspace_bytes(mode, M, K)
-    ws = DeviceBuffer(max(wsb, 256))
+    ws = Workspace(workspace_bytes("int8w", M, N, K))
     _ok(hip().p2h_q8b_gemm(MODES.get(mode, mode), M, N, K, alpha, dA.ptr, K, dB.ptr, N, dS.ptr, beta, dC.ptr,
-                           C0.shape[1], ws.ptr, max(wsb, 256), None), "p2h_q8b_gemm")
+                           C0.shape[1], ws.ptr, ws.nbytes, None), "p2h_q8b_gemm")
     return dC.download(C0.shape, np.float32)
 
 

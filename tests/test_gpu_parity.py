@@ -213,3 +213,43 @@ def test_full_size_sampled_rows(M, K, N):
     # a size-independent property over every row: rows scaled by 2^j give outputs scaled by exactly 2^j
     got2 = P.fvb_gemm("int8w", A * np.float32(4.0), w)
     assert _bits_equal(got2, (got * np.float32(4.0)).astype(np.float32))
+
+
+# ── every tile configuration and K split (the planner's choices forced through its tuning variables) ─────────────
+
+_TILE_CASES = {}
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+@pytest.mark.parametrize("split_rows", [0, 128, 512, 1024])
+@pytest.mark.parametrize("M,K,N", [(375, 4096, 1024), (130, 1028, 272), (38, 1024, 4096), (300, 2048, 512)])
+def test_tiles_and_splits_int8w(monkeypatch, tile, split_rows, M, K, N):
+    monkeypatch.setenv("P2H_TILE", str(tile))
+    monkeypatch.setenv("P2H_SPLIT_ROWS", str(split_rows))
+    key = (M, K, N)
+    if key not in _TILE_CASES:
+        signs, flags, lo, hi = _weight(K, N, 900 + K + N)
+        A = P.gen_activations(SEED, 901 + M, M, K)
+        q, sc = O.quant_rows(A)
+        C0 = P.gen_activations(SEED, 902 + N, M, N)
+        ref = O.gemm_i8_run("int8w", q, sc, signs, flags, lo, hi, N, alpha=0.75, C0=C0, beta_zero=False)
+        _TILE_CASES[key] = (P.FvWeight(signs, flags, lo, hi, K, N), q, sc, C0, ref)
+    w, q, sc, C0, ref = _TILE_CASES[key]
+    for rep in range(2):   # twice: the split counters must be back at zero after each call
+        got = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=0.75, beta=1.0, C0=C0)
+        _assert_fp32(got, ref)
+
+
+@pytest.mark.parametrize("tile", [0, 1])
+@pytest.mark.parametrize("split_rows", [0, 256])
+def test_tiles_and_splits_int8(monkeypatch, tile, split_rows):
+    monkeypatch.setenv("P2H_TILE", str(tile))
+    monkeypatch.setenv("P2H_SPLIT_ROWS", str(split_rows))
+    M, K, N = 200, 2052, 144
+    signs, flags, lo, hi = _weight(K, N, 950)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 951, M, K)
+    q, sc = O.quant_rows(A)
+    ref = O.gemm_i8_run("int8", q, sc, signs, flags, lo, hi, N)
+    _assert_fp32(P.fvb_gemm_q8a("int8", q, sc, w), ref)
+    _assert_fp32(P.fvb_gemm_q8a("int8", q, sc, w, split=False), ref)
