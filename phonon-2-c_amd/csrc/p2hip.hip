@@ -508,36 +508,44 @@ int env_int(const char *name, int dflt)
     return (v && *v) ? atoi(v) : dflt;
 }
 
-/* Tile and K split for one call. Splits divide a 1024-row fold block (so each lies in one block) and only run when
- * the output tiles alone leave the CUs short of work; P2H_TILE and P2H_SPLIT_ROWS override the choice (tuning). */
+/* Split-K counters: a fixed region at the start of the split workspace, so partial sums of one call never land on
+ * the counters of another; splits run only for grids of at most this many tiles. */
+constexpr int kSemSlots = 1024;
+constexpr size_t kSemBytes = kSemSlots * 4;
+
+/* Tile and K split for one call. A split divides a 1024-row fold block (so each lies in one block) and runs only
+ * with a workspace and only when the output tiles alone leave the CUs short of work; P2H_TILE and P2H_SPLIT_ROWS
+ * override the choice (tuning). */
 Plan make_plan(int mode, int M, int N, int K, bool can_split)
 {
     Plan p;
     int cfg = M <= 64 ? CFG_64 : CFG_128;
-    if (mode != P2H_INT8W && cfg > CFG_128) cfg = CFG_128;
     cfg = env_int("P2H_TILE", cfg);
     if (cfg < 0 || cfg >= CFG_COUNT || (mode != P2H_INT8W && cfg > CFG_128)) cfg = CFG_128;
     p.cfg = cfg;
     p.tiles_m = (M + kCfgBM[cfg] - 1) / kCfgBM[cfg];
     p.tiles_n = (N + kCfgBN[cfg] - 1) / kCfgBN[cfg];
     const int tiles = p.tiles_m * p.tiles_n;
-    int rows = K > p2k::kFoldRows ? p2k::kFoldRows : (int)align_up((size_t)K, p2k::BK);
-    if (can_split) {
-        const int want = 2 * (g_cus > 0 ? g_cus : 256);
-        while (rows > p2k::BK && (long)tiles * ((K + rows - 1) / rows) < want) rows /= 2;
-    }
-    int forced = env_int("P2H_SPLIT_ROWS", 0);
-    if (can_split && forced >= p2k::BK && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
-    p.split_rows = rows;
-    p.splits = (K + rows - 1) / rows;
-    const bool split = p.splits > 1 && K > 0;
-    if (!split) {   /* one split: K blocks fold in registers */
-        p.splits = 1;
-        p.split_rows = K > 0 ? K : 1;
+    const int want = 2 * (g_cus > 0 ? g_cus : 256);
+    p.splits = 1;
+    p.split_rows = K > 0 ? K : 1;
+    if (can_split && K > 0 && tiles <= kSemSlots) {
+        int rows = 0;
+        if (tiles < want) {
+            rows = K > p2k::kFoldRows ? p2k::kFoldRows : (int)align_up((size_t)K, p2k::BK);
+            while (rows > p2k::BK && (long)tiles * ((K + rows - 1) / rows) < want) rows /= 2;
+        }
+        const int forced = env_int("P2H_SPLIT_ROWS", 0);
+        if (forced >= p2k::BK && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
+        if (rows > 0 && (K + rows - 1) / rows > 1) {
+            p.split_rows = rows;
+            p.splits = (K + rows - 1) / rows;
+        }
     }
     const size_t planes = mode == P2H_INT8 ? 2 : 1;
+    const bool split = p.splits > 1;
     p.part_bytes = split ? align_up(planes * p.splits * (size_t)M * N * 4, 256) : 0;
-    p.sem_bytes = split ? align_up((size_t)tiles * 4, 256) : 0;
+    p.sem_bytes = split ? kSemBytes : 0;
     return p;
 }
 
@@ -554,8 +562,8 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
     g.tiles_n = p.tiles_n; g.tiles_m = p.tiles_m;
     g.splits = p.splits; g.split_rows = p.split_rows;
     if (p.splits > 1) {
-        g.part = (int32_t *)split_ws;
-        g.sem = (unsigned *)((char *)split_ws + p.part_bytes);
+        g.sem = (unsigned *)split_ws;
+        g.part = (int32_t *)((char *)split_ws + kSemBytes);
     }
     return g;
 }

@@ -339,7 +339,7 @@ def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None):
     return dC.download((M, ldc), np.float32)
 
 
-def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None, split=True):
+def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None, split=True, ws=None):
     """p2h_fvb_gemm_q8a on a quantised host matrix q [M, K] (re-padded to the library's ldq); split=False runs
     without a workspace (no K split)."""
     q = np.ascontiguousarray(q, np.int8)
@@ -350,7 +350,8 @@ def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None, split=True):
     qp[:, :K] = q
     C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
     dQ, dS, dC = to_device(qp), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
-    ws = Workspace(q8a_workspace_bytes(mode, M, N, K)) if split else None
+    if ws is None and split:
+        ws = Workspace(q8a_workspace_bytes(mode, M, N, K))
     fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ.ptr, ldq, dS.ptr, w, beta, dC.ptr, C0.shape[1],
                      ws.ptr if ws else None, ws.nbytes if ws else 0)
     return dC.download(C0.shape, np.float32)

@@ -253,3 +253,18 @@ def test_tiles_and_splits_int8(monkeypatch, tile, split_rows):
     ref = O.gemm_i8_run("int8", q, sc, signs, flags, lo, hi, N)
     _assert_fp32(P.fvb_gemm_q8a("int8", q, sc, w), ref)
     _assert_fp32(P.fvb_gemm_q8a("int8", q, sc, w, split=False), ref)
+
+
+def test_one_workspace_across_shapes():
+    """A workspace reused by calls of different shapes: each call's partial sums must not disturb the split
+    counters another call relies on (they live in a fixed region), and every call leaves them at zero."""
+    shapes = [(38, 4096, 1024), (9, 256, 32), (375, 1024, 1024), (38, 1024, 4096), (9, 256, 32)]
+    need = max(P.q8a_workspace_bytes("int8w", M, N, K) for M, K, N in shapes)
+    ws = P.Workspace(need)
+    for i, (M, K, N) in enumerate(shapes):
+        signs, flags, lo, hi = _weight(K, N, 960 + i)
+        w = P.FvWeight(signs, flags, lo, hi, K, N)
+        A = P.gen_activations(SEED, 970 + i, M, K)
+        q, sc = O.quant_rows(A)
+        ref = O.gemm_i8_run("int8w", q, sc, signs, flags, lo, hi, N)
+        _assert_fp32(P.fvb_gemm_q8a("int8w", q, sc, w, ws=ws), ref)
