@@ -120,7 +120,7 @@ size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K);
 int p2h_workspace_init(void *workspace, size_t bytes, void *stream);
 
 /* C = alpha · A · W + beta · C on fp32 A (p2_sgemm_fvb, blas.c:1481-1499): the int8 modes quantise A into the
- * workspace and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output
+ * workspace (at least p2h_fvb_workspace_bytes, zero-filled once by p2h_workspace_init) and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output
  * fmaf chain over k = 0..K-1 is the reference's exact kernel (blas.c:155-186, 929-987). */
 int    p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
                     float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream);

@@ -619,7 +619,7 @@ size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K)
 {
     if (ensure_init() || M <= 0 || N <= 0 || K <= 0 || (mode != P2H_INT8W && mode != P2H_INT8)) return 0;
     Plan p = make_plan(mode, M, N, K, true);
-    return p.part_bytes + p.sem_bytes;
+    return p.part_bytes + p.sem_bytes;   /* [counters][partials], or 0 when the call would not split */
 }
 
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
@@ -700,25 +700,25 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
 
 static size_t quant_area(int M, int K) { return align_up((size_t)M * p2h_q_ld(K), 256) + align_up((size_t)M * 4, 256); }
 
+/* Workspace of the fp32-input entries: [split counters, kSemBytes][split partials][quantised rows][row scales].
+ * The counters sit at offset 0 whatever the shape, so no call's data ever lands on them. */
 size_t p2h_fvb_workspace_bytes(int mode, int M, int N, int K)
 {
-    if (mode == P2H_EXACT || M <= 0 || K <= 0 || K % 4 != 0) return 0;
-    return quant_area(M, K) + p2h_fvb_q8a_workspace_bytes(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K);
+    if (ensure_init() || mode == P2H_EXACT || M <= 0 || N <= 0 || K <= 0 || K % 4 != 0) return 0;
+    Plan p = make_plan(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K, true);
+    return kSemBytes + p.part_bytes + quant_area(M, K);
 }
 
-static int quant_into_workspace(const char *who, int M, int N, int K, const float *dA, int lda, void *workspace,
-                                size_t workspace_bytes, signed char **dQ, float **dS, void **rest,
-                                size_t *rest_bytes, hipStream_t s)
+static int quant_into_workspace(const char *who, int mode, int M, int N, int K, const float *dA, int lda,
+                                void *workspace, size_t workspace_bytes, signed char **dQ, float **dS,
+                                hipStream_t s)
 {
-    size_t need = quant_area(M, K);
+    size_t need = p2h_fvb_workspace_bytes(mode, M, N, K);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
         return fail(P2H_E_WORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", who, need,
                     workspace_bytes);
-    (void)N;
-    *dQ = (signed char *)workspace;
-    *dS = (float *)((char *)workspace + align_up((size_t)M * p2h_q_ld(K), 256));
-    *rest = workspace_bytes > need ? (char *)workspace + need : nullptr;
-    *rest_bytes = workspace_bytes > need ? workspace_bytes - need : 0;
+    *dQ = (signed char *)workspace + (need - quant_area(M, K));
+    *dS = (float *)((char *)*dQ + align_up((size_t)M * p2h_q_ld(K), 256));
     return p2h_quant_rows(M, K, dA, lda, *dQ, p2h_q_ld(K), *dS, s);
 }
 
@@ -744,14 +744,11 @@ int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
         if (K == 0) return P2H_OK;
         signed char *dQ;
         float *dS;
-        void *rest;
-        size_t rest_bytes;
-        if (int rc = quant_into_workspace("p2h_fvb_gemm", M, N, K, dA, lda, workspace, workspace_bytes, &dQ, &dS,
-                                          &rest, &rest_bytes, s))
+        if (int rc = quant_into_workspace("p2h_fvb_gemm", mode, M, N, K, dA, lda, workspace, workspace_bytes, &dQ,
+                                          &dS, s))
             return rc;
-        Plan p = make_plan(mode, M, N, K, true);
-        if (rest_bytes < p.part_bytes + p.sem_bytes) rest = nullptr;   /* too small for the split: run without */
-        return p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, p2h_q_ld(K), dS, w, beta, dC, ldc, rest, rest_bytes, s);
+        return p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, p2h_q_ld(K), dS, w, beta, dC, ldc, workspace,
+                                (size_t)((char *)dQ - (char *)workspace), s);
     }
     p2k::ExactArgs g;
     memset(&g, 0, sizeof g);
@@ -806,10 +803,8 @@ int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
         if (K == 0) return P2H_OK;
         signed char *dQ;
         float *dS;
-        void *rest;
-        size_t rest_bytes;
-        if (int rc = quant_into_workspace("p2h_q8b_gemm", M, N, K, dA, lda, workspace, workspace_bytes, &dQ, &dS,
-                                          &rest, &rest_bytes, s))
+        if (int rc = quant_into_workspace("p2h_q8b_gemm", P2H_INT8W, M, N, K, dA, lda, workspace, workspace_bytes,
+                                          &dQ, &dS, s))
             return rc;
         return p2h_q8b_gemm_q8a(M, N, K, alpha, dQ, p2h_q_ld(K), dS, dB, ldb, dBscales, beta, dC, ldc, s);
     }

@@ -324,7 +324,7 @@ def quant_rows(A, K=None):
     return q, s
 
 
-def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None):
+def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None, ws=None):
     """p2h_fvb_gemm on host arrays: A [M, lda] (first K columns used), C0 [M, ldc] (ldc >= N) or None."""
     A = np.ascontiguousarray(A, np.float32)
     M, lda = A.shape
@@ -334,7 +334,8 @@ def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None):
     ldc = C0.shape[1]
     dA = to_device(A)
     dC = to_device(C0)
-    ws = Workspace(workspace_bytes(mode, M, N, K))
+    if ws is None:
+        ws = Workspace(workspace_bytes(mode, M, N, K))
     fvb_gemm_dev(mode, M, N, K, alpha, dA.ptr, lda, w, beta, dC.ptr, ldc, ws.ptr, ws.nbytes)
     return dC.download((M, ldc), np.float32)
 

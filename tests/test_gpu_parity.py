@@ -268,3 +268,19 @@ def test_one_workspace_across_shapes():
         q, sc = O.quant_rows(A)
         ref = O.gemm_i8_run("int8w", q, sc, signs, flags, lo, hi, N)
         _assert_fp32(P.fvb_gemm_q8a("int8w", q, sc, w, ws=ws), ref)
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+def test_one_fp32_workspace_across_shapes(mode):
+    """The fp32-input entry with one workspace for calls of different M, K and N, split and unsplit in turn (the
+    blas.h drop-in reuses its per-thread workspace exactly like this)."""
+    shapes = [(375, 1024, 1024), (38, 4096, 1024), (9, 256, 32), (2000, 1024, 2048), (38, 1024, 1024),
+              (9, 256, 32)]
+    ws = P.Workspace(max(P.workspace_bytes(mode, M, N, K) for M, K, N in shapes))
+    for i, (M, K, N) in enumerate(shapes):
+        signs, flags, lo, hi = _weight(K, N, 980 + i)
+        w = P.FvWeight(signs, flags, lo, hi, K, N)
+        A = P.gen_activations(SEED, 990 + i, M, K)
+        rows = np.arange(M) if M <= 400 else np.random.default_rng(i).choice(M, 64, replace=False)
+        got = P.fvb_gemm(mode, A, w, ws=ws)
+        _assert_fp32(got[rows], O.sgemm_fvb(mode, A[rows], signs, flags, lo, hi, N))
