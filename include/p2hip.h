@@ -111,16 +111,13 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
                      const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
                      size_t workspace_bytes, void *stream);
 /* Bytes of workspace that let p2h_fvb_gemm_q8a split K across workgroups (0 when the call would not split). With
- * workspace NULL the call runs unsplit. Split K adds the int32 partial sums of one 1024-row block exactly and folds
- * the blocks in order, so results do not depend on the split. */
+ * workspace NULL the call runs unsplit. A split call writes int32 partial sums per 1024-row block and a second
+ * kernel adds them (exact) and folds the blocks in order, so results do not depend on the split. Calls sharing a
+ * workspace must be stream-ordered. */
 size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K);
 
-/* A workspace must be zero-filled once before its first use (its tile counters start at zero and every call leaves
- * them at zero). A kernel, not a memset, so it may be captured. Calls sharing a workspace must be stream-ordered. */
-int p2h_workspace_init(void *workspace, size_t bytes, void *stream);
-
 /* C = alpha · A · W + beta · C on fp32 A (p2_sgemm_fvb, blas.c:1481-1499): the int8 modes quantise A into the
- * workspace (at least p2h_fvb_workspace_bytes, zero-filled once by p2h_workspace_init) and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output
+ * workspace (at least p2h_fvb_workspace_bytes) and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output
  * fmaf chain over k = 0..K-1 is the reference's exact kernel (blas.c:155-186, 929-987). */
 int    p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
                     float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream);

@@ -296,10 +296,7 @@ static void *workspace(Ctx *c, int mode, int M, int N, int K, size_t *bytes, con
     size_t need = p2h_fvb_workspace_bytes(mode, M, N, K);
     *bytes = need;
     if (need == 0) return NULL;
-    if (need > c->capW || !c->dW) {
-        dgrow(&c->dW, &c->capW, need, who);
-        check(p2h_workspace_init(c->dW, c->capW, c->stream), who);   /* split counters start at zero */
-    }
+    dgrow(&c->dW, &c->capW, need, who);
     *bytes = c->capW;
     return c->dW;
 }

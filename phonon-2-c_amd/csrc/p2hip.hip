@@ -488,18 +488,22 @@ static int check_q(const char *who, int M, int K, const signed char *dQ, int ldq
 
 namespace {
 
-using G64 = p2k::Geo<64, 64, 2, 2>;
-using G128 = p2k::Geo<128, 128, 2, 2>;
-using G256x128 = p2k::Geo<256, 128, 2, 2>;   /* 256 activation rows × 128 weight columns */
-using G128x256 = p2k::Geo<128, 256, 2, 2>;
+/* Tile configurations: activation rows × weight columns per workgroup, waves (m × n), K rows per stage. */
+using G64 = p2k::Geo<64, 64, 2, 2, 256>;
+using G128 = p2k::Geo<128, 128, 2, 2, 128>;
+using G256x128 = p2k::Geo<256, 128, 2, 2, 128>;
+using G128x256 = p2k::Geo<128, 256, 2, 2, 128>;
+using G64k512 = p2k::Geo<64, 64, 2, 2, 512>;
+using G64x128 = p2k::Geo<64, 128, 2, 2, 256>;
 
-enum { CFG_64 = 0, CFG_128 = 1, CFG_256x128 = 2, CFG_128x256 = 3, CFG_COUNT = 4 };
-const int kCfgBM[CFG_COUNT] = {64, 128, 256, 128};
-const int kCfgBN[CFG_COUNT] = {64, 128, 128, 256};
+enum { CFG_64 = 0, CFG_128 = 1, CFG_256x128 = 2, CFG_128x256 = 3, CFG_64K512 = 4, CFG_64x128 = 5, CFG_COUNT = 6 };
+const int kCfgBM[CFG_COUNT] = {64, 128, 256, 128, 64, 64};
+const int kCfgBN[CFG_COUNT] = {64, 128, 128, 256, 64, 128};
+const int kCfgBK[CFG_COUNT] = {256, 128, 128, 128, 512, 256};
 
 struct Plan {
     int cfg, splits, split_rows, tiles_m, tiles_n;
-    size_t part_bytes, sem_bytes;
+    size_t part_bytes;
 };
 
 int env_int(const char *name, int dflt)
@@ -508,44 +512,35 @@ int env_int(const char *name, int dflt)
     return (v && *v) ? atoi(v) : dflt;
 }
 
-/* Split-K counters: a fixed region at the start of the split workspace, so partial sums of one call never land on
- * the counters of another; splits run only for grids of at most this many tiles. */
-constexpr int kSemSlots = 1024;
-constexpr size_t kSemBytes = kSemSlots * 4;
-
-/* Tile and K split for one call. A split divides a 1024-row fold block (so each lies in one block) and runs only
- * with a workspace and only when the output tiles alone leave the CUs short of work; P2H_TILE and P2H_SPLIT_ROWS
- * override the choice (tuning). */
+/* Tile and K split for one call. A split is a whole number of stages inside one 1024-row fold block; it runs only
+ * with a workspace, for K > 1024 and output grids short of the CU count (its int32 partials cost splits × M × N × 4
+ * bytes of traffic, worth it only where the output is small next to K). P2H_TILE and P2H_SPLIT_ROWS (−1: never)
+ * override the choice for tuning. */
 Plan make_plan(int mode, int M, int N, int K, bool can_split)
 {
     Plan p;
     int cfg = M <= 64 ? CFG_64 : CFG_128;
     cfg = env_int("P2H_TILE", cfg);
-    if (cfg < 0 || cfg >= CFG_COUNT || (mode != P2H_INT8W && cfg > CFG_128)) cfg = CFG_128;
+    if (cfg < 0 || cfg >= CFG_COUNT || (mode != P2H_INT8W && cfg != CFG_64 && cfg != CFG_128)) cfg = CFG_128;
     p.cfg = cfg;
     p.tiles_m = (M + kCfgBM[cfg] - 1) / kCfgBM[cfg];
     p.tiles_n = (N + kCfgBN[cfg] - 1) / kCfgBN[cfg];
     const int tiles = p.tiles_m * p.tiles_n;
-    const int want = 2 * (g_cus > 0 ? g_cus : 256);
+    const int cus = g_cus > 0 ? g_cus : 256;
     p.splits = 1;
     p.split_rows = K > 0 ? K : 1;
-    if (can_split && K > 0 && tiles <= kSemSlots) {
-        int rows = 0;
-        if (tiles < want) {
-            rows = K > p2k::kFoldRows ? p2k::kFoldRows : (int)align_up((size_t)K, p2k::BK);
-            while (rows > p2k::BK && (long)tiles * ((K + rows - 1) / rows) < want) rows /= 2;
-        }
-        const int forced = env_int("P2H_SPLIT_ROWS", 0);
-        if (forced >= p2k::BK && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
-        if (rows > 0 && (K + rows - 1) / rows > 1) {
-            p.split_rows = rows;
-            p.splits = (K + rows - 1) / rows;
-        }
+    int rows = 0;
+    if (K > p2k::kFoldRows && tiles < cus) rows = p2k::kFoldRows;
+    const int forced = env_int("P2H_SPLIT_ROWS", 0);
+    if (forced < 0) rows = 0;
+    else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
+    if (rows > 0 && rows % kCfgBK[cfg] != 0) rows = 0;
+    if (can_split && K > 0 && rows > 0 && (K + rows - 1) / rows > 1) {
+        p.split_rows = rows;
+        p.splits = (K + rows - 1) / rows;
     }
     const size_t planes = mode == P2H_INT8 ? 2 : 1;
-    const bool split = p.splits > 1;
-    p.part_bytes = split ? align_up(planes * p.splits * (size_t)M * N * 4, 256) : 0;
-    p.sem_bytes = split ? kSemBytes : 0;
+    p.part_bytes = p.splits > 1 ? align_up(planes * p.splits * (size_t)M * N * 4, 256) : 0;
     return p;
 }
 
@@ -557,14 +552,12 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
     g.M = M; g.N = N; g.K = K;
     g.alpha = alpha; g.beta = beta;
     g.Q = (const int8_t *)dQ; g.ldq = ldq; g.a_scales = dScales;
+    g.kq = (int)align_up((size_t)K, P2H_Q_KALIGN);
     g.C = dC; g.ldc = ldc;
     g.c_vec4 = dC && (ldc % 4 == 0) && aligned(dC, 16);
     g.tiles_n = p.tiles_n; g.tiles_m = p.tiles_m;
     g.splits = p.splits; g.split_rows = p.split_rows;
-    if (p.splits > 1) {
-        g.sem = (unsigned *)split_ws;
-        g.part = (int32_t *)((char *)split_ws + kSemBytes);
-    }
+    if (p.splits > 1) g.part = (int32_t *)split_ws;
     return g;
 }
 
@@ -572,21 +565,28 @@ template <class G, int MODE>
 void launch_f32(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n * p.splits)), block(G::NT);
-    if (p.splits > 1)
+    if (p.splits > 1) {
         hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, false, true>), grid, block, 0, s, g);
-    else if (g.K > p2k::kFoldRows)
+        const size_t quads = (size_t)g.M * (g.N / 4);
+        hipLaunchKernelGGL((p2k::fold_splits<MODE == p2k::MODE_INT8>), dim3((unsigned)((quads + 255) / 256)),
+                           dim3(256), 0, s, g);
+    } else if (g.K > p2k::kFoldRows) {
         hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, true, false>), grid, block, 0, s, g);
-    else
+    } else {
         hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, false, false>), grid, block, 0, s, g);
+    }
 }
 
 template <int MODE>
 void launch_f32_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
+    constexpr int W = p2k::MODE_INT8W;
     switch (p.cfg) {
     case CFG_64: launch_f32<G64, MODE>(g, p, s); break;
-    case CFG_256x128: if (MODE == p2k::MODE_INT8W) launch_f32<G256x128, p2k::MODE_INT8W>(g, p, s); break;
-    case CFG_128x256: if (MODE == p2k::MODE_INT8W) launch_f32<G128x256, p2k::MODE_INT8W>(g, p, s); break;
+    case CFG_256x128: if (MODE == W) launch_f32<G256x128, W>(g, p, s); break;
+    case CFG_128x256: if (MODE == W) launch_f32<G128x256, W>(g, p, s); break;
+    case CFG_64K512: if (MODE == W) launch_f32<G64k512, W>(g, p, s); break;
+    case CFG_64x128: if (MODE == W) launch_f32<G64x128, W>(g, p, s); break;
     default: launch_f32<G128, MODE>(g, p, s); break;
     }
 }
@@ -594,8 +594,8 @@ void launch_f32_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 int check_split_ws(const char *who, const Plan &p, void *ws, size_t ws_bytes)
 {
     if (p.splits <= 1) return P2H_OK;
-    if (!ws || ws_bytes < p.part_bytes + p.sem_bytes || !aligned(ws, 256))
-        return fail(P2H_E_WORKSPACE, "%s: split workspace of %zu bytes needed", who, p.part_bytes + p.sem_bytes);
+    if (!ws || ws_bytes < p.part_bytes || !aligned(ws, 256))
+        return fail(P2H_E_WORKSPACE, "%s: split workspace of %zu bytes needed", who, p.part_bytes);
     return P2H_OK;
 }
 
@@ -603,23 +603,11 @@ int check_split_ws(const char *who, const Plan &p, void *ws, size_t ws_bytes)
 
 extern "C" {
 
-int p2h_workspace_init(void *workspace, size_t bytes, void *stream)
-{
-    if (int rc = ensure_init()) return rc;
-    if (!workspace || bytes == 0) return P2H_OK;
-    if (!aligned(workspace, 4)) return fail(P2H_E_ARG, "p2h_workspace_init: workspace must be 4-byte aligned");
-    size_t words = bytes / 4;
-    hipLaunchKernelGGL(p2k::fill_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream_of(stream),
-                       (uint32_t *)workspace, words, 0u);
-    HIPCHK(hipGetLastError());
-    return P2H_OK;
-}
-
 size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K)
 {
     if (ensure_init() || M <= 0 || N <= 0 || K <= 0 || (mode != P2H_INT8W && mode != P2H_INT8)) return 0;
     Plan p = make_plan(mode, M, N, K, true);
-    return p.part_bytes + p.sem_bytes;   /* [counters][partials], or 0 when the call would not split */
+    return p.part_bytes;   /* the split partials, or 0 when the call would not split */
 }
 
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
@@ -674,6 +662,8 @@ int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ld
     g.acc1 = dAcc; g.acc2 = dAcc2; g.ldacc = ldacc;
     hipStream_t s = stream_of(stream);
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G128::NT);
+    g.splits = 1;
+    g.split_rows = K;
     if (mode == P2H_INT8W)
         hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_INT8W, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
     else
@@ -700,13 +690,12 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
 
 static size_t quant_area(int M, int K) { return align_up((size_t)M * p2h_q_ld(K), 256) + align_up((size_t)M * 4, 256); }
 
-/* Workspace of the fp32-input entries: [split counters, kSemBytes][split partials][quantised rows][row scales].
- * The counters sit at offset 0 whatever the shape, so no call's data ever lands on them. */
+/* Workspace of the fp32-input entries: [split partials][quantised rows][row scales]. */
 size_t p2h_fvb_workspace_bytes(int mode, int M, int N, int K)
 {
     if (ensure_init() || mode == P2H_EXACT || M <= 0 || N <= 0 || K <= 0 || K % 4 != 0) return 0;
     Plan p = make_plan(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K, true);
-    return kSemBytes + p.part_bytes + quant_area(M, K);
+    return p.part_bytes + quant_area(M, K);
 }
 
 static int quant_into_workspace(const char *who, int mode, int M, int N, int K, const float *dA, int lda,

@@ -114,20 +114,21 @@ struct GemmArgs {
     float *C; int ldc; int c_vec4;                        /* fp32 output; c_vec4: ldc % 4 == 0 and C 16-B aligned */
     int32_t *acc1; int32_t *acc2; int ldacc;              /* OUT_ACC: raw sums */
     int tiles_n, tiles_m;                                 /* output tiles of the grid */
+    int kq;                                               /* K rounded up to 128: Q columns that may be read */
     int splits, split_rows;                               /* K splits; rows per split (divides 1024) */
     int32_t *part;                                        /* split partials [planes][splits][M][N] */
-    unsigned *sem;                                        /* per-tile arrival counters, zero between calls */
 };
 
-constexpr int BK = 128;          /* K rows per LDS stage */
-constexpr int SB = BK + 16;      /* LDS row pitch in bytes: 9 × 16 B, so 8 consecutive rows hit 8 bank groups */
 
 /* Tile geometry. Weight columns n play the MFMA "row" role and activation rows m the "column" role, so each lane's
  * four accumulators are four consecutive n of one output row (a 16-byte store). WN × WM waves; each wave owns
  * FN × FM MFMA tiles of 16 × 16. */
-template <int BM_, int BN_, int WM_, int WN_>
+template <int BM_, int BN_, int WM_, int WN_, int BK_>
 struct Geo {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+    static constexpr int BK = BK_;           /* K rows per LDS stage (divides 1024) */
+    static constexpr int SB = BK + 16;       /* LDS row pitch: an odd number of 16-byte chunks, so 8 consecutive rows
+                                                hit 8 different bank groups */
     static constexpr int NT = 64 * WM * WN;
     static constexpr int FN = BN / WN / 16, FM = BM / WM / 16;
     static constexpr int A_CHUNKS = BM * (BK / 16);      /* 16-byte chunks of an activation stage */
@@ -140,6 +141,7 @@ struct Geo {
     static_assert(A_CHUNKS % NT == 0, "activation chunks must divide among the threads");
     static_assert(NT % CGS == 0, "a thread's column group must not change between its units");
     static_assert(FN >= 1 && FM >= 1, "wave tile");
+    static_assert(1024 % BK == 0 && BK % 64 == 0, "stage depth");
 };
 
 /* byte permute: result byte i = byte sel_i of the 8-byte value {hi:lo}, selectors 0-3 from lo, 4-7 from hi */
@@ -172,7 +174,7 @@ constexpr uint32_t kPlaneS = 0x020100FFu;   /* [−1, 0, 1, 2] */
 
 /* Rows 4rq..4rq+3 of a stage × columns 16·cg..16·cg+15 of a five-value tile into the code tile(s): column n,
  * rows 4rq..4rq+3 land as one dword at LDS row n, 16-byte chunk (rq/4) ^ (n/16 mod 8), dword rq mod 4. */
-template <int MODE>
+template <int MODE, int SB>
 __device__ __forceinline__ void store_fv_codes(const uint32_t s[4], const uint32_t f[4], const uint32_t lo_tab[16],
                                                int8_t *tileB, int8_t *tileT, int cg, int rq)
 {
@@ -198,6 +200,7 @@ __device__ __forceinline__ void store_fv_codes(const uint32_t s[4], const uint32
 }
 
 /* An int8 table tile: rows 4rq..4rq+3, 16 columns from 16-byte row loads, transposed 4×4 per column quad. */
+template <int SB>
 __device__ __forceinline__ void store_q8_codes(const uint4 r[4], int8_t *tileB, int cg, int rq)
 {
     const int chunk = (rq >> 2) ^ (cg & 7);
@@ -232,16 +235,15 @@ __device__ __forceinline__ void tile_of(const GemmArgs &g, int &tile_n, int &til
  *  Stage loop: branch-free global loads of stage t+1 (addresses clamped in bounds, out-of-range values replaced
  *  afterwards) are issued before the MFMAs of stage t and written to the other LDS buffer after them.
  *  Folding the int32 sums into fp32 (blas.c:1355-1366): with one split, per 1024-row block in registers (MULTI keeps
- *  the running sum when K > 1024); with SPLIT, each workgroup writes its int32 partial sums, and the last of a
- *  tile's splits to arrive adds them per block (exact in int32) and folds the blocks in order. */
+ *  the running sum when K > 1024); with SPLIT, each workgroup writes its int32 partial sums and fold_splits, the
+ *  next kernel on the stream, adds them per block (exact in int32) and folds the blocks in order. */
 template <class G, int MODE, int OUT, bool MULTI, bool SPLIT>
 __global__ __launch_bounds__(G::NT, ((MODE == MODE_INT8 || MULTI || G::NT > 256 || 2 * G::LDS_ONE > 160 * 1024) ? 1 : 2))
 void gemm_i8(GemmArgs g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
-    constexpr int FN = G::FN, FM = G::FM;
+    constexpr int FN = G::FN, FM = G::FM, BK = G::BK, SB = G::SB;
     __shared__ __attribute__((aligned(16))) int8_t sm[2 * G::A_BYTES + (TWO ? 4 : 2) * G::B_BYTES];
-    __shared__ int s_last;
     auto smA = [&](int b) { return sm + b * G::A_BYTES; };
     auto smB = [&](int b) { return sm + 2 * G::A_BYTES + b * G::B_BYTES; };
     auto smT = [&](int b) { return sm + 2 * G::A_BYTES + ((TWO ? 2 : 0) + b) * G::B_BYTES; };
@@ -277,9 +279,10 @@ void gemm_i8(GemmArgs g)
         for (int i = 0; i < G::A_PER; i++) {
             const int c = tid + i * G::NT;
             const int m = m0 + c / (BK / 16);
-            const int mc = min(m, M - 1);
-            uint4 v = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + k0 + 16 * (c % (BK / 16)));
-            ra[i] = m < M ? v : make_uint4(0, 0, 0, 0);
+            const int kk = k0 + 16 * (c % (BK / 16));
+            const int mc = min(m, M - 1), kc = min(kk, g.kq - 16);
+            uint4 v = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + kc);
+            ra[i] = (m < M && kk < g.kq) ? v : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < G::B_PER; u++) {
@@ -312,8 +315,8 @@ void gemm_i8(GemmArgs g)
         for (int u = 0; u < G::B_PER; u++) {
             const int rq = rq0 + u * (G::NT / G::CGS);
             if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
-            if (MODE == MODE_Q8B) store_q8_codes(rb[u], smB(buf), cg, rq);
-            else store_fv_codes<MODE>(rs[u], rf[u], lo_tab, smB(buf), smT(buf), cg, rq);
+            if (MODE == MODE_Q8B) store_q8_codes<SB>(rb[u], smB(buf), cg, rq);
+            else store_fv_codes<MODE, SB>(rs[u], rf[u], lo_tab, smB(buf), smT(buf), cg, rq);
         }
     };
 
@@ -450,7 +453,7 @@ void gemm_i8(GemmArgs g)
         return;
     }
 
-    if (SPLIT) {
+    if (SPLIT) {   /* int32 partial sums of this split; fold_splits adds and folds them */
         const size_t plane = (size_t)g.splits * M * N;
 #pragma unroll
         for (int i = 0; i < FN; i++)
@@ -463,34 +466,51 @@ void gemm_i8(GemmArgs g)
                     if (TWO) *reinterpret_cast<v4i *>(p + plane) = accT[TWO ? i : 0][TWO ? j : 0];
                 }
             }
-        __threadfence();
-        __syncthreads();
-        const int tile = tile_m * g.tiles_n + tile_n;
-        if (tid == 0) s_last = atomicAdd(g.sem + tile, 1u) == (unsigned)(g.splits - 1);
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        const int per_block = kFoldRows / g.split_rows;
-        const int nblocks = (g.splits + per_block - 1) / per_block;
-#pragma unroll
-        for (int i = 0; i < FN; i++)
-#pragma unroll
-            for (int j = 0; j < FM; j++) {
-                const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
-                float runv[4] = {0, 0, 0, 0};
-                for (int b = 0; b < nblocks; b++) {
-                    v4i s1 = v4i{0, 0, 0, 0}, s2 = v4i{0, 0, 0, 0};
-                    const int s_end = min(g.splits, (b + 1) * per_block);
-                    for (int s = b * per_block; s < s_end; s++) {
-                        const int32_t *p = g.part + ((size_t)s * M + m) * N + n;
-                        s1 += *reinterpret_cast<const v4i *>(p);
-                        if (TWO) s2 += *reinterpret_cast<const v4i *>(p + plane);
-                    }
-                    fold_one(b, b + 1 == nblocks, i, j, s1, s2, runv);
-                }
-            }
-        if (tid == 0) g.sem[tile] = 0u;
     }
+}
+
+/* The fold after a split GEMM: per output, the int32 partial sums of the splits inside each 1024-row block are
+ * added (exact), then the blocks fold into fp32 in order exactly as the unsplit kernel folds them. One thread per
+ * four consecutive outputs of a row. */
+template <bool TWO>
+__global__ __launch_bounds__(256) void fold_splits(GemmArgs g)
+{
+    const int M = g.M, N = g.N;
+    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (size_t)M * (N / 4)) return;
+    const int m = (int)(q / (N / 4)), n = 4 * (int)(q % (N / 4));
+    const size_t plane = (size_t)g.splits * M * N;
+    const int per_block = kFoldRows / g.split_rows;
+    const int nblocks = (g.splits + per_block - 1) / per_block;
+    const float as = g.a_scales[m] * g.alpha;
+    float *cp = g.C + (size_t)m * g.ldc + n;
+    float c1v[4], c2v[4] = {0, 0, 0, 0}, run[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        c1v[r] = g.c1[n + r];
+        if (TWO) c2v[r] = g.c2[n + r];
+    }
+    if (g.beta != 0.0f) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) run[r] = g.beta == 1.0f ? cp[r] : cp[r] * g.beta;
+    }
+    for (int b = 0; b < nblocks; b++) {
+        v4i s1 = v4i{0, 0, 0, 0}, s2 = v4i{0, 0, 0, 0};
+        const int s_end = min(g.splits, (b + 1) * per_block);
+        for (int s = b * per_block; s < s_end; s++) {
+            const int32_t *p = g.part + ((size_t)s * M + m) * N + n;
+            s1 += *reinterpret_cast<const v4i *>(p);
+            if (TWO) s2 += *reinterpret_cast<const v4i *>(p + plane);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float f = (float)s1[r] * c1v[r];
+            if (TWO) f = __builtin_fmaf((float)s2[r], c2v[r], f);
+            run[r] = (b == 0 && g.beta == 0.0f) ? f * as : __builtin_fmaf(f, as, run[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) cp[r] = run[r];
 }
 
 /* ── the exact route ───────────────────────────────────────────────────────────────────────────────────────── */

@@ -65,7 +65,6 @@ _HIP_SIG = {
     "p2h_q_ld": (_i, [_i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
-    "p2h_workspace_init": (_i, [_vp, _sz, _vp]),
     "p2h_fvb_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_acc_i32": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp]),
@@ -284,12 +283,10 @@ def q8a_workspace_bytes(mode, M, N, K):
 
 
 class Workspace(DeviceBuffer):
-    """A zero-initialised workspace (its split-K tile counters must start at zero)."""
+    """Device scratch for the GEMM entries (quantised rows, split-K partial sums)."""
 
     def __init__(self, nbytes, stream=None):
         super().__init__(max(int(nbytes), 256))
-        _ok(hip().p2h_workspace_init(self.ptr, self.nbytes, stream), "p2h_workspace_init")
-        sync(stream)
 
 
 # ── device-pointer entry points (asynchronous on `stream`) ───────────────────────────────────────────────────────
