@@ -273,16 +273,16 @@ void gemm_i8(GemmArgs g)
     uint32_t rs[G::B_PER][4], rf[G::B_PER][4];
     uint4 rb[G::B_PER][4];
 
+    /* Loads only: every address is clamped in bounds, so no load is conditional and none is waited on here; the
+     * out-of-range values are replaced in store_stage, after the MFMAs of the current stage have been issued. */
     auto load_stage = [&](int t) {
         const int k0 = k_begin + t * BK;
 #pragma unroll
         for (int i = 0; i < G::A_PER; i++) {
             const int c = tid + i * G::NT;
-            const int m = m0 + c / (BK / 16);
-            const int kk = k0 + 16 * (c % (BK / 16));
-            const int mc = min(m, M - 1), kc = min(kk, g.kq - 16);
-            uint4 v = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + kc);
-            ra[i] = (m < M && kk < g.kq) ? v : make_uint4(0, 0, 0, 0);
+            const int mc = min(m0 + c / (BK / 16), M - 1);
+            const int kc = min(k0 + 16 * (c % (BK / 16)), g.kq - 16);
+            ra[i] = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + kc);
         }
 #pragma unroll
         for (int u = 0; u < G::B_PER; u++) {
@@ -290,33 +290,47 @@ void gemm_i8(GemmArgs g)
             if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int k = k0 + 4 * rq + r;
-                const bool ok = col_ok && k < k_end;
-                const int kc = min(k, K - 1);
+                const int kc = min(k0 + 4 * rq + r, K - 1);
                 if (MODE == MODE_Q8B) {
-                    uint4 v = *reinterpret_cast<const uint4 *>(g.B8 + (size_t)kc * g.ldb + n0 + 16 * cgc);
-                    rb[u][r] = ok ? v : make_uint4(0, 0, 0, 0);
+                    rb[u][r] = *reinterpret_cast<const uint4 *>(g.B8 + (size_t)kc * g.ldb + n0 + 16 * cgc);
                 } else {
-                    uint32_t sv = *reinterpret_cast<const uint32_t *>(g.signs + (size_t)kc * (N / 4) + n0 / 4 + 4 * cgc);
-                    uint32_t fv = *reinterpret_cast<const uint16_t *>(g.flags + (size_t)kc * (N / 8) + n0 / 8 + 2 * cgc);
-                    rs[u][r] = ok ? sv : 0x55555555u;   /* code 1 everywhere: zero weights */
-                    rf[u][r] = ok ? fv : 0u;
+                    rs[u][r] = *reinterpret_cast<const uint32_t *>(g.signs + (size_t)kc * (N / 4) + n0 / 4 + 4 * cgc);
+                    rf[u][r] = *reinterpret_cast<const uint16_t *>(g.flags + (size_t)kc * (N / 8) + n0 / 8 + 2 * cgc);
                 }
             }
         }
     };
-    auto store_stage = [&](int buf) {
+    auto store_stage = [&](int t, int buf) {
+        const int k0 = k_begin + t * BK;
 #pragma unroll
         for (int i = 0; i < G::A_PER; i++) {
             const int c = tid + i * G::NT;
-            *reinterpret_cast<uint4 *>(smA(buf) + (c / (BK / 16)) * SB + 16 * (c % (BK / 16))) = ra[i];
+            const bool ok = m0 + c / (BK / 16) < M && k0 + 16 * (c % (BK / 16)) < g.kq;
+            *reinterpret_cast<uint4 *>(smA(buf) + (c / (BK / 16)) * SB + 16 * (c % (BK / 16))) =
+                ok ? ra[i] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < G::B_PER; u++) {
             const int rq = rq0 + u * (G::NT / G::CGS);
             if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
-            if (MODE == MODE_Q8B) store_q8_codes<SB>(rb[u], smB(buf), cg, rq);
-            else store_fv_codes<MODE, SB>(rs[u], rf[u], lo_tab, smB(buf), smT(buf), cg, rq);
+            if (MODE == MODE_Q8B) {
+                uint4 v[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool ok = col_ok && k0 + 4 * rq + r < k_end;
+                    v[r] = ok ? rb[u][r] : make_uint4(0, 0, 0, 0);
+                }
+                store_q8_codes<SB>(v, smB(buf), cg, rq);
+            } else {
+                uint32_t sv[4], fv[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool ok = col_ok && k0 + 4 * rq + r < k_end;
+                    sv[r] = ok ? rs[u][r] : 0x55555555u;   /* code 1 everywhere: zero weights */
+                    fv[r] = ok ? rf[u][r] : 0u;
+                }
+                store_fv_codes<MODE, SB>(sv, fv, lo_tab, smB(buf), smT(buf), cg, rq);
+            }
         }
     };
 
@@ -384,7 +398,7 @@ void gemm_i8(GemmArgs g)
 
     if (nk > 0) {
         load_stage(0);
-        store_stage(0);
+        store_stage(0, 0);
     }
     __syncthreads();
 
@@ -419,7 +433,7 @@ void gemm_i8(GemmArgs g)
                             bt[TWO ? i : 0], b[j], accT[TWO ? i : 0][TWO ? j : 0], 0, 0, 0);
                 }
         }
-        if (t + 1 < nk) store_stage(buf ^ 1);
+        if (t + 1 < nk) store_stage(t + 1, buf ^ 1);
         if (OUT == OUT_F32 && !SPLIT) {
             const bool last = t + 1 == nk;
             if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
