@@ -519,7 +519,8 @@ int env_int(const char *name, int dflt)
 Plan make_plan(int mode, int M, int N, int K, bool can_split)
 {
     Plan p;
-    int cfg = M <= 64 ? CFG_64 : CFG_128;
+    /* measured on MI355X: 64×64 tiles with 256-row stages win up to a thousand rows, 128×128 beyond */
+    int cfg = M <= 1024 ? CFG_64 : CFG_128;
     cfg = env_int("P2H_TILE", cfg);
     if (cfg < 0 || cfg >= CFG_COUNT || (mode != P2H_INT8W && cfg != CFG_64 && cfg != CFG_128)) cfg = CFG_128;
     p.cfg = cfg;
@@ -530,7 +531,7 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     p.splits = 1;
     p.split_rows = K > 0 ? K : 1;
     int rows = 0;
-    if (K > p2k::kFoldRows && tiles < cus) rows = p2k::kFoldRows;
+    if (K > p2k::kFoldRows && tiles < cus) rows = (M <= 64 && tiles * (K / 512) <= 2 * cus) ? 512 : p2k::kFoldRows;
     const int forced = env_int("P2H_SPLIT_ROWS", 0);
     if (forced < 0) rows = 0;
     else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
