@@ -227,6 +227,9 @@ def main():
     ap.add_argument("--workload", default="ffn375", choices=["ffn375", "m6000", "m38", "sweep", "exact375"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run device-to-device copies of this many MiB (the plain copy kernel that scales "
+                         "FETCH_SIZE / WRITE_SIZE counter readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: the five-value GEMM path has no multi-GPU form in this build "
@@ -236,6 +239,14 @@ def main():
     dev = P.init()
     stream = P.Stream()
     print(f"# device {dev}, {P.device_cu_count()} CUs", file=sys.stderr, flush=True)
+    if args.copy_mib:
+        nbytes = args.copy_mib << 20
+        src, dst = P.DeviceBuffer(nbytes), P.DeviceBuffer(nbytes)
+        for _ in range(5):
+            P._ok(P.hip().p2h_memcpy_d2d(dst.ptr, src.ptr, nbytes, stream.ptr), "d2d")
+        stream.sync()
+        print(f"# copied {args.copy_mib} MiB x5", file=sys.stderr, flush=True)
+        return
 
     results = {}
 
@@ -275,9 +286,10 @@ def main():
     L = lins[i]
     alg = gemm_bytes(L.M, L.N, L.K, 1)
     achieved = alg / (gt[i] * 1e-3) / 1e9
+    plan = P.plan("int8w", L.M, L.N, L.K)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": f"gemm_i8<int8w> M={L.M} K={L.K} N={L.N}", "algorithmic_bytes": int(alg),
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(L, plan),
+                "kernel": f"gemm_i8<int8w> M={L.M} K={L.K} N={L.N} ({plan})", "algorithmic_bytes": int(alg),
                 "avg_ms": gt[i]}
 
     ops = sum(gemm_ops(l.M, l.N, l.K) for l in lins)
@@ -310,6 +322,18 @@ def main():
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+
+
+def measured_traffic(L, plan):
+    """HBM bytes per launch of this GEMM from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    (profiles/gemm_i8_traffic.json), when they were taken for the same shape and plan; otherwise None."""
+    path = os.path.join(ROOT, "profiles", "gemm_i8_traffic.json")
+    if not os.path.exists(path):
+        return None
+    for e in json.load(open(path))["entries"]:
+        if (e["M"], e["K"], e["N"]) == (L.M, L.K, L.N) and e["plan"] == plan:
+            return int(e["fetch_kib"] * 1024 * e["fetch_scale"] + e["write_kib"] * 1024 * e["write_scale"])
+    return None
 
 
 def exact_config(stream):

@@ -115,6 +115,8 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
  * kernel adds them (exact) and folds the blocks in order, so results do not depend on the split. Calls sharing a
  * workspace must be stream-ordered. */
 size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K);
+/* The tile and split p2h_fvb_gemm_q8a chooses for a shape, as text (per thread; valid until the next call). */
+const char *p2h_fvb_plan(int mode, int M, int N, int K, int with_workspace);
 
 /* C = alpha · A · W + beta · C on fp32 A (p2_sgemm_fvb, blas.c:1481-1499): the int8 modes quantise A into the
  * workspace (at least p2h_fvb_workspace_bytes) and run p2h_fvb_gemm_q8a; P2H_EXACT (or K % 4 != 0) runs the fp32 expansion route, whose per-output

@@ -530,8 +530,8 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     const int cus = g_cus > 0 ? g_cus : 256;
     p.splits = 1;
     p.split_rows = K > 0 ? K : 1;
-    int rows = 0;
-    if (K > p2k::kFoldRows && tiles < cus) rows = (M <= 64 && tiles * (K / 512) <= 2 * cus) ? 512 : p2k::kFoldRows;
+    int rows = 0;   /* K > 1024 splits per fold block: measured faster than folding in registers at every M */
+    if (K > p2k::kFoldRows) rows = (M <= 64 && tiles * (K / 512) <= 2 * cus) ? 512 : p2k::kFoldRows;
     const int forced = env_int("P2H_SPLIT_ROWS", 0);
     if (forced < 0) rows = 0;
     else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
@@ -603,6 +603,17 @@ int check_split_ws(const char *who, const Plan &p, void *ws, size_t ws_bytes)
 }  // namespace
 
 extern "C" {
+
+const char *p2h_fvb_plan(int mode, int M, int N, int K, int with_workspace)
+{
+    static thread_local char buf[160];
+    if (ensure_init() || M <= 0 || N <= 0 || K <= 0) return "";
+    Plan p = make_plan(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K, with_workspace != 0);
+    snprintf(buf, sizeof buf, "tile %dx%d k%d, %d split%s of %d rows%s", kCfgBM[p.cfg], kCfgBN[p.cfg],
+             kCfgBK[p.cfg], p.splits, p.splits > 1 ? "s" : "", p.split_rows,
+             p.splits > 1 ? " + fold" : (K > p2k::kFoldRows ? ", folds in registers" : ""));
+    return buf;
+}
 
 size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K)
 {

@@ -65,6 +65,7 @@ _HIP_SIG = {
     "p2h_q_ld": (_i, [_i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "p2h_fvb_plan": (C.c_char_p, [_i, _i, _i, _i, _i]),
     "p2h_fvb_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_acc_i32": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp]),
@@ -276,6 +277,11 @@ def q_ld(K):
 def workspace_bytes(mode, M, N, K):
     """Workspace of p2h_fvb_gemm (fp32 activations): quantised rows plus the split-K area."""
     return hip().p2h_fvb_workspace_bytes(MODES.get(mode, mode), M, N, K)
+
+
+def plan(mode, M, N, K, with_workspace=True):
+    """The tile and K split the library picks for this shape."""
+    return hip().p2h_fvb_plan(MODES.get(mode, mode), M, N, K, 1 if with_workspace else 0).decode()
 
 
 def q8a_workspace_bytes(mode, M, N, K):
