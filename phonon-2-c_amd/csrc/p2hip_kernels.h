@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace p2k {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -258,7 +260,7 @@ void gemm_i8(GemmArgs g)
     const int k_end = min(K, k_begin + g.split_rows);
     const int nk = (k_end - k_begin + BK - 1) / BK;
 
-    /* B producer: column group cg (fixed), quads rq0 + i·(NT/CGS) */
+    /* B producer: column group cg (fixed), quads rq0 + u·(NT/CGS) */
     const int cg = tid % G::CGS, rq0 = tid / G::CGS;
     const bool col_ok = n0 + 16 * cg < N;
     const int cgc = col_ok ? cg : 0;   /* clamped column group for addressing */
@@ -268,71 +270,6 @@ void gemm_i8(GemmArgs g)
 #pragma unroll
         for (int j = 0; j < 16; j++) lo_tab[j] = i8w_lo_table(g.clo[n0 + 16 * cgc + j]);
     }
-
-    uint4 ra[G::A_PER];
-    uint32_t rs[G::B_PER][4], rf[G::B_PER][4];
-    uint4 rb[G::B_PER][4];
-
-    /* Loads only: every address is clamped in bounds, so no load is conditional and none is waited on here; the
-     * out-of-range values are replaced in store_stage, after the MFMAs of the current stage have been issued. */
-    auto load_stage = [&](int t) {
-        const int k0 = k_begin + t * BK;
-#pragma unroll
-        for (int i = 0; i < G::A_PER; i++) {
-            const int c = tid + i * G::NT;
-            const int mc = min(m0 + c / (BK / 16), M - 1);
-            const int kc = min(k0 + 16 * (c % (BK / 16)), g.kq - 16);
-            ra[i] = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + kc);
-        }
-#pragma unroll
-        for (int u = 0; u < G::B_PER; u++) {
-            const int rq = rq0 + u * (G::NT / G::CGS);
-            if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int kc = min(k0 + 4 * rq + r, K - 1);
-                if (MODE == MODE_Q8B) {
-                    rb[u][r] = *reinterpret_cast<const uint4 *>(g.B8 + (size_t)kc * g.ldb + n0 + 16 * cgc);
-                } else {
-                    rs[u][r] = *reinterpret_cast<const uint32_t *>(g.signs + (size_t)kc * (N / 4) + n0 / 4 + 4 * cgc);
-                    rf[u][r] = *reinterpret_cast<const uint16_t *>(g.flags + (size_t)kc * (N / 8) + n0 / 8 + 2 * cgc);
-                }
-            }
-        }
-    };
-    auto store_stage = [&](int t, int buf) {
-        const int k0 = k_begin + t * BK;
-#pragma unroll
-        for (int i = 0; i < G::A_PER; i++) {
-            const int c = tid + i * G::NT;
-            const bool ok = m0 + c / (BK / 16) < M && k0 + 16 * (c % (BK / 16)) < g.kq;
-            *reinterpret_cast<uint4 *>(smA(buf) + (c / (BK / 16)) * SB + 16 * (c % (BK / 16))) =
-                ok ? ra[i] : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < G::B_PER; u++) {
-            const int rq = rq0 + u * (G::NT / G::CGS);
-            if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
-            if (MODE == MODE_Q8B) {
-                uint4 v[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const bool ok = col_ok && k0 + 4 * rq + r < k_end;
-                    v[r] = ok ? rb[u][r] : make_uint4(0, 0, 0, 0);
-                }
-                store_q8_codes<SB>(v, smB(buf), cg, rq);
-            } else {
-                uint32_t sv[4], fv[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const bool ok = col_ok && k0 + 4 * rq + r < k_end;
-                    sv[r] = ok ? rs[u][r] : 0x55555555u;   /* code 1 everywhere: zero weights */
-                    fv[r] = ok ? rf[u][r] : 0u;
-                }
-                store_fv_codes<MODE, SB>(sv, fv, lo_tab, smB(buf), smT(buf), cg, rq);
-            }
-        }
-    };
 
     v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
     float run[MULTI ? FN : 1][MULTI ? FM : 1][4];
@@ -396,62 +333,178 @@ void gemm_i8(GemmArgs g)
         }
     };
 
-    if (nk > 0) {
-        load_stage(0);
-        store_stage(0, 0);
+    /* Per-lane byte offsets of this thread's loads, fixed for the whole K loop: a stage adds a uniform base, so the
+     * loads address as (scalar base + 32-bit lane offset). */
+    uint32_t a_off[G::A_PER], s_off[G::B_PER][4], f_off[G::B_PER][4], b8_off[G::B_PER][4];
+#pragma unroll
+    for (int i = 0; i < G::A_PER; i++) {
+        const int c = tid + i * G::NT;
+        a_off[i] = (uint32_t)((c / (BK / 16)) * g.ldq + 16 * (c % (BK / 16)));
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < G::B_PER; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = 4 * (rq0 + u * (G::NT / G::CGS)) + r;
+            s_off[u][r] = (uint32_t)(row * (N / 4) + 4 * cgc);
+            f_off[u][r] = (uint32_t)(row * (N / 8) + 2 * cgc);
+            b8_off[u][r] = (uint32_t)(row * g.ldb + 16 * cgc);
+        }
 
-    int block = 0;
-    for (int t = 0; t < nk; t++) {
-        const int buf = t & 1;
-        if (t + 1 < nk) load_stage(t + 1);
-        const int8_t *tA = smA(buf), *tB = smB(buf), *tT = smT(buf);
+    uint4 ra[G::A_PER];
+    uint32_t rs[G::B_PER][4], rf[G::B_PER][4];
+    uint4 rb[G::B_PER][4];
+
+    /* Interior tiles (every row, column and K row in range) run without any bounds arithmetic; edge tiles clamp
+     * every address in bounds and mask the out-of-range values when they are written to LDS. Either way no load is
+     * conditional, and none is waited on before the MFMAs of the current stage are issued. */
+    const bool interior = m0 + G::BM <= M && n0 + G::BN <= N && (k_end - k_begin) % BK == 0;
+
+    auto body = [&](auto edge_tag) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        auto load_stage = [&](int t) {
+            const int k0 = k_begin + t * BK;
+            if (!EDGE) {
+                const int8_t *qk = g.Q + (size_t)m0 * g.ldq + k0;
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 64) {
-            const int g16 = (kk >> 4) + (lane >> 4);   /* this lane's 16-byte chunk along k */
-            v4i a[FN], b[FM], bt[TWO ? FN : 1];
+                for (int i = 0; i < G::A_PER; i++) ra[i] = *reinterpret_cast<const uint4 *>(qk + a_off[i]);
+                const uint8_t *sk = g.signs + (size_t)k0 * (N / 4) + n0 / 4;
+                const uint8_t *fk = g.flags + (size_t)k0 * (N / 8) + n0 / 8;
+                const int8_t *bk = g.B8 + (size_t)k0 * g.ldb + n0;
 #pragma unroll
-            for (int i = 0; i < FN; i++) {
-                const int nl = wn * (G::BN / G::WN) + 16 * i + (lane & 15);
-                const int off = nl * SB + 16 * (g16 ^ ((nl >> 4) & 7));
-                a[i] = *reinterpret_cast<const v4i *>(tB + off);
-                if (TWO) bt[TWO ? i : 0] = *reinterpret_cast<const v4i *>(tT + off);
+                for (int u = 0; u < G::B_PER; u++) {
+                    if (G::B_UNITS % G::NT != 0 && rq0 + u * (G::NT / G::CGS) >= BK / 4) break;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if (MODE == MODE_Q8B) {
+                            rb[u][r] = *reinterpret_cast<const uint4 *>(bk + b8_off[u][r]);
+                        } else {
+                            rs[u][r] = *reinterpret_cast<const uint32_t *>(sk + s_off[u][r]);
+                            rf[u][r] = *reinterpret_cast<const uint16_t *>(fk + f_off[u][r]);
+                        }
+                    }
+                }
+                return;
             }
 #pragma unroll
-            for (int j = 0; j < FM; j++) {
-                const int ml = wm * (G::BM / G::WM) + 16 * j + (lane & 15);
-                b[j] = *reinterpret_cast<const v4i *>(tA + ml * SB + 16 * g16);
+            for (int i = 0; i < G::A_PER; i++) {
+                const int c = tid + i * G::NT;
+                const int mc = min(m0 + c / (BK / 16), M - 1);
+                const int kc = min(k0 + 16 * (c % (BK / 16)), g.kq - 16);
+                ra[i] = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + kc);
             }
 #pragma unroll
-            for (int i = 0; i < FN; i++)
+            for (int u = 0; u < G::B_PER; u++) {
+                const int rq = rq0 + u * (G::NT / G::CGS);
+                if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int kc = min(k0 + 4 * rq + r, K - 1);
+                    if (MODE == MODE_Q8B) {
+                        rb[u][r] = *reinterpret_cast<const uint4 *>(g.B8 + (size_t)kc * g.ldb + n0 + 16 * cgc);
+                    } else {
+                        rs[u][r] = *reinterpret_cast<const uint32_t *>(g.signs + (size_t)kc * (N / 4) + n0 / 4 + 4 * cgc);
+                        rf[u][r] = *reinterpret_cast<const uint16_t *>(g.flags + (size_t)kc * (N / 8) + n0 / 8 + 2 * cgc);
+                    }
+                }
+            }
+        };
+        auto store_stage = [&](int t, int buf) {
+            const int k0 = k_begin + t * BK;
+#pragma unroll
+            for (int i = 0; i < G::A_PER; i++) {
+                const int c = tid + i * G::NT;
+                uint4 v = ra[i];
+                if (EDGE) {
+                    const bool ok = m0 + c / (BK / 16) < M && k0 + 16 * (c % (BK / 16)) < g.kq;
+                    v = ok ? v : make_uint4(0, 0, 0, 0);
+                }
+                *reinterpret_cast<uint4 *>(smA(buf) + (c / (BK / 16)) * SB + 16 * (c % (BK / 16))) = v;
+            }
+#pragma unroll
+            for (int u = 0; u < G::B_PER; u++) {
+                const int rq = rq0 + u * (G::NT / G::CGS);
+                if (G::B_UNITS % G::NT != 0 && rq >= BK / 4) break;
+                if (MODE == MODE_Q8B) {
+                    uint4 v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const bool ok = !EDGE || (col_ok && k0 + 4 * rq + r < k_end);
+                        v[r] = ok ? rb[u][r] : make_uint4(0, 0, 0, 0);
+                    }
+                    store_q8_codes<SB>(v, smB(buf), cg, rq);
+                } else {
+                    uint32_t sv[4], fv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const bool ok = !EDGE || (col_ok && k0 + 4 * rq + r < k_end);
+                        sv[r] = ok ? rs[u][r] : 0x55555555u;   /* code 1 everywhere: zero weights */
+                        fv[r] = ok ? rf[u][r] : 0u;
+                    }
+                    store_fv_codes<MODE, SB>(sv, fv, lo_tab, smB(buf), smT(buf), cg, rq);
+                }
+            }
+        };
+
+        if (nk > 0) {
+            load_stage(0);
+            store_stage(0, 0);
+        }
+        __syncthreads();
+
+        int block = 0;
+        for (int t = 0; t < nk; t++) {
+            const int buf = t & 1;
+            if (t + 1 < nk) load_stage(t + 1);
+            const int8_t *tA = smA(buf), *tB = smB(buf), *tT = smT(buf);
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 64) {
+                const int g16 = (kk >> 4) + (lane >> 4);   /* this lane's 16-byte chunk along k */
+                v4i a[FN], b[FM], bt[TWO ? FN : 1];
+#pragma unroll
+                for (int i = 0; i < FN; i++) {
+                    const int nl = wn * (G::BN / G::WN) + 16 * i + (lane & 15);
+                    const int off = nl * SB + 16 * (g16 ^ ((nl >> 4) & 7));
+                    a[i] = *reinterpret_cast<const v4i *>(tB + off);
+                    if (TWO) bt[TWO ? i : 0] = *reinterpret_cast<const v4i *>(tT + off);
+                }
 #pragma unroll
                 for (int j = 0; j < FM; j++) {
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-                    if (TWO)
-                        accT[TWO ? i : 0][TWO ? j : 0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            bt[TWO ? i : 0], b[j], accT[TWO ? i : 0][TWO ? j : 0], 0, 0, 0);
+                    const int ml = wm * (G::BM / G::WM) + 16 * j + (lane & 15);
+                    b[j] = *reinterpret_cast<const v4i *>(tA + ml * SB + 16 * g16);
                 }
-        }
-        if (t + 1 < nk) store_stage(t + 1, buf ^ 1);
-        if (OUT == OUT_F32 && !SPLIT) {
-            const bool last = t + 1 == nk;
-            if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
 #pragma unroll
                 for (int i = 0; i < FN; i++)
 #pragma unroll
                     for (int j = 0; j < FM; j++) {
-                        float tmp[4];
-                        float *rv = MULTI ? run[MULTI ? i : 0][MULTI ? j : 0] : tmp;
-                        fold_one(block, last, i, j, acc[i][j], TWO ? accT[TWO ? i : 0][TWO ? j : 0] : acc[i][j], rv);
-                        acc[i][j] = v4i{0, 0, 0, 0};
-                        if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+                        if (TWO)
+                            accT[TWO ? i : 0][TWO ? j : 0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                bt[TWO ? i : 0], b[j], accT[TWO ? i : 0][TWO ? j : 0], 0, 0, 0);
                     }
-                block++;
             }
+            if (t + 1 < nk) store_stage(t + 1, buf ^ 1);
+            if (OUT == OUT_F32 && !SPLIT) {
+                const bool last = t + 1 == nk;
+                if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
+#pragma unroll
+                    for (int i = 0; i < FN; i++)
+#pragma unroll
+                        for (int j = 0; j < FM; j++) {
+                            float tmp[4];
+                            float *rv = MULTI ? run[MULTI ? i : 0][MULTI ? j : 0] : tmp;
+                            fold_one(block, last, i, j, acc[i][j], TWO ? accT[TWO ? i : 0][TWO ? j : 0] : acc[i][j], rv);
+                            acc[i][j] = v4i{0, 0, 0, 0};
+                            if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+                        }
+                    block++;
+                }
+            }
+            __syncthreads();
         }
-        __syncthreads();
-    }
+    };
+    if (interior) body(std::false_type{});
+    else body(std::true_type{});
 
     if (OUT == OUT_ACC) {
 #pragma unroll
