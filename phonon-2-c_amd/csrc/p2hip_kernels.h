@@ -272,7 +272,7 @@ void gemm_i8(GemmArgs g)
     }
 
     v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
-    float run[MULTI ? FN : 1][MULTI ? FM : 1][4];
+    float run[MULTI ? FN : 1][FM][4];
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
@@ -286,51 +286,76 @@ void gemm_i8(GemmArgs g)
     const int m_lane = m0 + wm * (G::BM / G::WM) + (lane & 15);
     const bool beta_zero = g.beta == 0.0f;
 
-    /* One fold of a K block: f = (float)accS · c1 (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta 0)
-     * or fmaf(f, as, beta-scaled C); later blocks fmaf(f, as, running). `last` stores C. */
-    auto fold_one = [&](int block, bool last, int i, int j, const v4i &a1, const v4i &a2, float runv[4]) {
-        const int n = n_lane + 16 * i, m = m_lane + 16 * j;
-        const bool ok = n < N && m < M;
-        const int nc = min(n, N - 4), mc = min(m, M - 1);
-        float c1v[4], c2v[4] = {0, 0, 0, 0};
+    /* Epilogue factors of this lane, loaded before the K loop so their latency hides behind it: c1 (and c2) of its
+     * 4·FN columns, as = a_scale·alpha of its FM rows. */
+    float c1v[FN][4], c2v[TWO ? FN : 1][4], asv[FM];
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+        const int nc = min(n_lane + 16 * i, N - 4);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            c1v[r] = g.c1[nc + r];
-            if (TWO) c2v[r] = g.c2[nc + r];
+            c1v[i][r] = g.c1[nc + r];
+            if (TWO) c2v[TWO ? i : 0][r] = g.c2[nc + r];
         }
-        const float as = g.a_scales[mc] * g.alpha;
-        float *cp = g.C + (size_t)m * g.ldc + n;
-        float cold[4] = {0, 0, 0, 0};
-        if (block == 0 && !beta_zero && ok) {
-            if (g.c_vec4) {
-                float4 v = *reinterpret_cast<const float4 *>(cp);
-                cold[0] = v.x; cold[1] = v.y; cold[2] = v.z; cold[3] = v.w;
-            } else {
+    }
 #pragma unroll
-                for (int r = 0; r < 4; r++) cold[r] = cp[r];
-            }
+    for (int j = 0; j < FM; j++) asv[j] = (OUT == OUT_F32 && !SPLIT) ? g.a_scales[min(m_lane + 16 * j, M - 1)] * g.alpha : 0.0f;
+
+    /* One fold of a K block into every output of the lane (blas.c:1355-1366): f = (float)accS · c1
+     * (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta 0) or fmaf(f, as, beta-scaled C), later blocks
+     * fmaf(f, as, running); `last` stores C. The beta reads of C are all issued before any is used. */
+    auto fold_all = [&](int block, bool last, float (*runv)[FM][4]) {
+        float cold[FN][FM][4];
+        if (block == 0 && !beta_zero) {
+#pragma unroll
+            for (int i = 0; i < FN; i++)
+#pragma unroll
+                for (int j = 0; j < FM; j++) {
+                    const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
+                    const float *cp = g.C + (size_t)m * g.ldc + n;
+                    if (g.c_vec4) {
+                        float4 v = *reinterpret_cast<const float4 *>(cp);
+                        cold[i][j][0] = v.x; cold[i][j][1] = v.y; cold[i][j][2] = v.z; cold[i][j][3] = v.w;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[i][j][r] = cp[r];
+                    }
+                }
             if (g.beta != 1.0f) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) cold[r] = cold[r] * g.beta;
+                for (int i = 0; i < FN; i++)
+#pragma unroll
+                    for (int j = 0; j < FM; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[i][j][r] = cold[i][j][r] * g.beta;
             }
         }
-        float out[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float f = (float)a1[r] * c1v[r];
-            if (TWO) f = __builtin_fmaf((float)a2[r], c2v[r], f);
-            const float prev = block == 0 ? cold[r] : runv[r];
-            out[r] = (block == 0 && beta_zero) ? f * as : __builtin_fmaf(f, as, prev);
-            runv[r] = out[r];
-        }
-        if (last && ok) {
-            if (g.c_vec4) {
-                *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
-            } else {
+        for (int i = 0; i < FN; i++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) cp[r] = out[r];
+            for (int j = 0; j < FM; j++) {
+                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                float out[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float f = (float)acc[i][j][r] * c1v[i][r];
+                    if (TWO) f = __builtin_fmaf((float)accT[TWO ? i : 0][TWO ? j : 0][r], c2v[TWO ? i : 0][r], f);
+                    const float prev = block == 0 ? cold[i][j][r] : runv[i][j][r];
+                    out[r] = (block == 0 && beta_zero) ? f * asv[j] : __builtin_fmaf(f, asv[j], prev);
+                    if (MULTI) runv[i][j][r] = out[r];
+                }
+                acc[i][j] = v4i{0, 0, 0, 0};
+                if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+                if (last && n < N && m < M) {
+                    float *cp = g.C + (size_t)m * g.ldc + n;
+                    if (g.c_vec4) {
+                        *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cp[r] = out[r];
+                    }
+                }
             }
-        }
     };
 
     /* Per-lane byte offsets of this thread's loads, fixed for the whole K loop: a stage adds a uniform base, so the
@@ -486,19 +511,7 @@ void gemm_i8(GemmArgs g)
             if (t + 1 < nk) store_stage(t + 1, buf ^ 1);
             if (OUT == OUT_F32 && !SPLIT) {
                 const bool last = t + 1 == nk;
-                if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
-#pragma unroll
-                    for (int i = 0; i < FN; i++)
-#pragma unroll
-                        for (int j = 0; j < FM; j++) {
-                            float tmp[4];
-                            float *rv = MULTI ? run[MULTI ? i : 0][MULTI ? j : 0] : tmp;
-                            fold_one(block, last, i, j, acc[i][j], TWO ? accT[TWO ? i : 0][TWO ? j : 0] : acc[i][j], rv);
-                            acc[i][j] = v4i{0, 0, 0, 0};
-                            if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
-                        }
-                    block++;
-                }
+                if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) fold_all(block++, last, run);
             }
             __syncthreads();
         }
