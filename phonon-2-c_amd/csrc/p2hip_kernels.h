@@ -301,63 +301,6 @@ void gemm_i8(GemmArgs g)
 #pragma unroll
     for (int j = 0; j < FM; j++) asv[j] = (OUT == OUT_F32 && !SPLIT) ? g.a_scales[min(m_lane + 16 * j, M - 1)] * g.alpha : 0.0f;
 
-    /* One fold of a K block into every output of the lane (blas.c:1355-1366): f = (float)accS · c1
-     * (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta 0) or fmaf(f, as, beta-scaled C), later blocks
-     * fmaf(f, as, running); `last` stores C. The beta reads of C are all issued before any is used. */
-    auto fold_all = [&](int block, bool last, float (*runv)[FM][4]) {
-        float cold[FN][FM][4];
-        if (block == 0 && !beta_zero) {
-#pragma unroll
-            for (int i = 0; i < FN; i++)
-#pragma unroll
-                for (int j = 0; j < FM; j++) {
-                    const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
-                    const float *cp = g.C + (size_t)m * g.ldc + n;
-                    if (g.c_vec4) {
-                        float4 v = *reinterpret_cast<const float4 *>(cp);
-                        cold[i][j][0] = v.x; cold[i][j][1] = v.y; cold[i][j][2] = v.z; cold[i][j][3] = v.w;
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) cold[i][j][r] = cp[r];
-                    }
-                }
-            if (g.beta != 1.0f) {
-#pragma unroll
-                for (int i = 0; i < FN; i++)
-#pragma unroll
-                    for (int j = 0; j < FM; j++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) cold[i][j][r] = cold[i][j][r] * g.beta;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < FN; i++)
-#pragma unroll
-            for (int j = 0; j < FM; j++) {
-                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
-                float out[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    float f = (float)acc[i][j][r] * c1v[i][r];
-                    if (TWO) f = __builtin_fmaf((float)accT[TWO ? i : 0][TWO ? j : 0][r], c2v[TWO ? i : 0][r], f);
-                    const float prev = block == 0 ? cold[i][j][r] : runv[i][j][r];
-                    out[r] = (block == 0 && beta_zero) ? f * asv[j] : __builtin_fmaf(f, asv[j], prev);
-                    if (MULTI) runv[i][j][r] = out[r];
-                }
-                acc[i][j] = v4i{0, 0, 0, 0};
-                if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
-                if (last && n < N && m < M) {
-                    float *cp = g.C + (size_t)m * g.ldc + n;
-                    if (g.c_vec4) {
-                        *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; r++) cp[r] = out[r];
-                    }
-                }
-            }
-    };
-
     /* Per-lane byte offsets of this thread's loads, fixed for the whole K loop: a stage adds a uniform base, so the
      * loads address as (scalar base + 32-bit lane offset). */
     uint32_t a_off[G::A_PER], s_off[G::B_PER][4], f_off[G::B_PER][4], b8_off[G::B_PER][4];
@@ -511,7 +454,62 @@ void gemm_i8(GemmArgs g)
             if (t + 1 < nk) store_stage(t + 1, buf ^ 1);
             if (OUT == OUT_F32 && !SPLIT) {
                 const bool last = t + 1 == nk;
-                if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) fold_all(block++, last, run);
+                if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
+                    /* Fold this K block into every output of the lane (blas.c:1355-1366): f = (float)accS · c1
+                     * (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta 0) or fmaf(f, as, beta-scaled C),
+                     * later blocks fmaf(f, as, running); the last fold stores C. The beta reads of C are all issued
+                     * before any is used. */
+#pragma unroll
+                    for (int i = 0; i < FN; i++) {
+                        /* beta reads of this column group's outputs, all issued before any is used */
+                        float cold[FM][4];
+                        if (block == 0 && !beta_zero) {
+#pragma unroll
+                            for (int j = 0; j < FM; j++) {
+                                const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
+                                const float *cp = g.C + (size_t)m * g.ldc + n;
+                                if (g.c_vec4) {
+                                    const float4 v = *reinterpret_cast<const float4 *>(cp);
+                                    cold[j][0] = v.x; cold[j][1] = v.y; cold[j][2] = v.z; cold[j][3] = v.w;
+                                } else {
+#pragma unroll
+                                    for (int r = 0; r < 4; r++) cold[j][r] = cp[r];
+                                }
+                            }
+                            if (g.beta != 1.0f) {
+#pragma unroll
+                                for (int j = 0; j < FM; j++)
+#pragma unroll
+                                    for (int r = 0; r < 4; r++) cold[j][r] = cold[j][r] * g.beta;
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < FM; j++) {
+                            const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                            float out[4];
+#pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                float f = (float)acc[i][j][r] * c1v[i][r];
+                                if (TWO) f = __builtin_fmaf((float)accT[TWO ? i : 0][TWO ? j : 0][r], c2v[TWO ? i : 0][r], f);
+                                const float prev = block == 0 ? cold[j][r] : run[MULTI ? i : 0][j][r];
+                                out[r] = (block == 0 && beta_zero) ? f * asv[j] : __builtin_fmaf(f, asv[j], prev);
+                                if (MULTI) run[MULTI ? i : 0][j][r] = out[r];
+                            }
+                            acc[i][j] = v4i{0, 0, 0, 0};
+                            if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+                            if (last && n < N && m < M) {
+                                float *cp = g.C + (size_t)m * g.ldc + n;
+                                if (g.c_vec4) {
+                                    *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
+                                } else {
+#pragma unroll
+                                    for (int r = 0; r < 4; r++) cp[r] = out[r];
+                                }
+                            }
+                        }
+                    }
+                    block++;
+                }
             }
             __syncthreads();
         }
