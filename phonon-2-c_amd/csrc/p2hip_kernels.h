@@ -19,6 +19,7 @@
 namespace p2k {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 enum { MODE_INT8 = 0, MODE_EXACT = 1, MODE_INT8W = 2, MODE_Q8B = 3 };
 enum { OUT_F32 = 0, OUT_ACC = 1 };
@@ -240,10 +241,11 @@ __device__ __forceinline__ void tile_of(const GemmArgs &g, int &tile_n, int &til
  *  the running sum when K > 1024); with SPLIT, each workgroup writes its int32 partial sums and fold_splits, the
  *  next kernel on the stream, adds them per block (exact in int32) and folds the blocks in order. */
 template <class G, int MODE, int OUT, bool MULTI, bool SPLIT>
-__global__ __launch_bounds__(G::NT, ((MODE == MODE_INT8 || MULTI || G::NT > 256 || 2 * G::LDS_ONE > 160 * 1024) ? 1 : 2))
+__global__ __launch_bounds__(G::NT, ((MODE == MODE_INT8 || MULTI || G::NT > 256 || 2 * (G::LDS_ONE + 2048) > 160 * 1024) ? 1 : 2))
 void gemm_i8(GemmArgs g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
+    constexpr bool FOLD = OUT == OUT_F32 && !SPLIT;   /* this kernel folds into fp32 C itself */
     constexpr int FN = G::FN, FM = G::FM, BK = G::BK, SB = G::SB;
     __shared__ __attribute__((aligned(16))) int8_t sm[2 * G::A_BYTES + (TWO ? 4 : 2) * G::B_BYTES];
     auto smA = [&](int b) { return sm + b * G::A_BYTES; };
@@ -272,7 +274,7 @@ void gemm_i8(GemmArgs g)
     }
 
     v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
-    float run[MULTI ? FN : 1][FM][4];
+    float run[FOLD ? FN : 1][FOLD ? FM : 1][4];   /* fp32 outputs; with MULTI the running sum over K blocks */
 #pragma unroll
     for (int i = 0; i < FN; i++)
 #pragma unroll
@@ -286,20 +288,30 @@ void gemm_i8(GemmArgs g)
     const int m_lane = m0 + wm * (G::BM / G::WM) + (lane & 15);
     const bool beta_zero = g.beta == 0.0f;
 
-    /* Epilogue factors of this lane, loaded before the K loop so their latency hides behind it: c1 (and c2) of its
-     * 4·FN columns, as = a_scale·alpha of its FM rows. */
-    float c1v[FN][4], c2v[TWO ? FN : 1][4], asv[FM];
-#pragma unroll
-    for (int i = 0; i < FN; i++) {
-        const int nc = min(n_lane + 16 * i, N - 4);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            c1v[i][r] = g.c1[nc + r];
-            if (TWO) c2v[TWO ? i : 0][r] = g.c2[nc + r];
+    /* Epilogue factors of the tile – c1 (and c2) of its BN columns, as = a_scale·alpha of its BM rows – are loaded
+     * into registers here, written to LDS with stage 0 and read from LDS by the fold, so no epilogue wait involves
+     * the vector-memory counter that the C stores occupy. */
+    static_assert(G::NT >= G::BN && G::NT >= G::BM, "one factor per thread");
+    __shared__ __attribute__((aligned(16))) float f_c1[FOLD ? G::BN : 4], f_c2[FOLD && TWO ? G::BN : 4],
+        f_as[FOLD ? G::BM : 4];
+    float r_c1 = 0.0f, r_c2 = 0.0f, r_as = 0.0f;
+    if (FOLD) {
+        if (tid < G::BN) {
+            const int n = min(n0 + tid, N - 1);
+            r_c1 = g.c1[n];
+            if (TWO) r_c2 = g.c2[n];
         }
+        if (tid < G::BM) r_as = g.a_scales[min(m0 + tid, M - 1)] * g.alpha;
     }
-#pragma unroll
-    for (int j = 0; j < FM; j++) asv[j] = (OUT == OUT_F32 && !SPLIT) ? g.a_scales[min(m_lane + 16 * j, M - 1)] * g.alpha : 0.0f;
+    auto put_factors = [&]() {
+        if (FOLD) {
+            if (tid < G::BN) {
+                f_c1[tid] = r_c1;
+                if (TWO) f_c2[tid] = r_c2;
+            }
+            if (tid < G::BM) f_as[tid] = r_as;
+        }
+    };
 
     /* Per-lane byte offsets of this thread's loads, fixed for the whole K loop: a stage adds a uniform base, so the
      * loads address as (scalar base + 32-bit lane offset). */
@@ -327,6 +339,55 @@ void gemm_i8(GemmArgs g)
      * every address in bounds and mask the out-of-range values when they are written to LDS. Either way no load is
      * conditional, and none is waited on before the MFMAs of the current stage are issued. */
     const bool interior = m0 + G::BM <= M && n0 + G::BN <= N && (k_end - k_begin) % BK == 0;
+
+    /* Fold one 1024-row K block into the lane's outputs (blas.c:1355-1366): f = (float)accS · c1 (+ fmaf((float)accT,
+     * c2, f)); block 0 gives f · as (beta 0) or fmaf(f, as, beta-scaled C), later blocks fmaf(f, as, running). The
+     * beta reads of C are the only global accesses and are issued before any store of this workgroup. */
+    int block = 0;
+    auto fold = [&](int blk) __attribute__((always_inline)) {
+        const bool first = blk == 0;
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+            const int nl = wn * (G::BN / G::WN) + 16 * i + 4 * (lane >> 4);
+            const v4f c1 = *reinterpret_cast<const v4f *>(f_c1 + nl);
+            v4f c2 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (TWO) c2 = *reinterpret_cast<const v4f *>(f_c2 + nl);
+            float cold[FM][4];
+            if (first && !beta_zero) {
+#pragma unroll
+                for (int j = 0; j < FM; j++) {
+                    const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
+                    const float *cp = g.C + (size_t)m * g.ldc + n;
+                    if (g.c_vec4) {
+                        const v4f v = *reinterpret_cast<const v4f *>(cp);
+                        cold[j][0] = v[0]; cold[j][1] = v[1]; cold[j][2] = v[2]; cold[j][3] = v[3];
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[j][r] = cp[r];
+                    }
+                }
+                if (g.beta != 1.0f) {
+#pragma unroll
+                    for (int j = 0; j < FM; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[j][r] = cold[j][r] * g.beta;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const float as = f_as[wm * (G::BM / G::WM) + 16 * j + (lane & 15)];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float f = (float)acc[i][j][r] * c1[r];
+                    if (TWO) f = __builtin_fmaf((float)accT[TWO ? i : 0][TWO ? j : 0][r], c2[r], f);
+                    const float prev = first ? cold[j][r] : run[FOLD ? i : 0][FOLD ? j : 0][r];
+                    run[FOLD ? i : 0][FOLD ? j : 0][r] = (first && beta_zero) ? f * as : __builtin_fmaf(f, as, prev);
+                }
+                acc[i][j] = v4i{0, 0, 0, 0};
+                if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+            }
+        }
+    };
 
     auto body = [&](auto edge_tag) {
         constexpr bool EDGE = decltype(edge_tag)::value;
@@ -418,9 +479,9 @@ void gemm_i8(GemmArgs g)
             load_stage(0);
             store_stage(0, 0);
         }
+        put_factors();
         __syncthreads();
 
-        int block = 0;
         for (int t = 0; t < nk; t++) {
             const int buf = t & 1;
             if (t + 1 < nk) load_stage(t + 1);
@@ -452,70 +513,45 @@ void gemm_i8(GemmArgs g)
                     }
             }
             if (t + 1 < nk) store_stage(t + 1, buf ^ 1);
-            if (OUT == OUT_F32 && !SPLIT) {
-                const bool last = t + 1 == nk;
-                if (MULTI ? ((((t + 1) * BK) % kFoldRows == 0) || last) : last) {
-                    /* Fold this K block into every output of the lane (blas.c:1355-1366): f = (float)accS · c1
-                     * (+ fmaf((float)accT, c2, f)); block 0 stores f · as (beta 0) or fmaf(f, as, beta-scaled C),
-                     * later blocks fmaf(f, as, running); the last fold stores C. The beta reads of C are all issued
-                     * before any is used. */
-#pragma unroll
-                    for (int i = 0; i < FN; i++) {
-                        /* beta reads of this column group's outputs, all issued before any is used */
-                        float cold[FM][4];
-                        if (block == 0 && !beta_zero) {
-#pragma unroll
-                            for (int j = 0; j < FM; j++) {
-                                const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
-                                const float *cp = g.C + (size_t)m * g.ldc + n;
-                                if (g.c_vec4) {
-                                    const float4 v = *reinterpret_cast<const float4 *>(cp);
-                                    cold[j][0] = v.x; cold[j][1] = v.y; cold[j][2] = v.z; cold[j][3] = v.w;
-                                } else {
-#pragma unroll
-                                    for (int r = 0; r < 4; r++) cold[j][r] = cp[r];
-                                }
-                            }
-                            if (g.beta != 1.0f) {
-#pragma unroll
-                                for (int j = 0; j < FM; j++)
-#pragma unroll
-                                    for (int r = 0; r < 4; r++) cold[j][r] = cold[j][r] * g.beta;
-                            }
-                        }
-#pragma unroll
-                        for (int j = 0; j < FM; j++) {
-                            const int n = n_lane + 16 * i, m = m_lane + 16 * j;
-                            float out[4];
-#pragma unroll
-                            for (int r = 0; r < 4; r++) {
-                                float f = (float)acc[i][j][r] * c1v[i][r];
-                                if (TWO) f = __builtin_fmaf((float)accT[TWO ? i : 0][TWO ? j : 0][r], c2v[TWO ? i : 0][r], f);
-                                const float prev = block == 0 ? cold[j][r] : run[MULTI ? i : 0][j][r];
-                                out[r] = (block == 0 && beta_zero) ? f * asv[j] : __builtin_fmaf(f, asv[j], prev);
-                                if (MULTI) run[MULTI ? i : 0][j][r] = out[r];
-                            }
-                            acc[i][j] = v4i{0, 0, 0, 0};
-                            if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
-                            if (last && n < N && m < M) {
-                                float *cp = g.C + (size_t)m * g.ldc + n;
-                                if (g.c_vec4) {
-                                    *reinterpret_cast<float4 *>(cp) = make_float4(out[0], out[1], out[2], out[3]);
-                                } else {
-#pragma unroll
-                                    for (int r = 0; r < 4; r++) cp[r] = out[r];
-                                }
-                            }
-                        }
-                    }
-                    block++;
-                }
+            if (FOLD && MULTI && t + 1 < nk && ((t + 1) * BK) % kFoldRows == 0) {
+                fold(block);
+                block++;
             }
             __syncthreads();
         }
     };
     if (interior) body(std::false_type{});
     else body(std::true_type{});
+
+    if (FOLD) {
+        if (nk == 0) return;
+        fold(block);
+        /* every output of the lane is final: one burst of 16-byte stores, nothing waited on after it */
+        if (g.c_vec4) {
+#pragma unroll
+            for (int i = 0; i < FN; i++)
+#pragma unroll
+                for (int j = 0; j < FM; j++) {
+                    const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                    if (m < M && n < N)
+                        *reinterpret_cast<v4f *>(g.C + (size_t)m * g.ldc + n) =
+                            v4f{run[i][j][0], run[i][j][1], run[i][j][2], run[i][j][3]};
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FN; i++)
+#pragma unroll
+                for (int j = 0; j < FM; j++) {
+                    const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                    if (m < M && n < N) {
+                        float *cp = g.C + (size_t)m * g.ldc + n;
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cp[r] = run[i][j][r];
+                    }
+                }
+        }
+        return;
+    }
 
     if (OUT == OUT_ACC) {
 #pragma unroll
