@@ -64,7 +64,7 @@ class Scratch:
 
     def __init__(self, M, K, split_bytes):
         self.ldq = P.q_ld(K)
-        self.q = P.DeviceBuffer(M * self.ldq)
+        self.q = P.DeviceBuffer(P.q_bytes(M, K))
         self.s = P.DeviceBuffer(M * 4)
         self.ws = P.Workspace(split_bytes)
 
@@ -72,12 +72,13 @@ class Scratch:
 def run_linear(lin, dA, lda, ws, stream, alpha=None, events=None):
     """quantise A, then the q8a GEMM; events (e0, e1, e2) bracket the two kernels when given."""
     a = lin.alpha if alpha is None else alpha
+    ldq = P.q_ld(lin.K)   # the linear's own row pitch: the shared buffer is sized for the widest
     if events:
         events[0].record(stream.ptr)
-    P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ws.ldq, ws.s.ptr, stream.ptr)
+    P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr)
     if events:
         events[1].record(stream.ptr)
-    P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, a, ws.q.ptr, ws.ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr,
+    P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, a, ws.q.ptr, ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr,
                        lin.N, ws.ws.ptr, ws.ws.nbytes, stream.ptr)
     if events:
         events[2].record(stream.ptr)

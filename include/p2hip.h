@@ -96,11 +96,15 @@ int p2h_fv_pack_codes(const P2hWeight *w, signed char *d_codes, void *stream);
 /* ── activations ─────────────────────────────────────────────────────────────────────────────────────────────── */
 
 /* Per-row int8 quantisation (blas.c:1114-1145): scale = amax/127 (1 for a zero row), q = round-half-even(x/scale
- * as x·(1/scale)) saturated, the K % 16 tail as lrintf(x/scale) clamped to ±127. Q is [M][ldq] int8 with
- * ldq % 16 == 0 and ldq >= roundup(K, P2H_Q_KALIGN); columns K..roundup(K, P2H_Q_KALIGN)-1 are written as 0.
- * K % 4 == 0. */
+ * as x·(1/scale)) saturated, the K % 16 tail as lrintf(x/scale) clamped to ±127. K % 4 == 0.
+ * Q is stored tiled for the matrix cores, as the reference's QuantA.q is private to its GEMM (blas.c:1151-1154):
+ * rows are padded to Mp = roundup(M, 16) and columns to ldq (a multiple of P2H_Q_KALIGN, >= roundup(K,
+ * P2H_Q_KALIGN)), pads written as 0, and byte (m, k) sits at
+ *     ((m/16)·(ldq/64) + k/64)·1024 + ((k%64)/16·16 + m%16)·16 + k%16,
+ * i.e. one 1 KB block per 16 rows × 64 columns. The buffer holds Mp·ldq bytes (p2h_q_bytes for ldq = p2h_q_ld). */
 int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int ldq, float *dScales, void *stream);
-int p2h_q_ld(int K);   /* the smallest valid ldq for K */
+int p2h_q_ld(int K);              /* the smallest valid ldq for K */
+size_t p2h_q_bytes(int M, int K); /* bytes of Q for M rows at ldq = p2h_q_ld(K) */
 
 /* ── the five-value GEMM ─────────────────────────────────────────────────────────────────────────────────────── */
 

@@ -94,6 +94,8 @@ struct P2hWeight {
     const float *lo, *hi;
     uint8_t *clo;
     float *c1w, *c2;
+    uint8_t *rec;     /* operand records of the int8 routes (fv_repack): [N/16][units][64 lanes][12 B] */
+    int units;        /* 128-row K units: K rounded up / 128 */
     void *own;        /* the one device allocation this handle made */
     size_t own_bytes;
 };
@@ -329,6 +331,8 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     size_t off_clo = off; off += align_up((size_t)N, 256);
     size_t off_c1 = off; off += align_up((size_t)N * 4, 256);
     size_t off_c2 = off; off += align_up((size_t)N * 4, 256);
+    const int units = (K + 127) / 128;
+    size_t off_rec = off; off += align_up((size_t)(N / 16) * units * 768 + 16, 256);
     void *base = nullptr;
     if (hipMalloc(&base, off) != hipSuccess) {
         fail(P2H_E_NOMEM, "five-value weight: hipMalloc(%zu) failed", off);
@@ -346,6 +350,8 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     w->clo = b + off_clo;
     w->c1w = (float *)(b + off_c1);
     w->c2 = (float *)(b + off_c2);
+    w->rec = b + off_rec;
+    w->units = units;
     w->own = base;
     w->own_bytes = off;
     return w;
@@ -357,6 +363,12 @@ static int weight_tables(P2hWeight *w)
     hipLaunchKernelGGL(p2k::fv_tables, dim3((w->N + 255) / 256), dim3(256), 0, s, w->N, w->lo, w->hi, w->clo,
                        w->c1w, w->c2);
     HIPCHK(hipGetLastError());
+    const size_t recs = (size_t)(w->N / 16) * w->units * 64;
+    if (recs > 0) {
+        hipLaunchKernelGGL(p2k::fv_repack, dim3((unsigned)((recs + 255) / 256)), dim3(256), 0, s, w->K, w->N,
+                           w->units, w->signs, w->flags, (uint32_t *)w->rec);
+        HIPCHK(hipGetLastError());
+    }
     HIPCHK(hipStreamSynchronize(s));
     return P2H_OK;
 }
@@ -442,18 +454,42 @@ int p2h_fv_pack_codes(const P2hWeight *w, signed char *d_codes, void *stream)
 
 int p2h_q_ld(int K) { return (int)align_up((size_t)(K > 0 ? K : 0), P2H_Q_KALIGN); }
 
+size_t p2h_q_bytes(int M, int K)
+{
+    if (M <= 0 || K <= 0) return 0;
+    return align_up((size_t)M, 16) * (size_t)p2h_q_ld(K);
+}
+
 int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int ldq, float *dScales, void *stream)
 {
     if (int rc = ensure_init()) return rc;
     if (M < 0 || K < 0 || K % 4 != 0) return fail(P2H_E_ARG, "p2h_quant_rows: K = %d must be a multiple of 4", K);
     if (M == 0) return P2H_OK;
     if (!dA || !dQ || !dScales || lda < K) return fail(P2H_E_ARG, "p2h_quant_rows: bad pointer or lda");
-    if (ldq < p2h_q_ld(K) || ldq % 16 != 0 || !aligned(dQ, 16))
-        return fail(P2H_E_ARG, "p2h_quant_rows: ldq = %d must be >= %d, a multiple of 16, Q 16-byte aligned", ldq,
-                    p2h_q_ld(K));
-    int vec_ok = (lda % 4 == 0) && aligned(dA, 16);
-    hipLaunchKernelGGL(p2k::quant_rows, dim3((M + 3) / 4), dim3(256), 0, stream_of(stream), M, K, p2h_q_ld(K), dA,
-                       lda, vec_ok, (int8_t *)dQ, ldq, dScales);
+    if (ldq < p2h_q_ld(K) || ldq % P2H_Q_KALIGN != 0 || !aligned(dQ, 16))
+        return fail(P2H_E_ARG, "p2h_quant_rows: ldq = %d must be >= %d and a multiple of %d, Q 16-byte aligned",
+                    ldq, p2h_q_ld(K), P2H_Q_KALIGN);
+    const int vec_ok = (lda % 4 == 0) && aligned(dA, 16);
+    const int Mp = (int)align_up((size_t)M, 16);
+    const dim3 grid((unsigned)((Mp + 3) / 4)), block(256);
+    hipStream_t s = stream_of(stream);
+    auto launch = [&](auto nch_tag, auto vec_tag) {
+        constexpr int NCH = decltype(nch_tag)::value;
+        constexpr bool VEC = decltype(vec_tag)::value;
+        hipLaunchKernelGGL((p2k::quant_rows<NCH, VEC>), grid, block, 0, s, M, Mp, K, dA, lda, (int8_t *)dQ, ldq,
+                           dScales);
+    };
+    auto by_width = [&](auto vec_tag) {
+        switch ((ldq + 1023) / 1024) {   /* row chunks per lane kept in registers (0: the row is read twice) */
+        case 1: launch(std::integral_constant<int, 1>{}, vec_tag); break;
+        case 2: launch(std::integral_constant<int, 2>{}, vec_tag); break;
+        case 3: launch(std::integral_constant<int, 3>{}, vec_tag); break;
+        case 4: launch(std::integral_constant<int, 4>{}, vec_tag); break;
+        default: launch(std::integral_constant<int, 0>{}, vec_tag); break;
+        }
+    };
+    if (vec_ok) by_width(std::true_type{});
+    else by_width(std::false_type{});
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -476,9 +512,9 @@ static int check_q(const char *who, int M, int K, const signed char *dQ, int ldq
 {
     if (M < 0 || K < 0 || K % 4 != 0) return fail(P2H_E_ARG, "%s: K = %d must be a multiple of 4", who, K);
     if (M > 0 && (!dQ || !dScales)) return fail(P2H_E_ARG, "%s: NULL activations", who);
-    if (M > 0 && (ldq < p2h_q_ld(K) || ldq % 16 != 0 || !aligned(dQ, 16)))
-        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d and a multiple of 16, Q 16-byte aligned", who, ldq,
-                    p2h_q_ld(K));
+    if (M > 0 && (ldq < p2h_q_ld(K) || ldq % P2H_Q_KALIGN != 0 || !aligned(dQ, 16)))
+        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d and a multiple of %d, Q 16-byte aligned", who, ldq,
+                    p2h_q_ld(K), P2H_Q_KALIGN);
     return P2H_OK;
 }
 
@@ -488,18 +524,23 @@ static int check_q(const char *who, int M, int K, const signed char *dQ, int ldq
 
 namespace {
 
-/* Tile configurations: activation rows × weight columns per workgroup, waves (m × n), K rows per stage. */
+/* Five-value tiles (gemm_fv): FM 16-row groups × FN 16-column groups per wave, 4 waves side by side along N, an LDS
+ * ring of 4 stages of 128 K rows. */
+using FvT = p2k::FvGeo<2, 1, 4, 4>;   /*  32 ×  64 */
+using FvS = p2k::FvGeo<4, 1, 4, 4>;   /*  64 ×  64 */
+using FvM = p2k::FvGeo<4, 2, 4, 4>;   /*  64 × 128 */
+using FvL = p2k::FvGeo<8, 2, 4, 4>;   /* 128 × 128 */
+using FvX = p2k::FvGeo<8, 4, 4, 4>;   /* 128 × 256 (int8w only: the two-plane mode would need twice the accumulators) */
+using FvT8 = p2k::FvGeo<2, 1, 4, 8>;  /*  32 ×  64, 8 stages in flight */
+using FvS8 = p2k::FvGeo<4, 1, 4, 8>;  /*  64 ×  64, 8 stages in flight */
+using FvT6 = p2k::FvGeo<2, 1, 4, 6>;  /*  32 ×  64, 6 stages in flight */
+enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_COUNT = 8 };
+const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM};
+const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN};
+
+/* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
 using G128 = p2k::Geo<128, 128, 2, 2, 128>;
-using G256x128 = p2k::Geo<256, 128, 2, 2, 128>;
-using G128x256 = p2k::Geo<128, 256, 2, 2, 128>;
-using G64k512 = p2k::Geo<64, 64, 2, 2, 512>;
-using G64x128 = p2k::Geo<64, 128, 2, 2, 256>;
-
-enum { CFG_64 = 0, CFG_128 = 1, CFG_256x128 = 2, CFG_128x256 = 3, CFG_64K512 = 4, CFG_64x128 = 5, CFG_COUNT = 6 };
-const int kCfgBM[CFG_COUNT] = {64, 128, 256, 128, 64, 64};
-const int kCfgBN[CFG_COUNT] = {64, 128, 128, 256, 64, 128};
-const int kCfgBK[CFG_COUNT] = {256, 128, 128, 128, 512, 256};
 
 struct Plan {
     int cfg, splits, split_rows, tiles_m, tiles_n;
@@ -512,30 +553,29 @@ int env_int(const char *name, int dflt)
     return (v && *v) ? atoi(v) : dflt;
 }
 
-/* Tile and K split for one call. A split is a whole number of stages inside one 1024-row fold block; it runs only
- * with a workspace, for K > 1024 and output grids short of the CU count (its int32 partials cost splits × M × N × 4
- * bytes of traffic, worth it only where the output is small next to K). P2H_TILE and P2H_SPLIT_ROWS (−1: never)
- * override the choice for tuning. */
+/* Tile and K split of a five-value call. A split is a whole number of 128-row units inside one 1024-row fold block;
+ * it runs only with a workspace, for K > 1024 (its int32 partials cost splits × M × N × 4 bytes of traffic, worth
+ * it only where the output is small next to K). P2H_TILE and P2H_SPLIT_ROWS (−1: never) override the choice. */
 Plan make_plan(int mode, int M, int N, int K, bool can_split)
 {
     Plan p;
-    /* measured on MI355X: 64×64 tiles with 256-row stages win up to a thousand rows, 128×128 beyond */
-    int cfg = M <= 1024 ? CFG_64 : CFG_128;
+    /* measured on MI355X: 32 × 64 tiles are the fastest up to a thousand rows, 128 × 256 beyond */
+    int cfg = M <= 1024 ? FV_T : FV_X;
     cfg = env_int("P2H_TILE", cfg);
-    if (cfg < 0 || cfg >= CFG_COUNT || (mode != P2H_INT8W && cfg != CFG_64 && cfg != CFG_128)) cfg = CFG_128;
+    if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
+    if (mode == P2H_INT8 && cfg == FV_X) cfg = FV_L;
     p.cfg = cfg;
-    p.tiles_m = (M + kCfgBM[cfg] - 1) / kCfgBM[cfg];
-    p.tiles_n = (N + kCfgBN[cfg] - 1) / kCfgBN[cfg];
+    p.tiles_m = (M + kFvBM[cfg] - 1) / kFvBM[cfg];
+    p.tiles_n = (N + kFvBN[cfg] - 1) / kFvBN[cfg];
     const int tiles = p.tiles_m * p.tiles_n;
     const int cus = g_cus > 0 ? g_cus : 256;
     p.splits = 1;
     p.split_rows = K > 0 ? K : 1;
-    int rows = 0;   /* K > 1024 splits per fold block: measured faster than folding in registers at every M */
+    int rows = 0;
     if (K > p2k::kFoldRows) rows = (M <= 64 && tiles * (K / 512) <= 2 * cus) ? 512 : p2k::kFoldRows;
     const int forced = env_int("P2H_SPLIT_ROWS", 0);
     if (forced < 0) rows = 0;
-    else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0) rows = forced;
-    if (rows > 0 && rows % kCfgBK[cfg] != 0) rows = 0;
+    else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0 && forced % 128 == 0) rows = forced;
     if (can_split && K > 0 && rows > 0 && (K + rows - 1) / rows > 1) {
         p.split_rows = rows;
         p.splits = (K + rows - 1) / rows;
@@ -554,6 +594,9 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
     g.alpha = alpha; g.beta = beta;
     g.Q = (const int8_t *)dQ; g.ldq = ldq; g.a_scales = dScales;
     g.kq = (int)align_up((size_t)K, P2H_Q_KALIGN);
+    g.kst = ldq / 64;
+    g.mg_last = (int)(align_up((size_t)M, 16) / 16) - 1;
+    g.ng_last = N / 16 - 1;
     g.C = dC; g.ldc = ldc;
     g.c_vec4 = dC && (ldc % 4 == 0) && aligned(dC, 16);
     g.tiles_n = p.tiles_n; g.tiles_m = p.tiles_m;
@@ -563,32 +606,33 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
 }
 
 template <class G, int MODE>
-void launch_f32(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
+void launch_fv(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n * p.splits)), block(G::NT);
     if (p.splits > 1) {
-        hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, false, true>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<G, MODE, p2k::OUT_F32, false, true>), grid, block, 0, s, g);
         const size_t quads = (size_t)g.M * (g.N / 4);
         hipLaunchKernelGGL((p2k::fold_splits<MODE == p2k::MODE_INT8>), dim3((unsigned)((quads + 255) / 256)),
                            dim3(256), 0, s, g);
     } else if (g.K > p2k::kFoldRows) {
-        hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, true, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<G, MODE, p2k::OUT_F32, true, false>), grid, block, 0, s, g);
     } else {
-        hipLaunchKernelGGL((p2k::gemm_i8<G, MODE, p2k::OUT_F32, false, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<G, MODE, p2k::OUT_F32, false, false>), grid, block, 0, s, g);
     }
 }
 
 template <int MODE>
-void launch_f32_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
+void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
-    constexpr int W = p2k::MODE_INT8W;
     switch (p.cfg) {
-    case CFG_64: launch_f32<G64, MODE>(g, p, s); break;
-    case CFG_256x128: if (MODE == W) launch_f32<G256x128, W>(g, p, s); break;
-    case CFG_128x256: if (MODE == W) launch_f32<G128x256, W>(g, p, s); break;
-    case CFG_64K512: if (MODE == W) launch_f32<G64k512, W>(g, p, s); break;
-    case CFG_64x128: if (MODE == W) launch_f32<G64x128, W>(g, p, s); break;
-    default: launch_f32<G128, MODE>(g, p, s); break;
+    case FV_T: launch_fv<FvT, MODE>(g, p, s); break;
+    case FV_S: launch_fv<FvS, MODE>(g, p, s); break;
+    case FV_M: launch_fv<FvM, MODE>(g, p, s); break;
+    case FV_T8: launch_fv<FvT8, MODE>(g, p, s); break;
+    case FV_S8: launch_fv<FvS8, MODE>(g, p, s); break;
+    case FV_T6: launch_fv<FvT6, MODE>(g, p, s); break;
+    case FV_X: if (MODE == p2k::MODE_INT8W) { launch_fv<FvX, p2k::MODE_INT8W>(g, p, s); break; } /* fall through */
+    default: launch_fv<FvL, MODE>(g, p, s); break;
     }
 }
 
@@ -609,8 +653,8 @@ const char *p2h_fvb_plan(int mode, int M, int N, int K, int with_workspace)
     static thread_local char buf[160];
     if (ensure_init() || M <= 0 || N <= 0 || K <= 0) return "";
     Plan p = make_plan(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K, with_workspace != 0);
-    snprintf(buf, sizeof buf, "tile %dx%d k%d, %d split%s of %d rows%s", kCfgBM[p.cfg], kCfgBN[p.cfg],
-             kCfgBK[p.cfg], p.splits, p.splits > 1 ? "s" : "", p.split_rows,
+    snprintf(buf, sizeof buf, "tile %dx%d, %d split%s of %d rows%s", kFvBM[p.cfg], kFvBN[p.cfg], p.splits,
+             p.splits > 1 ? "s" : "", p.split_rows,
              p.splits > 1 ? " + fold" : (K > p2k::kFoldRows ? ", folds in registers" : ""));
     return buf;
 }
@@ -641,13 +685,13 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
     Plan p = make_plan(mode, M, N, K, workspace != nullptr);
     if (int rc = check_split_ws("p2h_fvb_gemm_q8a", p, workspace, workspace_bytes)) return rc;
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
-    g.signs = w->signs; g.flags = w->flags; g.clo = w->clo;
+    g.rec = w->rec; g.units = w->units; g.clo = w->clo;
     if (mode == P2H_INT8W) {
         g.c1 = w->c1w;
-        launch_f32_cfg<p2k::MODE_INT8W>(g, p, s);
+        launch_fv_cfg<p2k::MODE_INT8W>(g, p, s);
     } else {
         g.c1 = w->lo; g.c2 = w->c2;
-        launch_f32_cfg<p2k::MODE_INT8>(g, p, s);
+        launch_fv_cfg<p2k::MODE_INT8>(g, p, s);
     }
     HIPCHK(hipGetLastError());
     return P2H_OK;
@@ -666,20 +710,20 @@ int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ld
         return fail(P2H_E_ARG, "p2h_fvb_acc_i32: accumulators must be 16-byte aligned with ldacc %% 4 == 0");
     if (M == 0) return P2H_OK;
     Plan p = make_plan(mode, M, N, K, false);
-    p.cfg = CFG_128;
-    p.tiles_m = (M + 127) / 128;
-    p.tiles_n = (N + 127) / 128;
+    p.cfg = FV_L;
+    p.splits = 1;
+    p.split_rows = K;
+    p.tiles_m = (M + FvL::BM - 1) / FvL::BM;
+    p.tiles_n = (N + FvL::BN - 1) / FvL::BN;
     p2k::GemmArgs g = gemm_args(M, N, K, 1.0f, 0.0f, dQ, ldq, nullptr, nullptr, 0, p, nullptr);
-    g.signs = w->signs; g.flags = w->flags; g.clo = w->clo;
+    g.rec = w->rec; g.units = w->units; g.clo = w->clo;
     g.acc1 = dAcc; g.acc2 = dAcc2; g.ldacc = ldacc;
     hipStream_t s = stream_of(stream);
-    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G128::NT);
-    g.splits = 1;
-    g.split_rows = K;
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(FvL::NT);
     if (mode == P2H_INT8W)
-        hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_INT8W, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<FvL, p2k::MODE_INT8W, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
     else
-        hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_INT8, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<FvL, p2k::MODE_INT8, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -700,7 +744,7 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
     return P2H_OK;
 }
 
-static size_t quant_area(int M, int K) { return align_up((size_t)M * p2h_q_ld(K), 256) + align_up((size_t)M * 4, 256); }
+static size_t quant_area(int M, int K) { return align_up(p2h_q_bytes(M, K), 256) + align_up((size_t)M * 4, 256); }
 
 /* Workspace of the fp32-input entries: [split partials][quantised rows][row scales]. */
 size_t p2h_fvb_workspace_bytes(int mode, int M, int N, int K)
@@ -719,7 +763,7 @@ static int quant_into_workspace(const char *who, int mode, int M, int N, int K, 
         return fail(P2H_E_WORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, %zu given", who, need,
                     workspace_bytes);
     *dQ = (signed char *)workspace + (need - quant_area(M, K));
-    *dS = (float *)((char *)*dQ + align_up((size_t)M * p2h_q_ld(K), 256));
+    *dS = (float *)((char *)*dQ + align_up(p2h_q_bytes(M, K), 256));
     return p2h_quant_rows(M, K, dA, lda, *dQ, p2h_q_ld(K), *dS, s);
 }
 
@@ -774,10 +818,24 @@ int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, in
     if (M == 0 || N == 0) return P2H_OK;
     if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);
     if (K == 0) return (beta != 0.0f) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;
-    Plan p = make_plan(P2H_INT8, M, N, K, false);
+    Plan p;
+    memset(&p, 0, sizeof p);
+    const bool small = M <= 1024;   /* 64 × 64 tiles up to a thousand rows, 128 × 128 beyond */
+    p.tiles_m = (M + (small ? 63 : 127)) / (small ? 64 : 128);
+    p.tiles_n = (N + (small ? 63 : 127)) / (small ? 64 : 128);
+    p.splits = 1;
+    p.split_rows = K;
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, nullptr);
     g.B8 = (const int8_t *)dB; g.ldb = ldb; g.c1 = dBscales;
-    launch_f32_cfg<p2k::MODE_Q8B>(g, p, s);
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G64::NT);
+    if (small && K > p2k::kFoldRows)
+        hipLaunchKernelGGL((p2k::gemm_i8<G64, p2k::MODE_Q8B, p2k::OUT_F32, true, false>), grid, block, 0, s, g);
+    else if (small)
+        hipLaunchKernelGGL((p2k::gemm_i8<G64, p2k::MODE_Q8B, p2k::OUT_F32, false, false>), grid, block, 0, s, g);
+    else if (K > p2k::kFoldRows)
+        hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_Q8B, p2k::OUT_F32, true, false>), grid, block, 0, s, g);
+    else
+        hipLaunchKernelGGL((p2k::gemm_i8<G128, p2k::MODE_Q8B, p2k::OUT_F32, false, false>), grid, block, 0, s, g);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }

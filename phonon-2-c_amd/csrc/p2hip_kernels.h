@@ -26,6 +26,20 @@ enum { OUT_F32 = 0, OUT_ACC = 1 };
 
 constexpr int kFoldRows = 1024;   /* K rows per fp32 fold of the int32 sums (KC_I8, blas.c:1025) */
 
+/* Quantised activations are stored tiled for the MFMA operand: per 16-row group and 64-column step one 1 KB block,
+ * in which operand lane l (row l % 16, columns 16·(l / 16) .. +15) holds 16 consecutive bytes. Rows are padded to a
+ * multiple of 16 and columns to ldq (a multiple of 128) with zeros. kst = ldq / 64. */
+__host__ __device__ __forceinline__ size_t q_index(int m, int k, int kst)
+{
+    return ((size_t)(m >> 4) * kst + (k >> 6)) * 1024 + (size_t)(((((k >> 4) & 3) << 4) + (m & 15)) * 16) + (k & 15);
+}
+
+/* byte permute: result byte i = byte sel_i of the 8-byte value {hi:lo}, selectors 0-3 from lo, 4-7 from hi */
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
+{
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
 /* ── per-column tables ─────────────────────────────────────────────────────────────────────────────────────── */
 
 /* clo[n] = clamp(lrintf(127·lo/hi), 0, 127), 0 when hi <= 0 (blas.c:1319-1326); c1w[n] = hi·(1/127)
@@ -48,59 +62,121 @@ __global__ void fv_tables(int N, const float *__restrict__ lo, const float *__re
 
 /* ── activation quantisation ───────────────────────────────────────────────────────────────────────────────── */
 
-__device__ __forceinline__ float wave_max(float v)
+
+/* Maximum over the wave: DPP within each row of 16 lanes, then the four row results. */
+__device__ __forceinline__ float wave_max_dpp(float v)
 {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));  /* [1,0,3,2] */
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));  /* [2,3,0,1] */
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false))); /* half mirror */
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false))); /* mirror */
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-/* One wave per row. scale = amax/127 (1 for amax == 0), inv = 1/scale; the first K − K%16 entries become
- * sat8(rint(x·inv)), the tail lrintf(x/scale) clamped to ±127; columns K..kpad−1 of Q are zeroed. K % 4 == 0. */
-__global__ __launch_bounds__(256) void quant_rows(int M, int K, int kpad, const float *__restrict__ A, int lda,
-                                                  int vec_ok, int8_t *__restrict__ Q, int ldq,
-                                                  float *__restrict__ scales)
+/* four int32 values in [-128, 127] → their low bytes packed little-endian */
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d)
+{
+    const uint32_t lo = perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u), hi = perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return perm(hi, lo, 0x05040100u);
+}
+
+/* 16 columns k0..k0+15 of one row (values x) into 16 bytes (blas.c:1114-1145): columns below k16 = K − K%16
+ * become sat8(rint(x·inv)), the tail rint(x/scale) clamped to ±127, columns at or beyond K zero. */
+__device__ __forceinline__ uint4 quant16(const float x[16], int k0, int K, int k16, float scale, float inv)
+{
+    int q[16];
+    if (k0 + 16 <= k16) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) q[e] = (int)__builtin_amdgcn_fmed3f(__builtin_rintf(x[e] * inv), -128.0f, 127.0f);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int k = k0 + e;
+            const float body = __builtin_amdgcn_fmed3f(__builtin_rintf(x[e] * inv), -128.0f, 127.0f);
+            const float tail = __builtin_amdgcn_fmed3f(__builtin_rintf(x[e] / scale), -127.0f, 127.0f);
+            q[e] = (int)(k < k16 ? body : k < K ? tail : 0.0f);
+        }
+    }
+    return make_uint4(pack4(q[0], q[1], q[2], q[3]), pack4(q[4], q[5], q[6], q[7]), pack4(q[8], q[9], q[10], q[11]),
+                      pack4(q[12], q[13], q[14], q[15]));
+}
+
+/* 16 columns k0..k0+15 of a row, zeros at and beyond K (K % 4 == 0); every load is issued, out-of-range ones at
+ * column 0 */
+template <bool VEC>
+__device__ __forceinline__ void load16(const float *__restrict__ row, int k0, int K, float x[16])
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int k = k0 + 4 * q;
+        const bool ok = k < K;
+        const int kk = ok ? k : 0;
+        float4 v;
+        if (VEC) v = *reinterpret_cast<const float4 *>(row + kk);
+        else v = make_float4(row[kk], row[kk + 1], row[kk + 2], row[kk + 3]);
+        x[4 * q] = ok ? v.x : 0.0f;
+        x[4 * q + 1] = ok ? v.y : 0.0f;
+        x[4 * q + 2] = ok ? v.z : 0.0f;
+        x[4 * q + 3] = ok ? v.w : 0.0f;
+    }
+}
+
+/* One wave per row of the padded row range, into the tiled layout (q_index). Lane l owns the 16-column chunks
+ * 16·(l + 64c); with NCH > 0 the row (ldq <= 1024·NCH) stays in registers between the row maximum and the
+ * quantisation, with NCH == 0 it is read twice. scale = amax/127 (1 for amax == 0), inv = 1/scale. Rows M..Mp−1 and
+ * columns K..ldq−1 are written as zeros. VEC: lda % 4 == 0 and A 16-byte aligned. */
+template <int NCH, bool VEC>
+__global__ __launch_bounds__(256) void quant_rows(int M, int Mp, int K, const float *__restrict__ A, int lda,
+                                                  int8_t *__restrict__ Q, int ldq, float *__restrict__ scales)
 {
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (m >= M) return;
-    const float *row = A + (size_t)m * lda;
-    float amax = 0.0f;
-    for (int k = 4 * lane; k < K; k += 256) {
-        float4 v;
-        if (vec_ok) v = *reinterpret_cast<const float4 *>(row + k);
-        else v = make_float4(row[k], row[k + 1], row[k + 2], row[k + 3]);
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    if (m >= Mp) return;
+    const int kst = ldq / 64, k16 = K / 16 * 16;
+    if (m >= M) {
+        for (int k0 = 16 * lane; k0 < ldq; k0 += 1024)
+            *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
+        return;
     }
-    amax = wave_max(amax);
+    const float *row = A + (size_t)m * lda;
+    if (NCH > 0) {
+        float x[NCH > 0 ? NCH : 1][16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            load16<VEC>(row, 16 * (lane + 64 * c), K, x[c]);
+#pragma unroll
+            for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[c][e]));
+        }
+        amax = wave_max_dpp(amax);
+        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int k0 = 16 * (lane + 64 * c);
+            if (k0 < ldq) *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = quant16(x[c], k0, K, k16, scale, inv);
+        }
+        if (lane == 0) scales[m] = scale;
+        return;
+    }
+    float amax = 0.0f;
+    for (int k0 = 16 * lane; k0 < K; k0 += 1024) {
+        float x[16];
+        load16<VEC>(row, k0, K, x);
+#pragma unroll
+        for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[e]));
+    }
+    amax = wave_max_dpp(amax);
     const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / scale;
-    const int k16 = K / 16 * 16;
-    int8_t *qrow = Q + (size_t)m * ldq;
-    for (int k = 4 * lane; k < kpad; k += 256) {
-        uint32_t packed = 0;
-        if (k < K) {
-            float x[4];
-            if (vec_ok) {
-                float4 v = *reinterpret_cast<const float4 *>(row + k);
-                x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
-            } else {
-                x[0] = row[k]; x[1] = row[k + 1]; x[2] = row[k + 2]; x[3] = row[k + 3];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float r;
-                if (k + i < k16) {
-                    r = __builtin_rintf(x[i] * inv);
-                    r = fminf(fmaxf(r, -128.0f), 127.0f);
-                } else {
-                    r = __builtin_rintf(x[i] / scale);
-                    r = fminf(fmaxf(r, -127.0f), 127.0f);
-                }
-                packed |= ((uint32_t)(int)r & 0xFFu) << (8 * i);
-            }
-        }
-        *reinterpret_cast<uint32_t *>(qrow + k) = packed;
+    for (int k0 = 16 * lane; k0 < ldq; k0 += 1024) {
+        float x[16];
+        load16<VEC>(row, k0, K, x);
+        *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = quant16(x, k0, K, k16, scale, inv);
     }
     if (lane == 0) scales[m] = scale;
 }
@@ -120,7 +196,12 @@ struct GemmArgs {
     int kq;                                               /* K rounded up to 128: Q columns that may be read */
     int splits, split_rows;                               /* K splits; rows per split (divides 1024) */
     int32_t *part;                                        /* split partials [planes][splits][M][N] */
+    const uint8_t *rec;                                   /* five-value operand records (fv_repack) */
+    int units;                                            /* 128-row K units of the records: K rounded up / 128 */
+    int kst;                                              /* 64-column steps per 16-row group of Q: ldq / 64 */
+    int mg_last, ng_last;                                 /* last 16-row group of Q, last 16-column group of C */
 };
+
 
 
 /* Tile geometry. Weight columns n play the MFMA "row" role and activation rows m the "column" role, so each lane's
@@ -147,11 +228,6 @@ struct Geo {
     static_assert(1024 % BK == 0 && BK % 64 == 0, "stage depth");
 };
 
-/* byte permute: result byte i = byte sel_i of the 8-byte value {hi:lo}, selectors 0-3 from lo, 4-7 from hi */
-__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
-{
-    return __builtin_amdgcn_perm(hi, lo, sel);
-}
 
 /* 4×4 byte transpose: out[q] byte r = in[r] byte q. */
 __device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4])
@@ -319,7 +395,8 @@ void gemm_i8(GemmArgs g)
 #pragma unroll
     for (int i = 0; i < G::A_PER; i++) {
         const int c = tid + i * G::NT;
-        a_off[i] = (uint32_t)((c / (BK / 16)) * g.ldq + 16 * (c % (BK / 16)));
+        const int row = c / (BK / 16), kc = c % (BK / 16);   /* row of the tile, 16-byte column chunk of the stage */
+        a_off[i] = (uint32_t)(((row >> 4) * g.kst + (kc >> 2)) * 1024 + (((kc & 3) << 4) + (row & 15)) * 16);
     }
 #pragma unroll
     for (int u = 0; u < G::B_PER; u++)
@@ -394,7 +471,7 @@ void gemm_i8(GemmArgs g)
         auto load_stage = [&](int t) {
             const int k0 = k_begin + t * BK;
             if (!EDGE) {
-                const int8_t *qk = g.Q + (size_t)m0 * g.ldq + k0;
+                const int8_t *qk = g.Q + ((size_t)(m0 >> 4) * g.kst + (k0 >> 6)) * 1024;
 #pragma unroll
                 for (int i = 0; i < G::A_PER; i++) ra[i] = *reinterpret_cast<const uint4 *>(qk + a_off[i]);
                 const uint8_t *sk = g.signs + (size_t)k0 * (N / 4) + n0 / 4;
@@ -420,7 +497,7 @@ void gemm_i8(GemmArgs g)
                 const int c = tid + i * G::NT;
                 const int mc = min(m0 + c / (BK / 16), M - 1);
                 const int kc = min(k0 + 16 * (c % (BK / 16)), g.kq - 16);
-                ra[i] = *reinterpret_cast<const uint4 *>(g.Q + (size_t)mc * g.ldq + kc);
+                ra[i] = *reinterpret_cast<const uint4 *>(g.Q + q_index(mc, kc, g.kst));
             }
 #pragma unroll
             for (int u = 0; u < G::B_PER; u++) {
@@ -578,6 +655,369 @@ void gemm_i8(GemmArgs g)
                     int32_t *p = g.part + ((size_t)split * M + m) * N + n;
                     *reinterpret_cast<v4i *>(p) = acc[i][j];
                     if (TWO) *reinterpret_cast<v4i *>(p + plane) = accT[TWO ? i : 0][TWO ? j : 0];
+                }
+            }
+    }
+}
+
+/* ── the five-value GEMM on operand records ──────────────────────────────────────────────────────────────────── */
+
+/* Five-value planes → operand records. Record (column group cg, unit u) holds for each of 64 lanes three dwords:
+ * lane l serves column n = 16·cg + l % 16 and rows k = 128·u + 64·s + 16·(l / 16) + 4·d + b (s = 0, 1: the two
+ * 64-row steps of the unit; d, b = 0..3), with
+ *   dword s: byte b, bits 2d..2d+1 = the 2-bit sign code;   dword 2: byte b, bit d + 4s = the flag.
+ * Rows k >= K hold code 1 (weight 0) and flag 0. Records are stored [N/16][units][64][3 dwords], so a 16-column
+ * group streams along K, and one 64-lane load brings a whole operand's codes (3 bits per weight, as the planes). */
+__global__ void fv_repack(int K, int N, int units, const uint8_t *__restrict__ signs,
+                          const uint8_t *__restrict__ flags, uint32_t *__restrict__ rec)
+{
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)(N / 16) * units * 64) return;
+    const int l = (int)(idx % 64);
+    const size_t gu = idx / 64;
+    const int u = (int)(gu % units), cg = (int)(gu / units);
+    const int n = 16 * cg + (l & 15), kq = l >> 4;
+    uint32_t w[3] = {0u, 0u, 0u};
+    for (int s = 0; s < 2; s++)
+        for (int d = 0; d < 4; d++)
+            for (int b = 0; b < 4; b++) {
+                const int k = 128 * u + 64 * s + 16 * kq + 4 * d + b;
+                uint32_t code = 1u, flag = 0u;
+                if (k < K) {
+                    code = (signs[(size_t)k * (N / 4) + (n >> 2)] >> (2 * (n & 3))) & 3u;
+                    flag = (flags[(size_t)k * (N / 8) + (n >> 3)] >> (n & 7)) & 1u;
+                }
+                w[s] |= code << (8 * b + 2 * d);
+                w[2] |= flag << (8 * b + d + 4 * s);
+            }
+    rec[3 * idx] = w[0];
+    rec[3 * idx + 1] = w[1];
+    rec[3 * idx + 2] = w[2];
+}
+
+/* One 16-byte weight operand (64 rows × one column per lane, as the MFMA reads it) from a lane's record: 64-row step
+ * s, sign dword S, flag dword F. Selector byte = code | flag << 2, then the column's code table (i8w_lo_table). */
+template <int STEP>
+__device__ __forceinline__ uint32_t fv_sel(uint32_t S, uint32_t F, int d)
+{
+    const int sh = d + 4 * STEP - 2;   /* moves flag bit d + 4s of each byte to bit 2 */
+    const uint32_t fl = (sh >= 0 ? (F >> sh) : (F << -sh)) & 0x04040404u;
+    return ((S >> (2 * d)) & 0x03030303u) | fl;
+}
+
+template <int FM_, int FN_, int NW_, int D_>
+struct FvGeo {
+    static constexpr int FM = FM_, FN = FN_, NW = NW_, D = D_;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 16 * FM, BN = 16 * FN * NW;
+    static constexpr int A_STAGE = 2 * FM * 1024;   /* FM row groups × two 64-row steps of activation operands */
+    static constexpr int B_STAGE = FN * NW * 1024;  /* one weight record per 16-column group: 64 lanes × 16-B slots */
+    static constexpr int STAGE = A_STAGE + B_STAGE;
+    static constexpr int A_DMA = 2 * FM / NW;       /* activation DMAs per wave per stage */
+    static constexpr int DMA = A_DMA + FN;          /* DMAs per wave per stage */
+    static_assert((2 * FM) % NW == 0, "activation operands divide among the waves");
+    static_assert(FN <= 4 && FM <= 16, "epilogue factors: one column and one row per thread");
+    static_assert(D >= 2 && D * STAGE <= 160 * 1024, "LDS ring");
+};
+
+/* Direct global → LDS loads (16 or 12 bytes per lane into 16-byte lane slots at lds + 16·lane). Issued from inline
+ * assembly so that the compiler adds no waits of its own for them: the GEMM waits for them explicitly (wait_vm),
+ * and the compiler's waits for its own loads stay correct since the vector-memory counter retires in order. */
+__device__ __forceinline__ void dma_16(const void *src, const void *lds)
+{
+    const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_12(const void *src, const void *lds)
+{
+    const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx3 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
+}
+
+/* s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left open); a compiler barrier for memory operations */
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+
+/* this wave's LDS reads complete, then the workgroup barrier; no wait on vector memory */
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+/* The int8 five-value GEMM (sgemm_i8_worker, blas.c:1296-1370) on operand records.
+ *  A workgroup of NW waves owns a BM × BN output tile; wave w owns its FN 16-column groups for all FM 16-row groups,
+ *  so each weight operand is decoded exactly once per workgroup, in registers, and feeds FM MFMAs.
+ *  Operands stream through a ring of D LDS stages (two 64-row steps each) by direct global→LDS loads: stage t + D − 1
+ *  is requested while stage t is computed, with one barrier per stage and no register staging.
+ *  Folding into fp32 is as in gemm_i8: per 1024-row block in registers, or int32 partials per split for fold_splits. */
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT>
+__global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
+{
+    constexpr bool TWO = (MODE == MODE_INT8);
+    constexpr bool FOLD = OUT == OUT_F32 && !SPLIT;
+    constexpr int FM = G::FM, FN = G::FN, D = G::D, STAGE = G::STAGE;
+    constexpr int UNITS_PER_FOLD = kFoldRows / 128;
+    __shared__ __attribute__((aligned(16))) int8_t ring[D * STAGE];
+    __shared__ __attribute__((aligned(16))) float f_c1[FOLD ? G::BN : 4], f_c2[FOLD && TWO ? G::BN : 4],
+        f_as[FOLD ? G::BM : 4];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tile_n, tile_m, split;
+    tile_of(g, tile_n, tile_m, split);
+    const int n0 = tile_n * G::BN, m0 = tile_m * G::BM;
+    const int M = g.M, N = g.N;
+    const int split_units = (g.split_rows + 127) / 128;
+    const int u_begin = split * split_units;
+    const int nst = max(0, min(g.units, u_begin + split_units) - u_begin);
+
+    /* DMA sources of this lane (row and column groups clamped into the padded operands; their outputs are masked) */
+    const int8_t *a_src[G::A_DMA];
+    int a_dst[G::A_DMA];
+#pragma unroll
+    for (int q = 0; q < G::A_DMA; q++) {
+        const int f = wave + q * G::NW;            /* operand f = 2·j + s of the stage */
+        const int mg = min((m0 >> 4) + (f >> 1), g.mg_last);
+        a_src[q] = g.Q + ((size_t)mg * g.kst + 2 * u_begin + (f & 1)) * 1024 + lane * 16;
+        a_dst[q] = f * 1024;
+    }
+    const uint8_t *b_src[FN];
+    uint32_t lo_tab[FN];
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+        const int cg = min((n0 >> 4) + wave * FN + i, g.ng_last);
+        b_src[i] = g.rec + ((size_t)cg * g.units + u_begin) * 768 + lane * 12;
+        if (MODE == MODE_INT8W) lo_tab[i] = i8w_lo_table(g.clo[16 * cg + (lane & 15)]);
+    }
+    auto issue = [&](int t) {   /* stage t → ring slot t % D */
+        int8_t *slot = ring + (t % D) * STAGE;
+#pragma unroll
+        for (int q = 0; q < G::A_DMA; q++) dma_16(a_src[q] + (size_t)t * 2048, slot + a_dst[q]);
+#pragma unroll
+        for (int i = 0; i < FN; i++) dma_12(b_src[i] + (size_t)t * 768, slot + G::A_STAGE + (wave * FN + i) * 1024);
+    };
+    /* epilogue factors: loaded before the first DMAs (so waiting for them waits for no DMA), into LDS before the
+     * first barrier */
+    float r_c1 = 0.0f, r_c2 = 0.0f, r_as = 0.0f;
+    if (FOLD) {
+        if (tid < G::BN) {
+            const int n = min(n0 + tid, N - 1);
+            r_c1 = g.c1[n];
+            if (TWO) r_c2 = g.c2[n];
+        }
+        if (tid < G::BM) r_as = g.a_scales[min(m0 + tid, M - 1)];
+    }
+#pragma unroll
+    for (int t = 0; t < D - 1; t++)
+        if (t < nst) issue(t);
+    if (FOLD) {
+        r_as *= g.alpha;
+        if (tid < G::BN) {
+            f_c1[tid] = r_c1;
+            if (TWO) f_c2[tid] = r_c2;
+        }
+        if (tid < G::BM) f_as[tid] = r_as;
+    }
+
+    v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++) {
+            acc[i][j] = v4i{0, 0, 0, 0};
+            if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+        }
+
+    const int n_lane = n0 + wave * 16 * FN + 4 * (lane >> 4);   /* outputs (m_lane + 16 j, n_lane + 16 i + r) */
+    const int m_lane = m0 + (lane & 15);
+    const bool beta_zero = g.beta == 0.0f;
+    float run[FOLD ? FN : 1][FOLD ? FM : 1][4];
+    int block = 0;
+    /* CASE 0: block 0 with beta 0 (f·as); 1: block 0 with beta-scaled C (fmaf(f, as, β·C)); 2: a later block
+     * (fmaf(f, as, running)). Each case is straight-line code, selected by a uniform branch. */
+    auto fold_case = [&](auto case_tag) __attribute__((always_inline)) {
+        constexpr int CASE = decltype(case_tag)::value;
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+            const int nl = wave * 16 * FN + 16 * i + 4 * (lane >> 4);
+            const v4f c1 = *reinterpret_cast<const v4f *>(f_c1 + nl);
+            v4f c2 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (TWO) c2 = *reinterpret_cast<const v4f *>(f_c2 + nl);
+            float cold[CASE == 1 ? FM : 1][4];
+            if (CASE == 1) {
+#pragma unroll
+                for (int j = 0; j < FM; j++) {
+                    const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
+                    const float *cp = g.C + (size_t)m * g.ldc + n;
+                    if (g.c_vec4) {
+                        const v4f v = *reinterpret_cast<const v4f *>(cp);
+                        cold[CASE == 1 ? j : 0][0] = v[0]; cold[CASE == 1 ? j : 0][1] = v[1];
+                        cold[CASE == 1 ? j : 0][2] = v[2]; cold[CASE == 1 ? j : 0][3] = v[3];
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[CASE == 1 ? j : 0][r] = cp[r];
+                    }
+                }
+                if (g.beta != 1.0f) {
+#pragma unroll
+                    for (int j = 0; j < FM; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[CASE == 1 ? j : 0][r] = cold[CASE == 1 ? j : 0][r] * g.beta;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const float as = f_as[16 * j + (lane & 15)];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float f = (float)acc[i][j][r] * c1[r];
+                    if (TWO) f = __builtin_fmaf((float)accT[TWO ? i : 0][TWO ? j : 0][r], c2[r], f);
+                    float &out = run[FOLD ? i : 0][FOLD ? j : 0][r];
+                    if (CASE == 0) out = f * as;
+                    else if (CASE == 1) out = __builtin_fmaf(f, as, cold[CASE == 1 ? j : 0][r]);
+                    else out = __builtin_fmaf(f, as, out);
+                }
+                acc[i][j] = v4i{0, 0, 0, 0};
+                if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+            }
+        }
+    };
+    auto fold = [&](int blk) __attribute__((always_inline)) {
+        if (blk > 0) fold_case(std::integral_constant<int, 2>{});
+        else if (beta_zero) fold_case(std::integral_constant<int, 0>{});
+        else fold_case(std::integral_constant<int, 1>{});
+    };
+
+    for (int t = 0; t < nst; t++) {
+        /* this wave's DMAs of stage t have landed (D − 2 younger stages may still be in flight) ... */
+        if (t + D - 2 < nst) wait_vm<G::DMA * (D - 2)>();
+        else wait_vm<0>();
+        /* ... and every wave's; every wave is also done reading the slot that stage t + D − 1 reuses */
+        lds_barrier();
+        if (t + D - 1 < nst) issue(t + D - 1);
+
+        const int8_t *sa = ring + (t % D) * STAGE;
+        const int8_t *sb = sa + G::A_STAGE + (wave * FN) * 1024 + lane * 16;
+        /* all LDS reads of the stage first: FN weight records, 2·FM activation operands */
+        uint32_t rw[FN][3];
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+            const uint32_t *p = reinterpret_cast<const uint32_t *>(sb + i * 1024);
+            rw[i][0] = p[0]; rw[i][1] = p[1]; rw[i][2] = p[2];
+        }
+        v4i av[2][FM];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int j = 0; j < FM; j++)
+                av[s2][j] = *reinterpret_cast<const v4i *>(sa + (2 * j + s2) * 1024 + lane * 16);
+        /* weight operands of both 64-row steps */
+        v4i bw[2][FN], bt[2][TWO ? FN : 1];
+        auto decode = [&](auto step_tag) __attribute__((always_inline)) {
+            constexpr int S = decltype(step_tag)::value;
+#pragma unroll
+            for (int i = 0; i < FN; i++)
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint32_t sel = fv_sel<S>(rw[i][S], rw[i][2], d);
+                    if (MODE == MODE_INT8W) {
+                        bw[S][i][d] = (int)perm(kI8wHiTable, lo_tab[i], sel);
+                    } else {
+                        bw[S][i][d] = (int)perm(kPlaneS, kPlaneS, sel);
+                        bt[S][TWO ? i : 0][d] = (int)perm(kPlaneS, 0u, sel);
+                    }
+                }
+        };
+        auto mma = [&](auto step_tag) __attribute__((always_inline)) {
+            constexpr int S = decltype(step_tag)::value;
+#pragma unroll
+            for (int j = 0; j < FM; j++)
+#pragma unroll
+                for (int i = 0; i < FN; i++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[S][i], av[S][j], acc[i][j], 0, 0, 0);
+                    if (TWO)
+                        accT[TWO ? i : 0][TWO ? j : 0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            bt[S][TWO ? i : 0], av[S][j], accT[TWO ? i : 0][TWO ? j : 0], 0, 0, 0);
+                }
+        };
+        decode(std::integral_constant<int, 0>{});
+        mma(std::integral_constant<int, 0>{});
+        decode(std::integral_constant<int, 1>{});
+        mma(std::integral_constant<int, 1>{});
+        /* Issue order for the scheduler: the LDS reads, the step-0 decode, then step 0's MFMAs each followed by a
+         * share of the step-1 decode (which the matrix cores' latency hides), then step 1's MFMAs. */
+        constexpr int N_MFMA = FM * FN * (TWO ? 2 : 1);
+        constexpr int DEC_VALU = FN * 4 * (TWO ? 6 : 5);
+        constexpr int PER = (DEC_VALU + N_MFMA - 1) / N_MFMA;
+        __builtin_amdgcn_sched_group_barrier(0x100, 3 * FN + 2 * FM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, DEC_VALU, 0);
+#pragma unroll
+        for (int x = 0; x < N_MFMA; x++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, PER, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, N_MFMA, 0);
+        if (FOLD && MULTI && t + 1 < nst && (t + 1) % UNITS_PER_FOLD == 0) {
+            fold(block);
+            block++;
+        }
+    }
+
+    if (OUT == OUT_ACC) {
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                if (m < M && n < N) {
+                    *reinterpret_cast<v4i *>(g.acc1 + (size_t)m * g.ldacc + n) = acc[i][j];
+                    if (TWO) *reinterpret_cast<v4i *>(g.acc2 + (size_t)m * g.ldacc + n) = accT[TWO ? i : 0][TWO ? j : 0];
+                }
+            }
+        return;
+    }
+    if (SPLIT) {   /* int32 partial sums of this split; fold_splits adds and folds them */
+        const size_t plane = (size_t)g.splits * M * N;
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                if (m < M && n < N) {
+                    int32_t *p = g.part + ((size_t)split * M + m) * N + n;
+                    *reinterpret_cast<v4i *>(p) = acc[i][j];
+                    if (TWO) *reinterpret_cast<v4i *>(p + plane) = accT[TWO ? i : 0][TWO ? j : 0];
+                }
+            }
+        return;
+    }
+    if (nst == 0) return;
+    fold(block);
+    /* every output of the lane is final: one burst of 16-byte stores, nothing waited on after it */
+    if (g.c_vec4) {
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                if (m < M && n < N)
+                    *reinterpret_cast<v4f *>(g.C + (size_t)m * g.ldc + n) =
+                        v4f{run[i][j][0], run[i][j][1], run[i][j][2], run[i][j][3]};
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int n = n_lane + 16 * i, m = m_lane + 16 * j;
+                if (m < M && n < N) {
+                    float *cp = g.C + (size_t)m * g.ldc + n;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) cp[r] = run[i][j][r];
                 }
             }
     }

@@ -63,6 +63,7 @@ _HIP_SIG = {
     "p2h_fv_pack_codes": (_i, [_vp, _vp, _vp]),
     "p2h_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_q_ld": (_i, [_i]),
+    "p2h_q_bytes": (C.c_size_t, [_i, _i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_plan": (C.c_char_p, [_i, _i, _i, _i, _i]),
@@ -274,6 +275,29 @@ def q_ld(K):
     return hip().p2h_q_ld(K)
 
 
+def q_bytes(M, K):
+    """Bytes of a tiled quantised-activation buffer for M rows (rows padded to 16, columns to q_ld(K))."""
+    return hip().p2h_q_bytes(M, K)
+
+
+def q_tile(q, ldq):
+    """Row-major int8 q [M, <= ldq] → the library's tiled layout (rows padded to 16, columns to ldq, with zeros):
+    per 16 rows × 64 columns one 1 KB block of 64 lanes × 16 bytes, lane = (column/16 % 4)·16 + row % 16."""
+    q = np.asarray(q, np.int8)
+    M, K = q.shape
+    Mp = (M + 15) // 16 * 16
+    full = np.zeros((Mp, ldq), np.int8)
+    full[:M, :K] = q
+    return np.ascontiguousarray(full.reshape(Mp // 16, 16, ldq // 64, 4, 16).transpose(0, 2, 3, 1, 4)).reshape(-1)
+
+
+def q_untile(t, M, ldq):
+    """Inverse of q_tile: the tiled buffer → row-major [roundup(M, 16), ldq]."""
+    Mp = (M + 15) // 16 * 16
+    t = np.asarray(t, np.int8)[: Mp * ldq]
+    return np.ascontiguousarray(t.reshape(Mp // 16, ldq // 64, 4, 16, 16).transpose(0, 3, 1, 2, 4)).reshape(Mp, ldq)
+
+
 def workspace_bytes(mode, M, N, K):
     """Workspace of p2h_fvb_gemm (fp32 activations): quantised rows plus the split-K area."""
     return hip().p2h_fvb_workspace_bytes(MODES.get(mode, mode), M, N, K)
@@ -314,15 +338,18 @@ def fvb_gemm_dev(mode, M, N, K, alpha, dA, lda, w, beta, dC, ldc, ws, ws_bytes, 
 # ── host-array conveniences (upload, run, download, synchronise) ─────────────────────────────────────────────────
 
 def quant_rows(A, K=None):
+    """p2h_quant_rows on a host matrix: q as row-major [roundup(M, 16), ldq] (untiled, pads included), scales [M]."""
     A = np.ascontiguousarray(A, np.float32)
     M, lda = A.shape
     K = lda if K is None else K
     ldq = q_ld(K)
     dA = to_device(A)
-    dQ = DeviceBuffer(max(M, 1) * max(ldq, 16))
+    nbytes = max(q_bytes(M, K), 16)
+    dQ = DeviceBuffer(nbytes)
+    dQ.upload(np.full(nbytes, 0x5A, np.uint8))   # every byte, pads included, must be written
     dS = DeviceBuffer(max(M, 1) * 4)
     quant_rows_dev(M, K, dA.ptr, lda, dQ.ptr, ldq, dS.ptr)
-    q = dQ.download((M, ldq), np.int8)
+    q = q_untile(dQ.download((q_bytes(M, K),), np.int8), M, ldq) if M > 0 else np.zeros((0, ldq), np.int8)
     s = dS.download((M,), np.float32)
     return q, s
 
@@ -350,10 +377,8 @@ def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None, split=True, w
     M, K = q.shape
     N = w.N
     ldq = q_ld(K)
-    qp = np.zeros((M, ldq), np.int8)
-    qp[:, :K] = q
     C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
-    dQ, dS, dC = to_device(qp), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
+    dQ, dS, dC = to_device(q_tile(q, ldq)), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
     if ws is None and split:
         ws = Workspace(q8a_workspace_bytes(mode, M, N, K))
     fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ.ptr, ldq, dS.ptr, w, beta, dC.ptr, C0.shape[1],
@@ -367,9 +392,7 @@ def fvb_acc_i32(mode, q, w):
     M, K = q.shape
     N = w.N
     ldq = q_ld(K)
-    qp = np.zeros((M, ldq), np.int8)
-    qp[:, :K] = q
-    dQ = to_device(qp)
+    dQ = to_device(q_tile(q, ldq))
     d1 = DeviceBuffer(M * N * 4)
     d2 = DeviceBuffer(M * N * 4)
     m = MODES.get(mode, mode)

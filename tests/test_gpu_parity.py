@@ -58,15 +58,16 @@ def test_quant_rows_bit_exact(M, K):
     q_gpu, s_gpu = P.quant_rows(A)
     q_ref, s_ref = O.quant_rows(A)
     assert _bits_equal(s_gpu, s_ref)
-    assert np.array_equal(q_gpu[:, :K], q_ref)
-    assert (q_gpu[:, K:] == 0).all(), "padding columns must be zero"
+    assert np.array_equal(q_gpu[:M, :K], q_ref)
+    assert (q_gpu[:M, K:] == 0).all(), "padding columns must be zero"
+    assert (q_gpu[M:] == 0).all(), "padding rows must be zero"
 
 
 def test_quant_rows_strided_unaligned():
     A = P.gen_activations(SEED, 7, 9, 303)
     q_gpu, s_gpu = P.quant_rows(A, K=300)   # lda 303: rows are not 16-byte aligned
     q_ref, s_ref = O.quant_rows(A, K=300)
-    assert _bits_equal(s_gpu, s_ref) and np.array_equal(q_gpu[:, :300], q_ref)
+    assert _bits_equal(s_gpu, s_ref) and np.array_equal(q_gpu[:9, :300], q_ref)
 
 
 # ── int32 accumulators ──────────────────────────────────────────────────────────────────────────────────────────
@@ -220,7 +221,7 @@ def test_full_size_sampled_rows(M, K, N):
 _TILE_CASES = {}
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("split_rows", [-1, 0, 256, 512, 1024])
 @pytest.mark.parametrize("M,K,N", [(375, 4096, 1024), (130, 1028, 272), (38, 1024, 4096), (300, 2048, 512)])
 def test_tiles_and_splits_int8w(monkeypatch, tile, split_rows, M, K, N):
@@ -235,12 +236,12 @@ def test_tiles_and_splits_int8w(monkeypatch, tile, split_rows, M, K, N):
         ref = O.gemm_i8_run("int8w", q, sc, signs, flags, lo, hi, N, alpha=0.75, C0=C0, beta_zero=False)
         _TILE_CASES[key] = (P.FvWeight(signs, flags, lo, hi, K, N), q, sc, C0, ref)
     w, q, sc, C0, ref = _TILE_CASES[key]
-    for rep in range(2):   # twice: the split counters must be back at zero after each call
+    for rep in range(2):   # twice: a call must not depend on what the previous one left in its workspace
         got = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=0.75, beta=1.0, C0=C0)
         _assert_fp32(got, ref)
 
 
-@pytest.mark.parametrize("tile", [0, 1])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
 @pytest.mark.parametrize("split_rows", [0, 256, 1024])
 def test_tiles_and_splits_int8(monkeypatch, tile, split_rows):
     monkeypatch.setenv("P2H_TILE", str(tile))
@@ -256,8 +257,8 @@ def test_tiles_and_splits_int8(monkeypatch, tile, split_rows):
 
 
 def test_one_workspace_across_shapes():
-    """A workspace reused by calls of different shapes: each call's partial sums must not disturb the split
-    counters another call relies on (they live in a fixed region), and every call leaves them at zero."""
+    """A workspace reused by calls of different shapes, split and unsplit in turn: no call may depend on what an
+    earlier call left in it."""
     shapes = [(38, 4096, 1024), (9, 256, 32), (375, 1024, 1024), (38, 1024, 4096), (9, 256, 32)]
     need = max(P.q8a_workspace_bytes("int8w", M, N, K) for M, K, N in shapes)
     ws = P.Workspace(need)

@@ -46,3 +46,23 @@ def test_no_device_is_an_error_not_a_fallback():
     rc = P.hip().p2h_init()
     assert rc == -2, rc
     assert "device" in P.last_error()
+
+
+def test_q_tile_layout_matches_the_documented_index():
+    """The tiled activation layout p2h_quant_rows documents: byte (m, k) at
+    ((m/16)·(ldq/64) + k/64)·1024 + ((k%64)/16·16 + m%16)·16 + k%16; pads are zero; q_untile inverts q_tile."""
+    import numpy as np
+    rng = np.random.default_rng(5)
+    for M, K, ldq in [(1, 4, 128), (17, 130, 256), (40, 256, 384)]:
+        q = rng.integers(-127, 128, (M, K), dtype=np.int8)
+        t = P.q_tile(q, ldq)
+        Mp = (M + 15) // 16 * 16
+        assert t.size == Mp * ldq
+        expect = np.zeros(Mp * ldq, np.int8)
+        for m in range(M):
+            for k in range(K):
+                idx = ((m // 16) * (ldq // 64) + k // 64) * 1024 + ((k % 64) // 16 * 16 + m % 16) * 16 + k % 16
+                expect[idx] = q[m, k]
+        assert np.array_equal(t, expect)
+        back = P.q_untile(t, M, ldq)
+        assert np.array_equal(back[:M, :K], q) and not back[M:].any() and not back[:, K:].any()
