@@ -95,6 +95,7 @@ struct P2hWeight {
     uint8_t *clo;
     float *c1w, *c2;
     uint8_t *rec;     /* operand records of the int8 routes (fv_repack): [N/16][units][64 lanes][12 B] */
+    uint8_t *rec4;    /* 4-bit selector records of the large-M GEMM (fv_repack4): [N/16][units][64 lanes][16 B] */
     int units;        /* 128-row K units: K rounded up / 128 */
     void *own;        /* the one device allocation this handle made */
     size_t own_bytes;
@@ -333,6 +334,7 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     size_t off_c2 = off; off += align_up((size_t)N * 4, 256);
     const int units = (K + 127) / 128;
     size_t off_rec = off; off += align_up((size_t)(N / 16) * units * 768 + 16, 256);
+    size_t off_rec4 = off; off += align_up((size_t)(N / 16) * units * 1024 + 16, 256);
     void *base = nullptr;
     if (hipMalloc(&base, off) != hipSuccess) {
         fail(P2H_E_NOMEM, "five-value weight: hipMalloc(%zu) failed", off);
@@ -351,6 +353,7 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     w->c1w = (float *)(b + off_c1);
     w->c2 = (float *)(b + off_c2);
     w->rec = b + off_rec;
+    w->rec4 = b + off_rec4;
     w->units = units;
     w->own = base;
     w->own_bytes = off;
@@ -367,6 +370,9 @@ static int weight_tables(P2hWeight *w)
     if (recs > 0) {
         hipLaunchKernelGGL(p2k::fv_repack, dim3((unsigned)((recs + 255) / 256)), dim3(256), 0, s, w->K, w->N,
                            w->units, w->signs, w->flags, (uint32_t *)w->rec);
+        HIPCHK(hipGetLastError());
+        hipLaunchKernelGGL(p2k::fv_repack4, dim3((unsigned)((recs + 255) / 256)), dim3(256), 0, s, w->K, w->N,
+                           w->units, w->signs, w->flags, (uint4 *)w->rec4);
         HIPCHK(hipGetLastError());
     }
     HIPCHK(hipStreamSynchronize(s));
@@ -534,9 +540,15 @@ using FvX = p2k::FvGeo<8, 4, 4, 4>;   /* 128 × 256 (int8w only: the two-plane m
 using FvT8 = p2k::FvGeo<2, 1, 4, 8>;  /*  32 ×  64, 8 stages in flight */
 using FvS8 = p2k::FvGeo<4, 1, 4, 8>;  /*  64 ×  64, 8 stages in flight */
 using FvT6 = p2k::FvGeo<2, 1, 4, 6>;  /*  32 ×  64, 6 stages in flight */
-enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_COUNT = 8 };
-const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM};
-const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN};
+/* Large-M tiles (int8w): two workgroups per CU, 4-bit selector records, outputs staged through LDS */
+using FvW6 = p2k::FvGeo<6, 4, 4, 2>;  /*  96 × 256, 2 stages: K <= 1024 */
+using FvW8 = p2k::FvGeo<8, 2, 4, 3>;  /* 128 × 128, 3 stages: K > 1024, unsplit */
+enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_W8 = 9,
+       FV_COUNT = 10 };
+const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
+                             FvW8::BM};
+const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN, FvW6::BN,
+                             FvW8::BN};
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -559,11 +571,13 @@ int env_int(const char *name, int dflt)
 Plan make_plan(int mode, int M, int N, int K, bool can_split)
 {
     Plan p;
-    /* measured on MI355X: 32 × 64 tiles are the fastest up to a thousand rows, 128 × 256 beyond */
-    int cfg = M <= 1024 ? FV_T : FV_X;
+    /* measured on MI355X: 32 × 64 tiles are the fastest up to a thousand rows; beyond, the two-workgroups-per-CU
+     * tiles on 4-bit records (int8w) or 128 × 128 (the two-plane mode needs twice the accumulators) */
+    int cfg = M <= 1024 ? FV_T : (mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_W8 : FV_W6) : FV_L);
     cfg = env_int("P2H_TILE", cfg);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
-    if (mode == P2H_INT8 && cfg == FV_X) cfg = FV_L;
+    if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_W8)) cfg = FV_L;
+    const bool large = cfg == FV_W6 || cfg == FV_W8;   /* these never split K: the fold stays in registers */
     p.cfg = cfg;
     p.tiles_m = (M + kFvBM[cfg] - 1) / kFvBM[cfg];
     p.tiles_n = (N + kFvBN[cfg] - 1) / kFvBN[cfg];
@@ -576,7 +590,7 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     const int forced = env_int("P2H_SPLIT_ROWS", 0);
     if (forced < 0) rows = 0;
     else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0 && forced % 128 == 0) rows = forced;
-    if (can_split && K > 0 && rows > 0 && (K + rows - 1) / rows > 1) {
+    if (can_split && !large && K > 0 && rows > 0 && (K + rows - 1) / rows > 1) {
         p.split_rows = rows;
         p.splits = (K + rows - 1) / rows;
     }
@@ -605,6 +619,19 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
     return g;
 }
 
+/* the large-M tiles: unsplit, two workgroups per CU, 4-bit records, staged output rows */
+template <class G>
+void launch_fv_large(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
+{
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G::NT);
+    if (g.K > p2k::kFoldRows)
+        hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, true, false, 2, true, true>), grid, block, 0,
+                           s, g);
+    else
+        hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, false, false, 2, true, true>), grid, block,
+                           0, s, g);
+}
+
 template <class G, int MODE>
 void launch_fv(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
@@ -631,6 +658,8 @@ void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
     case FV_T8: launch_fv<FvT8, MODE>(g, p, s); break;
     case FV_S8: launch_fv<FvS8, MODE>(g, p, s); break;
     case FV_T6: launch_fv<FvT6, MODE>(g, p, s); break;
+    case FV_W6: if (MODE == p2k::MODE_INT8W) { launch_fv_large<FvW6>(g, p, s); break; } /* fall through */
+    case FV_W8: if (MODE == p2k::MODE_INT8W) { launch_fv_large<FvW8>(g, p, s); break; } /* fall through */
     case FV_X: if (MODE == p2k::MODE_INT8W) { launch_fv<FvX, p2k::MODE_INT8W>(g, p, s); break; } /* fall through */
     default: launch_fv<FvL, MODE>(g, p, s); break;
     }
@@ -685,7 +714,8 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
     Plan p = make_plan(mode, M, N, K, workspace != nullptr);
     if (int rc = check_split_ws("p2h_fvb_gemm_q8a", p, workspace, workspace_bytes)) return rc;
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
-    g.rec = w->rec; g.units = w->units; g.clo = w->clo;
+    g.rec = (p.cfg == FV_W6 || p.cfg == FV_W8) ? w->rec4 : w->rec;
+    g.units = w->units; g.clo = w->clo;
     if (mode == P2H_INT8W) {
         g.c1 = w->c1w;
         launch_fv_cfg<p2k::MODE_INT8W>(g, p, s);

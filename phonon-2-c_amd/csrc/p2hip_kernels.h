@@ -7,6 +7,7 @@
  *                   v_mfma_i32_16x16x64_i8 with int32 accumulation, fp32 epilogue per 1024-row K block
  *    gemm_exact     the exact route (blas.c:838-987): fp32 panels expanded in LDS, one fmaf chain per output
  *    fv_pack_codes  the reference's pre-packed int8w code layout (blas.c:1372-1400)
+ *    fv_repack / fv_repack4  the planes re-laid per matrix-core operand (3 and 4 bits per weight) at upload
  *    scale_c        C = beta · C (blas.c:60-70)
  */
 #pragma once
@@ -695,6 +696,35 @@ __global__ void fv_repack(int K, int N, int units, const uint8_t *__restrict__ s
     rec[3 * idx + 2] = w[2];
 }
 
+/* Five-value planes → 4-bit selector records, the operand layout of the large-M GEMM. Record (cg, u) holds 16 bytes
+ * per lane l (column n = 16·cg + l % 16, rows k = 128·u + 64·s + 16·(l / 16) + 4·d + b as in fv_repack): dword
+ * 2s + d/2, byte b, nibble d % 2 is the byte-permute selector code | flag << 2 of row k. Rows k >= K hold code 1 (weight
+ * 0). Half a byte per weight: one 16-byte load per lane brings a whole 128-row unit, and an operand dword decodes with
+ * one mask (and one shift for odd d) before the table permute. */
+__global__ void fv_repack4(int K, int N, int units, const uint8_t *__restrict__ signs,
+                           const uint8_t *__restrict__ flags, uint4 *__restrict__ rec)
+{
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)(N / 16) * units * 64) return;
+    const int l = (int)(idx % 64);
+    const size_t gu = idx / 64;
+    const int u = (int)(gu % units), cg = (int)(gu / units);
+    const int n = 16 * cg + (l & 15), kq = l >> 4;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    for (int s = 0; s < 2; s++)
+        for (int d = 0; d < 4; d++)
+            for (int b = 0; b < 4; b++) {
+                const int k = 128 * u + 64 * s + 16 * kq + 4 * d + b;
+                uint32_t code = 1u, flag = 0u;
+                if (k < K) {
+                    code = (signs[(size_t)k * (N / 4) + (n >> 2)] >> (2 * (n & 3))) & 3u;
+                    flag = (flags[(size_t)k * (N / 8) + (n >> 3)] >> (n & 7)) & 1u;
+                }
+                w[2 * s + (d >> 1)] |= (code | (flag << 2)) << (8 * b + 4 * (d & 1));
+            }
+    rec[idx] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 /* One 16-byte weight operand (64 rows × one column per lane, as the MFMA reads it) from a lane's record: 64-row step
  * s, sign dword S, flag dword F. Selector byte = code | flag << 2, then the column's code table (i8w_lo_table). */
 template <int STEP>
@@ -755,8 +785,8 @@ __device__ __forceinline__ void lds_barrier()
  *  Operands stream through a ring of D LDS stages (two 64-row steps each) by direct global→LDS loads: stage t + D − 1
  *  is requested while stage t is computed, with one barrier per stage and no register staging.
  *  Folding into fp32 is as in gemm_i8: per 1024-row block in registers, or int32 partials per split for fold_splits. */
-template <class G, int MODE, int OUT, bool MULTI, bool SPLIT>
-__global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC = 1, bool REC4 = false, bool CSHUF = false>
+__global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
     constexpr bool FOLD = OUT == OUT_F32 && !SPLIT;
@@ -790,7 +820,8 @@ __global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
 #pragma unroll
     for (int i = 0; i < FN; i++) {
         const int cg = min((n0 >> 4) + wave * FN + i, g.ng_last);
-        b_src[i] = g.rec + ((size_t)cg * g.units + u_begin) * 768 + lane * 12;
+        b_src[i] = REC4 ? g.rec + ((size_t)cg * g.units + u_begin) * 1024 + lane * 16
+                        : g.rec + ((size_t)cg * g.units + u_begin) * 768 + lane * 12;
         if (MODE == MODE_INT8W) lo_tab[i] = i8w_lo_table(g.clo[16 * cg + (lane & 15)]);
     }
     auto issue = [&](int t) {   /* stage t → ring slot t % D */
@@ -798,7 +829,10 @@ __global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
 #pragma unroll
         for (int q = 0; q < G::A_DMA; q++) dma_16(a_src[q] + (size_t)t * 2048, slot + a_dst[q]);
 #pragma unroll
-        for (int i = 0; i < FN; i++) dma_12(b_src[i] + (size_t)t * 768, slot + G::A_STAGE + (wave * FN + i) * 1024);
+        for (int i = 0; i < FN; i++) {
+            if (REC4) dma_16(b_src[i] + (size_t)t * 1024, slot + G::A_STAGE + (wave * FN + i) * 1024);
+            else dma_12(b_src[i] + (size_t)t * 768, slot + G::A_STAGE + (wave * FN + i) * 1024);
+        }
     };
     /* epilogue factors: loaded before the first DMAs (so waiting for them waits for no DMA), into LDS before the
      * first barrier */
@@ -903,11 +937,16 @@ __global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
         const int8_t *sa = ring + (t % D) * STAGE;
         const int8_t *sb = sa + G::A_STAGE + (wave * FN) * 1024 + lane * 16;
         /* all LDS reads of the stage first: FN weight records, 2·FM activation operands */
-        uint32_t rw[FN][3];
+        uint32_t rw[FN][4];
 #pragma unroll
         for (int i = 0; i < FN; i++) {
-            const uint32_t *p = reinterpret_cast<const uint32_t *>(sb + i * 1024);
-            rw[i][0] = p[0]; rw[i][1] = p[1]; rw[i][2] = p[2];
+            if (REC4) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(sb + i * 1024);
+                rw[i][0] = v.x; rw[i][1] = v.y; rw[i][2] = v.z; rw[i][3] = v.w;
+            } else {
+                const uint32_t *p = reinterpret_cast<const uint32_t *>(sb + i * 1024);
+                rw[i][0] = p[0]; rw[i][1] = p[1]; rw[i][2] = p[2]; rw[i][3] = 0u;
+            }
         }
         v4i av[2][FM];
 #pragma unroll
@@ -923,7 +962,8 @@ __global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
             for (int i = 0; i < FN; i++)
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
-                    const uint32_t sel = fv_sel<S>(rw[i][S], rw[i][2], d);
+                    const uint32_t sel = REC4 ? ((rw[i][2 * S + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u)
+                                              : fv_sel<S>(rw[i][S], rw[i][2], d);
                     if (MODE == MODE_INT8W) {
                         bw[S][i][d] = (int)perm(kI8wHiTable, lo_tab[i], sel);
                     } else {
@@ -997,6 +1037,48 @@ __global__ __launch_bounds__(G::NT, 1) void gemm_fv(GemmArgs g)
     }
     if (nst == 0) return;
     fold(block);
+    if (CSHUF) {
+        /* The outputs are staged through the ring (idle once the last stage is read) and stored as whole row
+         * segments: the matrix-core layout alone gives 16 rows × 64 bytes per store, which streams C to HBM at
+         * about two thirds of the rate of full row segments. Chunks of CJ row groups, padded rows. */
+        constexpr int SROW = G::BN + 4;
+        constexpr int CJF = (D * STAGE) / (16 * SROW * 4);
+        constexpr int CJ = CJF < FM ? CJF : FM;
+        static_assert(CJ >= 1, "staging chunk");
+        constexpr int LPR = G::BN / 4;   /* lanes per staged row */
+        constexpr int RPI = 64 / LPR;    /* rows per store instruction */
+        static_assert(64 % LPR == 0, "row segments per wave");
+        float *stg = reinterpret_cast<float *>(ring);
+        const int lr = lane / LPR, lc = lane % LPR;
+        lds_barrier();
+#pragma unroll
+        for (int j0 = 0; j0 < FM; j0 += CJ) {
+#pragma unroll
+            for (int j = j0; j < j0 + CJ && j < FM; j++)
+#pragma unroll
+                for (int i = 0; i < FN; i++) {
+                    const int nl = wave * 16 * FN + 16 * i + 4 * (lane >> 4);
+                    *reinterpret_cast<v4f *>(stg + (16 * (j - j0) + (lane & 15)) * SROW + nl) =
+                        v4f{run[i][j][0], run[i][j][1], run[i][j][2], run[i][j][3]};
+                }
+            lds_barrier();
+            const int rows = 16 * (min(j0 + CJ, FM) - j0);
+            for (int r = wave * RPI + lr; r < rows; r += 4 * RPI) {
+                const int m = m0 + 16 * j0 + r, n = n0 + 4 * lc;
+                if (m < M && n < N) {
+                    const v4f v = *reinterpret_cast<const v4f *>(stg + r * SROW + 4 * lc);
+                    if (g.c_vec4) {
+                        *reinterpret_cast<v4f *>(g.C + (size_t)m * g.ldc + n) = v;
+                    } else {
+                        float *cp = g.C + (size_t)m * g.ldc + n;
+                        cp[0] = v[0]; cp[1] = v[1]; cp[2] = v[2]; cp[3] = v[3];
+                    }
+                }
+            }
+            if (j0 + CJ < FM) lds_barrier();
+        }
+        return;
+    }
     /* every output of the lane is final: one burst of 16-byte stores, nothing waited on after it */
     if (g.c_vec4) {
 #pragma unroll
