@@ -104,15 +104,15 @@ static void scale_c(float *C, int M, int N, int ldc, float beta)
  * which does not change the value. */
 static void exact_chain(int M, int N, int K, float alpha, const float *A, int lda, const float *W, float *C, int ldc)
 {
-    for (int m = 0; m < M; m++)
-        for (int n = 0; n < N; n++) {
-            float c = C[(size_t)m * ldc + n];
-            for (int k = 0; k < K; k++) {
-                float a = alpha * A[(size_t)m * lda + k];
-                c = fmaf(a, W[(size_t)k * N + n], c);
-            }
-            C[(size_t)m * ldc + n] = c;
+    /* row at a time, k outer: every output still sees exactly the chain above, in k order */
+    for (int m = 0; m < M; m++) {
+        float *c = C + (size_t)m * ldc;
+        for (int k = 0; k < K; k++) {
+            float a = alpha * A[(size_t)m * lda + k];
+            const float *w = W + (size_t)k * N;
+            for (int n = 0; n < N; n++) c[n] = fmaf(a, w[n], c[n]);
         }
+    }
 }
 
 void p2o_sgemm_fvb_exact(int M, int N, int K, float alpha, const float *A, int lda,
@@ -216,12 +216,16 @@ void p2o_planes_i8(const uint8_t *signs, const uint8_t *flags, int K, int N, int
 
 void p2o_acc_i32(const int8_t *q, int M, int K, const int8_t *B, int N, int k0, int k1, int32_t *acc)
 {
-    for (int m = 0; m < M; m++)
-        for (int n = 0; n < N; n++) {
-            int32_t s = 0;
-            for (int k = k0; k < k1; k++) s += (int32_t)q[(size_t)m * K + k] * (int32_t)B[(size_t)k * N + n];
-            acc[(size_t)m * N + n] = s;
+    /* integer sums are exact, so the order of the k terms is free: a row of accumulators, k outer */
+    for (int m = 0; m < M; m++) {
+        int32_t *a = acc + (size_t)m * N;
+        for (int n = 0; n < N; n++) a[n] = 0;
+        for (int k = k0; k < k1; k++) {
+            const int32_t qk = q[(size_t)m * K + k];
+            const int8_t *b = B + (size_t)k * N;
+            for (int n = 0; n < N; n++) a[n] += qk * (int32_t)b[n];
         }
+    }
 }
 
 /* blas.c:1296-1370. Per K block of 1024 rows: f = (float)accS · c1 (+ fmaf((float)accT, c2, f) with two planes);

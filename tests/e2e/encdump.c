@@ -1,0 +1,51 @@
+/*  encdump.c – the reference engine's stages on one WAV file: log-mel, encoder, greedy decode.
+ *
+ *  Test infrastructure. oracle/Makefile links it with the reference's library sources in the same three ways as the
+ *  reference CLI (its own GEMMs, the GPU library, the oracle), so tests can compare the encoder output (the frames
+ *  after all 216 five-value linears and the projector) bit for bit, as well as the decoded token ids.
+ *
+ *  usage: encdump <weights_dir> <mono 16 kHz wav> <out.f32>
+ *  Writes T × 640 fp32 encoder frames (phonon2.h:395, encoder.c:725-751) to out.f32 and prints "T <T>" and the
+ *  token ids of p2_greedy_decode (phonon2.h:407) on stdout.
+ */
+#include "phonon2.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+
+int main(int argc, char **argv)
+{
+    if (argc != 4) {
+        fprintf(stderr, "usage: %s <weights_dir> <audio.wav> <out.f32>\n", argv[0]);
+        return 2;
+    }
+    P2Engine *e = p2_engine_open(argv[1]);
+    if (!e) return 1;
+    float *audio = NULL;
+    int n = 0, rate = 0, channels = 0;
+    if (p2_wav_read(argv[2], &audio, &n, &rate, &channels) != 0 || channels != 1 || rate != P2_SAMPLE_RATE) {
+        fprintf(stderr, "%s: a mono %d Hz WAV is expected\n", argv[2], P2_SAMPLE_RATE);
+        return 1;
+    }
+    float *mel = NULL;
+    int frames = 0;
+    if (p2_mel_spectrogram(audio, n, &mel, &frames) != 0) return 1;
+    const P2Model *m = p2_engine_model(e);
+    float *enc = NULL;
+    int T = 0;
+    if (p2_encoder(m, mel, frames, &enc, &T) != 0) return 1;
+    FILE *f = fopen(argv[3], "wb");
+    if (!f || fwrite(enc, sizeof(float), (size_t)T * P2_JOINT_DIM, f) != (size_t)T * P2_JOINT_DIM) return 1;
+    fclose(f);
+    P2Token *toks = NULL;
+    int nt = p2_greedy_decode(m, enc, T, &toks);
+    printf("T %d\n", T);
+    for (int i = 0; i < nt; i++) printf("%d%s", toks[i].id, i + 1 < nt ? " " : "\n");
+    if (nt == 0) printf("\n");
+    free(toks);
+    free(enc);
+    free(mel);
+    free(audio);
+    p2_engine_close(e);
+    return 0;
+}

@@ -1,0 +1,47 @@
+"""End to end on the GPU: the reference engine (built from its own sources, oracle/Makefile) with its quantised
+GEMMs bound to libphonon2_gemm.so, against the same engine with its own GEMMs (exact mode) and with the oracle's
+(int8w, int8), on a synthetic model in the reference's weights.bin format.
+
+The encoder frames – the output of all 24 blocks' 216 five-value linears, the int8 subsampling and projector
+linears and everything between them – must be bit-identical, and the greedy TDT decoder must emit the same token
+ids; the reference CLI (main.c --tokens, through p2_engine_open / p2_transcribe) must print the same ids."""
+import numpy as np
+import pytest
+
+from e2e import model, run
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not run.have("encdump_cpu", "encdump_gpu", "encdump_oracle", "phonon2_cpu",
+                                              "phonon2_gpu", "phonon2_oracle"),
+                                 reason="oracle/_ref engines not built")]
+
+
+@pytest.fixture(scope="module")
+def fx(tmp_path_factory):
+    d = tmp_path_factory.mktemp("e2e_gpu")
+    print(f"writing the synthetic model under {d}", flush=True)
+    model.write_model(str(d / "model"))
+    model.write_wav(str(d / "a.wav"), 3.0, seed=5)
+    model.write_wav(str(d / "b.wav"), 1.5, seed=11)
+    return str(d)
+
+
+@pytest.mark.parametrize("mode,reference", [("exact", "cpu"), ("int8w", "oracle"), ("int8", "oracle")])
+def test_encoder_frames_and_tokens(fx, mode, reference):
+    print(f"encdump_gpu vs encdump_{reference}, {mode}", flush=True)
+    got, got_ids = run.encdump("gpu", mode, fx + "/model", fx + "/a.wav", fx + f"/gpu_{mode}.f32")
+    ref, ref_ids = run.encdump(reference, mode, fx + "/model", fx + "/a.wav", fx + f"/{reference}_{mode}.f32")
+    neq = got.view(np.uint32) != ref.view(np.uint32)
+    assert not neq.any(), f"{neq.sum()} of {neq.size} encoder values differ; first at {np.argwhere(neq)[0]}"
+    assert got_ids == ref_ids
+    assert len(ref_ids) >= 8 and len(set(ref_ids)) >= 5, ref_ids
+
+
+@pytest.mark.parametrize("mode,reference", [("exact", "cpu"), ("int8w", "oracle")])
+def test_cli_token_ids(fx, mode, reference):
+    wavs = [fx + "/a.wav", fx + "/b.wav"]
+    print(f"phonon2_gpu vs phonon2_{reference}, {mode}", flush=True)
+    got = run.cli_tokens("gpu", mode, fx + "/model", wavs)
+    ref = run.cli_tokens(reference, mode, fx + "/model", wavs)
+    assert got == ref
+    assert all(len(v) > 0 for v in ref.values())
