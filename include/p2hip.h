@@ -70,6 +70,7 @@ void *p2h_event_create(void);
 int   p2h_event_destroy(void *event);
 int   p2h_event_record(void *event, void *stream);
 int   p2h_event_sync(void *event);
+int   p2h_stream_wait_event(void *stream, void *event);   /* later work on stream waits for event (also in capture) */
 float p2h_event_elapsed_ms(void *start, void *stop);   /* < 0 on error */
 
 /* ── five-value weights ─────────────────────────────────────────────────────────────────────────────────────────

@@ -306,6 +306,14 @@ int p2h_event_sync(void *event)
     return P2H_OK;
 }
 
+int p2h_stream_wait_event(void *stream, void *event)
+{
+    if (int rc = ensure_init()) return rc;
+    if (!event) return fail(P2H_E_ARG, "p2h_stream_wait_event: NULL event");
+    HIPCHK(hipStreamWaitEvent(stream_of(stream), (hipEvent_t)event, 0));
+    return P2H_OK;
+}
+
 float p2h_event_elapsed_ms(void *start, void *stop)
 {
     float ms = -1.0f;
@@ -543,12 +551,19 @@ using FvT6 = p2k::FvGeo<2, 1, 4, 6>;  /*  32 ×  64, 6 stages in flight */
 /* Large-M tiles (int8w): two workgroups per CU, 4-bit selector records, outputs staged through LDS */
 using FvW6 = p2k::FvGeo<6, 4, 4, 2>;  /*  96 × 256, 2 stages: K <= 1024 */
 using FvW8 = p2k::FvGeo<8, 2, 4, 3>;  /* 128 × 128, 3 stages: K > 1024, unsplit */
+/* Small-M tiles (gemm_fvs): operands straight to registers, K split across the four waves, 4-bit records */
+using SmS = p2k::SmGeo<2, 2, true>;     /*  32 ×  32 */
+using SmW = p2k::SmGeo<3, 4, true>;     /*  48 ×  64 (int8w) */
 enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_W8 = 9,
-       FV_COUNT = 10 };
+       FV_SS = 10, FV_SW = 11, FV_COUNT = 12 };
 const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
-                             FvW8::BM};
+                             FvW8::BM, SmS::BM, SmW::BM};
 const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN, FvW6::BN,
-                             FvW8::BN};
+                             FvW8::BN, SmS::BN, SmW::BN};
+/* gemm_fvs splits K among the four waves of a workgroup: at most four K segments, so K <= 4096 */
+inline bool small_ok(int K) { return K <= 4 * p2k::kFoldRows; }
+inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW; }
+inline bool uses_rec4(int cfg) { return cfg == FV_W6 || cfg == FV_W8 || cfg == FV_SS || cfg == FV_SW; }
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -573,11 +588,18 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     Plan p;
     /* measured on MI355X: 32 × 64 tiles are the fastest up to a thousand rows; beyond, the two-workgroups-per-CU
      * tiles on 4-bit records (int8w) or 128 × 128 (the two-plane mode needs twice the accumulators) */
-    int cfg = M <= 1024 ? FV_T : (mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_W8 : FV_W6) : FV_L);
+    int cfg;
+    if (M <= 1024)   /* small M: the register-streaming kernel, 48 × 64 for wide outputs at a few hundred rows */
+        cfg = !small_ok(K) ? FV_T : (K <= p2k::kFoldRows && N >= 2048 && M >= 256) ? FV_SW : FV_SS;
+    else
+        cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_W8 : FV_W6) : FV_L;
     cfg = env_int("P2H_TILE", cfg);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
     if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_W8)) cfg = FV_L;
-    const bool large = cfg == FV_W6 || cfg == FV_W8;   /* these never split K: the fold stays in registers */
+    if (mode == P2H_INT8 && cfg == FV_SW) cfg = FV_SS;
+    if (is_small(cfg) && !small_ok(K)) cfg = FV_T;
+    /* these never split K across workgroups: the fold stays in the kernel */
+    const bool large = cfg == FV_W6 || cfg == FV_W8 || is_small(cfg);
     p.cfg = cfg;
     p.tiles_m = (M + kFvBM[cfg] - 1) / kFvBM[cfg];
     p.tiles_n = (N + kFvBN[cfg] - 1) / kFvBN[cfg];
@@ -648,10 +670,20 @@ void launch_fv(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
     }
 }
 
+template <class G, int MODE>
+void launch_fvs(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
+{
+    hipLaunchKernelGGL((p2k::gemm_fvs<G, MODE>), dim3((unsigned)((size_t)p.tiles_m * p.tiles_n)), dim3(256), 0, s,
+                       g);
+}
+
 template <int MODE>
 void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     switch (p.cfg) {
+    case FV_SS: launch_fvs<SmS, MODE>(g, p, s); break;
+    case FV_SW: if (MODE == p2k::MODE_INT8W) { launch_fvs<SmW, p2k::MODE_INT8W>(g, p, s); break; }
+                launch_fvs<SmS, MODE>(g, p, s); break;
     case FV_T: launch_fv<FvT, MODE>(g, p, s); break;
     case FV_S: launch_fv<FvS, MODE>(g, p, s); break;
     case FV_M: launch_fv<FvM, MODE>(g, p, s); break;
@@ -682,9 +714,13 @@ const char *p2h_fvb_plan(int mode, int M, int N, int K, int with_workspace)
     static thread_local char buf[160];
     if (ensure_init() || M <= 0 || N <= 0 || K <= 0) return "";
     Plan p = make_plan(mode == P2H_INT8 ? P2H_INT8 : P2H_INT8W, M, N, K, with_workspace != 0);
-    snprintf(buf, sizeof buf, "tile %dx%d, %d split%s of %d rows%s", kFvBM[p.cfg], kFvBN[p.cfg], p.splits,
-             p.splits > 1 ? "s" : "", p.split_rows,
-             p.splits > 1 ? " + fold" : (K > p2k::kFoldRows ? ", folds in registers" : ""));
+    if (is_small(p.cfg))
+        snprintf(buf, sizeof buf, "tile %dx%d, K split across the workgroup's waves, fold in LDS", kFvBM[p.cfg],
+                 kFvBN[p.cfg]);
+    else
+        snprintf(buf, sizeof buf, "tile %dx%d, %d split%s of %d rows%s", kFvBM[p.cfg], kFvBN[p.cfg], p.splits,
+                 p.splits > 1 ? "s" : "", p.split_rows,
+                 p.splits > 1 ? " + fold" : (K > p2k::kFoldRows ? ", folds in registers" : ""));
     return buf;
 }
 
@@ -714,7 +750,7 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
     Plan p = make_plan(mode, M, N, K, workspace != nullptr);
     if (int rc = check_split_ws("p2h_fvb_gemm_q8a", p, workspace, workspace_bytes)) return rc;
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
-    g.rec = (p.cfg == FV_W6 || p.cfg == FV_W8) ? w->rec4 : w->rec;
+    g.rec = uses_rec4(p.cfg) ? w->rec4 : w->rec;
     g.units = w->units; g.clo = w->clo;
     if (mode == P2H_INT8W) {
         g.c1 = w->c1w;

@@ -5,6 +5,8 @@
  *    quant_rows     per-row int8 quantisation of fp32 activations (blas.c:1114-1145)
  *    gemm_i8        the int8 five-value GEMM on int8 MFMA (blas.c:1296-1370): packed planes → int8 codes in LDS,
  *                   v_mfma_i32_16x16x64_i8 with int32 accumulation, fp32 epilogue per 1024-row K block
+ *    gemm_fvs       the same for small M: operands streamed from global memory into registers, K split
+ *                   across the waves of a workgroup, partial sums combined and folded through LDS
  *    gemm_exact     the exact route (blas.c:838-987): fp32 panels expanded in LDS, one fmaf chain per output
  *    fv_pack_codes  the reference's pre-packed int8w code layout (blas.c:1372-1400)
  *    fv_repack / fv_repack4  the planes re-laid per matrix-core operand (3 and 4 bits per weight) at upload
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(256) void quant_rows(int M, int Mp, int K, const fl
                                                   int8_t *__restrict__ Q, int ldq, float *__restrict__ scales)
 {
     const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (m >= Mp) return;
     const int kst = ldq / 64, k16 = K / 16 * 16;
     if (m >= M) {
@@ -1102,6 +1104,212 @@ __global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
                     for (int r = 0; r < 4; r++) cp[r] = run[i][j][r];
                 }
             }
+    }
+}
+
+/* ── the small-M five-value GEMM ─────────────────────────────────────────────────────────────────────────────── */
+
+/* Small-M tile: a workgroup of four waves owns one BM × BN output tile (BM = 16·FM activation rows, BN = 16·FN
+ * weight columns) and splits K among its waves. Each wave loads its operands straight from global memory into
+ * registers – the tiled activations and the operand records are already in matrix-core order – two 128-row units
+ * per load batch, the next batch in flight while the current one is decoded and multiplied. No LDS staging and no
+ * barrier in the K loop. */
+template <int FM_, int FN_, bool REC4_>
+struct SmGeo {
+    static constexpr int FM = FM_, FN = FN_;
+    static constexpr bool REC4 = REC4_;
+    static constexpr int BM = 16 * FM, BN = 16 * FN;
+    static constexpr int PITCH = BN + 4;     /* int32 per row of a partial tile in LDS */
+    static constexpr int MAXSEG = 4;         /* K segments per tile (one per wave; K <= 4096) */
+    static constexpr int CH = 2;             /* 128-row units per load batch */
+};
+
+/* K segments of a small-M call: up to 1024 rows, four segments of ceil(units / 4) units inside the one fold block;
+ * beyond, one segment per 1024-row fold block (so every segment's int32 sum belongs to one block). */
+__host__ __device__ __forceinline__ int sm_seg_units(int units) { return units <= 8 ? (units + 3) / 4 : 8; }
+
+template <class G, int MODE, bool TWO_OUT>
+__device__ __forceinline__ void sm_unit_mma(const v4i (&a)[2][G::FM], const uint32_t (&r)[G::FN][4],
+                                            const uint32_t (&lo_tab)[G::FN], v4i (&acc)[G::FN][G::FM],
+                                            v4i (&accT)[TWO_OUT ? G::FN : 1][TWO_OUT ? G::FM : 1])
+{
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        v4i bw[G::FN], bt[TWO_OUT ? G::FN : 1];
+#pragma unroll
+        for (int i = 0; i < G::FN; i++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                uint32_t sel;
+                if (G::REC4) {
+                    sel = (r[i][2 * s + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u;
+                } else {
+                    const int sh = d + 4 * s - 2;
+                    const uint32_t fl = (sh >= 0 ? (r[i][2] >> sh) : (r[i][2] << -sh)) & 0x04040404u;
+                    sel = ((r[i][s] >> (2 * d)) & 0x03030303u) | fl;
+                }
+                if (MODE == MODE_INT8W) {
+                    bw[i][d] = (int)perm(kI8wHiTable, lo_tab[i], sel);
+                } else {
+                    bw[i][d] = (int)perm(kPlaneS, kPlaneS, sel);
+                    bt[TWO_OUT ? i : 0][d] = (int)perm(kPlaneS, 0u, sel);
+                }
+            }
+#pragma unroll
+        for (int j = 0; j < G::FM; j++)
+#pragma unroll
+            for (int i = 0; i < G::FN; i++) {
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[i], a[s][j], acc[i][j], 0, 0, 0);
+                if (TWO_OUT)
+                    accT[TWO_OUT ? i : 0][TWO_OUT ? j : 0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        bt[TWO_OUT ? i : 0], a[s][j], accT[TWO_OUT ? i : 0][TWO_OUT ? j : 0], 0, 0, 0);
+            }
+    }
+}
+
+/* The int8 five-value GEMM for small M (sgemm_i8_worker, blas.c:1296-1370). Each wave accumulates int32 sums over its
+ * K segments and writes them to LDS; after one barrier the workgroup adds the partial sums of each 1024-row block
+ * (exact in int32) and folds the blocks into fp32 in order, exactly as the reference does per K block
+ * (blas.c:1355-1366), storing C as whole row segments. */
+template <class G, int MODE>
+__global__ __launch_bounds__(256, 2) void gemm_fvs(GemmArgs g)
+{
+    constexpr bool TWO = (MODE == MODE_INT8);
+    constexpr int FM = G::FM, FN = G::FN, BM = G::BM, BN = G::BN, PITCH = G::PITCH, CH = G::CH;
+    constexpr int TILE = BM * PITCH;
+    __shared__ __attribute__((aligned(16))) int32_t part[(TWO ? 2 : 1) * G::MAXSEG * TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
+    const int n0 = tile_n * BN, m0 = tile_m * BM;
+    const int M = g.M, N = g.N, units = g.units;
+    const int seg_units = sm_seg_units(units);
+    const int nseg = (units + seg_units - 1) / seg_units;
+
+    /* per-lane operand addresses (row and column groups clamped into the padded operands; outputs are masked) */
+    const int8_t *a_base[FM];
+#pragma unroll
+    for (int j = 0; j < FM; j++) {
+        const int mg = min((m0 >> 4) + j, g.mg_last);
+        a_base[j] = g.Q + (size_t)mg * g.kst * 1024 + lane * 16;
+    }
+    const uint8_t *b_base[FN];
+    uint32_t lo_tab[FN];
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+        const int cg = min((n0 >> 4) + i, g.ng_last);
+        b_base[i] = g.rec + (size_t)cg * units * (G::REC4 ? 1024 : 768) + lane * (G::REC4 ? 16 : 12);
+        lo_tab[i] = MODE == MODE_INT8W ? i8w_lo_table(g.clo[16 * cg + (lane & 15)]) : 0u;
+    }
+
+    v4i a[2][CH][2][FM];
+    uint32_t r[2][CH][FN][4];
+    auto load_batch = [&](int buf, int u0, int nu) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int u = min(u0 + c, u0 + nu - 1);   /* a short last batch reloads its last unit (never used) */
+#pragma unroll
+            for (int j = 0; j < FM; j++)
+#pragma unroll
+                for (int s = 0; s < 2; s++)
+                    a[buf][c][s][j] = *reinterpret_cast<const v4i *>(a_base[j] + (size_t)(2 * u + s) * 1024);
+#pragma unroll
+            for (int i = 0; i < FN; i++) {
+                if (G::REC4) {
+                    const uint4 v = *reinterpret_cast<const uint4 *>(b_base[i] + (size_t)u * 1024);
+                    r[buf][c][i][0] = v.x; r[buf][c][i][1] = v.y; r[buf][c][i][2] = v.z; r[buf][c][i][3] = v.w;
+                } else {
+                    const uint3 v = *reinterpret_cast<const uint3 *>(b_base[i] + (size_t)u * 768);
+                    r[buf][c][i][0] = v.x; r[buf][c][i][1] = v.y; r[buf][c][i][2] = v.z; r[buf][c][i][3] = 0u;
+                }
+            }
+        }
+    };
+
+    for (int seg = wave; seg < nseg; seg += 4) {
+        const int u_begin = seg * seg_units, u_end = min(units, u_begin + seg_units);
+        v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                acc[i][j] = v4i{0, 0, 0, 0};
+                if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
+            }
+        /* batches of CH units, the next batch loading while the current one is multiplied (at most 8 units, 4 batches) */
+        load_batch(0, u_begin, min(CH, u_end - u_begin));
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int u0 = u_begin + b * CH;
+            if (u0 >= u_end) break;
+            if (u0 + CH < u_end) load_batch((b + 1) & 1, u0 + CH, min(CH, u_end - u0 - CH));
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                if (u0 + c < u_end) sm_unit_mma<G, MODE, TWO>(a[b & 1][c], r[b & 1][c], lo_tab, acc, accT);
+        }
+        /* this segment's int32 sums → LDS, [row][column] with padded rows */
+        int32_t *dst = part + seg * TILE;
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const int row = 16 * j + (lane & 15), col = 16 * i + 4 * (lane >> 4);
+                *reinterpret_cast<v4i *>(dst + row * PITCH + col) = acc[i][j];
+                if (TWO) *reinterpret_cast<v4i *>(dst + G::MAXSEG * TILE + row * PITCH + col) = accT[TWO ? i : 0][TWO ? j : 0];
+            }
+    }
+    __syncthreads();
+
+    /* fold: thread t owns rows t / (BN / 4) + 256 / (BN / 4)·q and four consecutive columns 4·(t % (BN / 4)) */
+    constexpr int TPR = BN / 4;                  /* threads per output row */
+    constexpr int RPP = 256 / TPR;               /* rows per pass */
+    const int cq = tid % TPR, n = n0 + 4 * cq;
+    if (n >= N) return;
+    v4f c1 = *reinterpret_cast<const v4f *>(g.c1 + n);
+    v4f c2 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (TWO) c2 = *reinterpret_cast<const v4f *>(g.c2 + n);
+    const bool beta_zero = g.beta == 0.0f;
+    const int nblocks = (units + 7) / 8;
+    for (int row = tid / TPR; row < BM; row += RPP) {
+        const int m = m0 + row;
+        if (m >= M) break;
+        const float as = g.a_scales[m] * g.alpha;
+        float *cp = g.C + (size_t)m * g.ldc + n;
+        float run[4];
+        if (!beta_zero) {
+            if (g.c_vec4) {
+                const v4f v = *reinterpret_cast<const v4f *>(cp);
+                run[0] = v[0]; run[1] = v[1]; run[2] = v[2]; run[3] = v[3];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) run[e] = cp[e];
+            }
+            if (g.beta != 1.0f) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) run[e] = run[e] * g.beta;
+            }
+        }
+        for (int blk = 0; blk < nblocks; blk++) {
+            /* the segments of this block: all of them below 1024 rows, else exactly the block's own */
+            const int s0 = units <= 8 ? 0 : blk, s1 = units <= 8 ? nseg : blk + 1;
+            v4i sum = v4i{0, 0, 0, 0}, sumT = v4i{0, 0, 0, 0};
+            for (int sg = s0; sg < s1; sg++) {
+                sum += *reinterpret_cast<const v4i *>(part + sg * TILE + row * PITCH + 4 * cq);
+                if (TWO) sumT += *reinterpret_cast<const v4i *>(part + G::MAXSEG * TILE + sg * TILE + row * PITCH + 4 * cq);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float f = (float)sum[e] * c1[e];
+                if (TWO) f = __builtin_fmaf((float)sumT[e], c2[e], f);
+                run[e] = (blk == 0 && beta_zero) ? f * as : __builtin_fmaf(f, as, run[e]);
+            }
+        }
+        if (g.c_vec4) {
+            *reinterpret_cast<v4f *>(cp) = v4f{run[0], run[1], run[2], run[3]};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) cp[e] = run[e];
+        }
     }
 }
 

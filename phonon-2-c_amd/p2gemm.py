@@ -54,6 +54,7 @@ _HIP_SIG = {
     "p2h_event_destroy": (_i, [_vp]),
     "p2h_event_record": (_i, [_vp, _vp]),
     "p2h_event_sync": (_i, [_vp]),
+    "p2h_stream_wait_event": (_i, [_vp, _vp]),
     "p2h_event_elapsed_ms": (_f, [_vp, _vp]),
     "p2h_fv_weight_upload": (_vp, [_vp, _vp, _vp, _vp, _i, _i]),
     "p2h_fv_weight_wrap": (_vp, [_vp, _vp, _vp, _vp, _i, _i]),
@@ -175,6 +176,10 @@ class Stream:
 
     def sync(self):
         sync(self.ptr)
+
+    def wait(self, event):
+        """Work queued on this stream after this call waits for `event` (a dependency edge under capture)."""
+        _ok(hip().p2h_stream_wait_event(self.ptr, event.ptr), "stream wait event")
 
     def __del__(self):
         try:
