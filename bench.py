@@ -69,19 +69,13 @@ class Scratch:
         self.ws = P.Workspace(split_bytes)
 
 
-def run_linear(lin, dA, lda, ws, stream, alpha=None, events=None):
-    """quantise A, then the q8a GEMM; events (e0, e1, e2) bracket the two kernels when given."""
+def run_linear(lin, dA, lda, ws, stream, alpha=None):
+    """Quantise A, then the q8a GEMM."""
     a = lin.alpha if alpha is None else alpha
     ldq = P.q_ld(lin.K)   # the linear's own row pitch: the shared buffer is sized for the widest
-    if events:
-        events[0].record(stream.ptr)
     P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr)
-    if events:
-        events[1].record(stream.ptr)
     P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, a, ws.q.ptr, ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr,
                        lin.N, ws.ws.ptr, ws.ws.nbytes, stream.ptr)
-    if events:
-        events[2].record(stream.ptr)
 
 
 def time_graph(graph, stream, steps, warmup):
@@ -99,19 +93,48 @@ def time_graph(graph, stream, steps, warmup):
     return e0.elapsed_ms(e1) / steps, wall
 
 
+def time_launches(launch, stream, reps):
+    """Average duration (ms) of one kernel launched `reps` times on `stream` behind a stream hold, between two HIP
+    events: the hold keeps the GPU busy while the host queues the launches, so they run back to back and the
+    figure is the kernel time plus the dispatch gap between consecutive kernels. If the host took longer to queue
+    them than the hold lasted, the measurement is repeated with a longer hold."""
+    launch()
+    stream.sync()
+    hold_us = 2000
+    for _ in range(4):
+        e0, e1 = P.Event(), P.Event()
+        stream.hold(hold_us)
+        e0.record(stream.ptr)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            launch()
+        host_us = (time.perf_counter() - t0) * 1e6
+        e1.record(stream.ptr)
+        e1.sync()
+        if host_us < 0.8 * hold_us:
+            return e0.elapsed_ms(e1) / reps
+        hold_us = min(1_000_000, int(2 * host_us) + 1000)
+    raise RuntimeError(f"host queued {reps} launches more slowly than a {hold_us} us hold")
+
+
 def kernel_times(linears, inputs, ws, stream, reps):
-    """Average duration (ms) of each linear's quantise and GEMM kernels, from HIP events on their stream."""
-    ev = [[P.Event() for _ in range(3)] for _ in linears]
+    """Duration (ms) of each linear's quantise and GEMM kernels, each timed on its own by time_launches."""
     q = np.zeros(len(linears))
-    g = np.zeros(len(linears))
-    for _ in range(reps):
-        for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
-            run_linear(lin, dA, lda, ws, stream, events=ev[i])
-        stream.sync()
-        for i in range(len(linears)):
-            q[i] += ev[i][0].elapsed_ms(ev[i][1])
-            g[i] += ev[i][1].elapsed_ms(ev[i][2])
-    return q / reps, g / reps
+    t = np.zeros(len(linears))
+    for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
+        ldq = P.q_ld(lin.K)
+        q[i] = time_launches(lambda: P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr),
+                             stream, reps)
+        t[i] = time_launches(lambda: P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, lin.alpha, ws.q.ptr, ldq,
+                                                        ws.s.ptr, lin.w, 0.0, lin.out.ptr, lin.N, ws.ws.ptr,
+                                                        ws.ws.nbytes, stream.ptr),
+                             stream, reps)
+    stream.sync()
+    return q, t
+
+
+def kernel_name(plan):
+    return "gemm_fvs" if "waves" in plan else "gemm_fv"
 
 
 # ── workloads ──────────────────────────────────────────────────────────────────────────────────────────────────
@@ -162,33 +185,19 @@ def sweep_spec(M=375):
     return spec
 
 
-def measure_chain(spec, stream, steps, warmup, kreps, side=None):
-    """Capture the chain into one graph. With `side` (a second stream), the linears that read a fresh input rather
-    than an earlier linear's output – the positional projections, whose input is the positional table
-    (encoder.c:500) – run on a parallel branch of the graph with their own quantisation scratch."""
+def measure_chain(spec, stream, steps, warmup, kreps):
+    """Capture the chain into one graph on one stream and time its replays; then, when kreps > 0, time each kernel
+    on its own. (A parallel graph branch for the positional projections, whose input is the positional table
+    rather than an earlier linear's output, measured slower on MI355X than the single chain.)"""
     linears, inputs, ws, keep = build_chain(spec, None)
-    branch = [i > 0 and spec[i][4] == "x" for i in range(len(spec))] if side is not None else [False] * len(spec)
-    side_ws = None
-    if any(branch):
-        bl = [l for l, b in zip(linears, branch) if b]
-        side_ws = Scratch(max(l.M for l in bl), max(l.K for l in bl),
-                          max(P.q8a_workspace_bytes("int8w", l.M, l.N, l.K) for l in bl))
-    fork, join = P.Event(), P.Event()
     with P.Graph(stream) as graph:
-        if side_ws is not None:
-            fork.record(stream.ptr)
-            side.wait(fork)
-            for lin, (dA, lda), b in zip(linears, inputs, branch):
-                if b:
-                    run_linear(lin, dA, lda, side_ws, side)
-            join.record(side.ptr)
-        for lin, (dA, lda), b in zip(linears, inputs, branch):
-            if not b:
-                run_linear(lin, dA, lda, ws, stream)
-        if side_ws is not None:
-            stream.wait(join)
+        for lin, (dA, lda) in zip(linears, inputs):
+            run_linear(lin, dA, lda, ws, stream)
     ms, wall = time_graph(graph, stream, steps, warmup)
-    qt, gt = kernel_times(linears, inputs, ws, stream, kreps)
+    if kreps > 0:
+        qt, gt = kernel_times(linears, inputs, ws, stream, kreps)
+    else:
+        qt, gt = np.full(len(linears), np.nan), np.full(len(linears), np.nan)
     return linears, ms, wall, qt, gt
 
 
@@ -201,10 +210,12 @@ def summarize(linears, ms, qt, gt):
         "tops": ops / (ms * 1e-3) / 1e12,
         "pct_int8_peak": 100.0 * ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS,
         "planes_gbs": planes / (ms * 1e-3) / 1e9,
-        "gemm_kernels_ms": [round(float(x), 5) for x in gt],
-        "quant_kernels_ms": [round(float(x), 5) for x in qt],
-        "gemm_kernel_gbs": [round(b / (t * 1e-3) / 1e9, 1) for b, t in zip(gbytes, gt)],
-        "gemm_kernel_tops": [round(gemm_ops(l.M, l.N, l.K) / (t * 1e-3) / 1e12, 1) for l, t in zip(linears, gt)],
+        "gemm_kernels_ms": None if np.isnan(gt).any() else [round(float(x), 5) for x in gt],
+        "quant_kernels_ms": None if np.isnan(qt).any() else [round(float(x), 5) for x in qt],
+        "gemm_kernel_gbs": None if np.isnan(gt).any() else [round(b / (t * 1e-3) / 1e9, 1)
+                                                             for b, t in zip(gbytes, gt)],
+        "gemm_kernel_tops": None if np.isnan(gt).any() else [round(gemm_ops(l.M, l.N, l.K) / (t * 1e-3) / 1e12, 1)
+                                                              for l, t in zip(linears, gt)],
     }
 
 
@@ -240,6 +251,23 @@ def cpu_baseline(M, shapes, seconds=8.0):
             f"P2_THREADS={cores}; {dt * 1e3:.2f} ms per pass"}
 
 
+def headline_roofline(lins, gt):
+    """The dominant GEMM of the headline chain (longest duration) against the HBM roofline."""
+    i = int(np.argmax(gt))
+    L = lins[i]
+    alg = gemm_bytes(L.M, L.N, L.K, 1)
+    achieved = alg / (gt[i] * 1e-3) / 1e9
+    plan = P.plan("int8w", L.M, L.N, L.K)
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(L, plan),
+                "kernel": f"{kernel_name(plan)}<int8w> M={L.M} K={L.K} N={L.N} ({plan})",
+                "algorithmic_bytes": int(alg), "avg_ms": gt[i],
+                "tops": round(gemm_ops(L.M, L.N, L.K) / (gt[i] * 1e-3) / 1e12, 1),
+                "pct_int8_peak": round(100 * gemm_ops(L.M, L.N, L.K) / (gt[i] * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2)}
+
+    return roofline
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +276,8 @@ def main():
     ap.add_argument("--workload", default="ffn375", choices=["ffn375", "m6000", "m38", "sweep", "exact375"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=200,
+                    help="back-to-back launches of each kernel for the per-kernel durations (0: skip them)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run device-to-device copies of this many MiB (the plain copy kernel that scales "
                          "FETCH_SIZE / WRITE_SIZE counter readings to bytes)")
@@ -272,8 +302,6 @@ def main():
     results = {}
 
     def run(name, spec, steps, warmup, kreps):
-        # one stream: a parallel graph branch for the positional projections (measure_chain's `side`) measured
-        # slower on MI355X than the single chain
         lins, ms, wall, qt, gt = measure_chain(spec, stream, steps, warmup, kreps)
         r = summarize(lins, ms, qt, gt)
         r["wall_s"] = round(wall, 3)
@@ -290,7 +318,7 @@ def main():
     }
     if main_wl == "exact375":
         raise SystemExit("exact375 is reported under extra; pick an int8 workload for the headline")
-    lins, r = run(main_wl, specs[main_wl](), args.steps, args.warmup, 20)
+    lins, r = run(main_wl, specs[main_wl](), args.steps, args.warmup, args.kernel_reps)
 
     extra = {}
     if not args.no_extra:
@@ -298,22 +326,17 @@ def main():
             if name == main_wl:
                 continue
             steps = {"m6000": 200, "m38": 2000, "sweep": 50}[name]
-            _, rr = run(name, specs[name](), steps, 20, 5 if name == "sweep" else 20)
+            _, rr = run(name, specs[name](), steps, 20, 0 if name == "sweep" else args.kernel_reps)
             extra[name] = rr
         extra["sweep_ms_per_30s_window"] = (results["sweep"][1]["ms_per_step"] if "sweep" in results else None)
         extra["exact375"] = exact_config(stream)
 
-    # dominant kernel of the headline workload: the GEMM with the largest share of the step
+    # dominant kernel of the headline workload: the GEMM with the longest duration
     gt = r["gemm_kernels_ms"]
-    i = int(np.argmax(gt))
-    L = lins[i]
-    alg = gemm_bytes(L.M, L.N, L.K, 1)
-    achieved = alg / (gt[i] * 1e-3) / 1e9
-    plan = P.plan("int8w", L.M, L.N, L.K)
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(L, plan),
-                "kernel": f"gemm_i8<int8w> M={L.M} K={L.K} N={L.N} ({plan})", "algorithmic_bytes": int(alg),
-                "avg_ms": gt[i]}
+    roofline = None
+    if gt is not None:
+        roofline = headline_roofline(lins, gt)
+
 
     ops = sum(gemm_ops(l.M, l.N, l.K) for l in lins)
     cpu = None if args.no_cpu_baseline else cpu_baseline(lins[0].M, [(l.K, l.N) for l in lins])
@@ -349,8 +372,8 @@ def main():
 
 def measured_traffic(L, plan):
     """HBM bytes per launch of this GEMM from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    (profiles/gemm_i8_traffic.json), when they were taken for the same shape and plan; otherwise None."""
-    path = os.path.join(ROOT, "profiles", "gemm_i8_traffic.json")
+    (profiles/gemm_fv_traffic.json), when they were taken for the same shape and plan; otherwise None."""
+    path = os.path.join(ROOT, "profiles", "gemm_fv_traffic.json")
     if not os.path.exists(path):
         return None
     for e in json.load(open(path))["entries"]:

@@ -72,6 +72,9 @@ int   p2h_event_record(void *event, void *stream);
 int   p2h_event_sync(void *event);
 int   p2h_stream_wait_event(void *stream, void *event);   /* later work on stream waits for event (also in capture) */
 float p2h_event_elapsed_ms(void *start, void *stop);   /* < 0 on error */
+/* Keep the stream busy for about usec microseconds (≤ 1 s) with one sleeping wave, so that launches queued behind it
+ * run back to back without host submission gaps: used to time single kernels. No counterpart in the reference. */
+int   p2h_stream_hold(void *stream, unsigned usec);
 
 /* ── five-value weights ─────────────────────────────────────────────────────────────────────────────────────────
  *  A device-resident five-value weight [K, N] (blas.h:38-45 FiveValueB; phonon2.h:116-126 Weight): the sign and

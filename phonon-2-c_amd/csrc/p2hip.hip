@@ -25,6 +25,7 @@ int g_init_rc = P2H_E_DEVICE;
 char g_init_err[512];
 char g_arch[64];
 int g_cus = 0;
+int g_wall_khz = 0;   /* rate of the constant wall clock that stream_hold reads */
 
 int fail(int rc, const char *fmt, ...)
 {
@@ -62,6 +63,8 @@ void do_init()
         return;
     }
     g_cus = prop.multiProcessorCount;
+    if (hipDeviceGetAttribute(&g_wall_khz, hipDeviceAttributeWallClockRate, 0) != hipSuccess || g_wall_khz <= 0)
+        g_wall_khz = 100000;
     e = hipSetDevice(0);
     if (e != hipSuccess) {
         snprintf(g_init_err, sizeof g_init_err, "p2h_init: hipSetDevice: %s", hipGetErrorString(e));
@@ -311,6 +314,17 @@ int p2h_stream_wait_event(void *stream, void *event)
     if (int rc = ensure_init()) return rc;
     if (!event) return fail(P2H_E_ARG, "p2h_stream_wait_event: NULL event");
     HIPCHK(hipStreamWaitEvent(stream_of(stream), (hipEvent_t)event, 0));
+    return P2H_OK;
+}
+
+int p2h_stream_hold(void *stream, unsigned usec)
+{
+    if (int rc = ensure_init()) return rc;
+    if (usec > 1000000u) return fail(P2H_E_ARG, "p2h_stream_hold: %u us is above the 1 s limit", usec);
+    const unsigned long long ticks = (unsigned long long)usec * (unsigned long long)g_wall_khz / 1000ull;
+    /* a nap is at least 8k cycles, i.e. over 2 us at any clock this device runs: usec/2 + 16 naps bound the wait */
+    hipLaunchKernelGGL(p2k::stream_hold, dim3(1), dim3(64), 0, stream_of(stream), ticks, usec / 2u + 16u);
+    HIPCHK(hipGetLastError());
     return P2H_OK;
 }
 

@@ -1545,6 +1545,14 @@ __global__ void fill_u32(uint32_t *__restrict__ p, size_t words, uint32_t value)
     if (idx < words) p[idx] = value;
 }
 
+/* One wave that sleeps until `ticks` of the constant-rate wall clock have passed, or `max_naps` naps of
+ * s_sleep 127 (about 8k cycles each) have been taken, whichever comes first: the wait ends on either bound. */
+__global__ __launch_bounds__(64) void stream_hold(unsigned long long ticks, unsigned max_naps)
+{
+    const unsigned long long t0 = wall_clock64();
+    for (unsigned i = 0; i < max_naps && wall_clock64() - t0 < ticks; ++i) __builtin_amdgcn_s_sleep(127);
+}
+
 __global__ void scale_c(int M, int N, float beta, float *__restrict__ C, int ldc)
 {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -56,6 +56,7 @@ _HIP_SIG = {
     "p2h_event_sync": (_i, [_vp]),
     "p2h_stream_wait_event": (_i, [_vp, _vp]),
     "p2h_event_elapsed_ms": (_f, [_vp, _vp]),
+    "p2h_stream_hold": (_i, [_vp, C.c_uint]),
     "p2h_fv_weight_upload": (_vp, [_vp, _vp, _vp, _vp, _i, _i]),
     "p2h_fv_weight_wrap": (_vp, [_vp, _vp, _vp, _vp, _i, _i]),
     "p2h_weight_free": (None, [_vp]),
@@ -180,6 +181,10 @@ class Stream:
     def wait(self, event):
         """Work queued on this stream after this call waits for `event` (a dependency edge under capture)."""
         _ok(hip().p2h_stream_wait_event(self.ptr, event.ptr), "stream wait event")
+
+    def hold(self, usec):
+        """Keep the stream busy for about `usec` microseconds, so launches queued behind run back to back."""
+        _ok(hip().p2h_stream_hold(self.ptr, int(usec)), "stream hold")
 
     def __del__(self):
         try:
