@@ -564,20 +564,20 @@ using FvS8 = p2k::FvGeo<4, 1, 4, 8>;  /*  64 ×  64, 8 stages in flight */
 using FvT6 = p2k::FvGeo<2, 1, 4, 6>;  /*  32 ×  64, 6 stages in flight */
 /* Large-M tiles (int8w): two workgroups per CU, 4-bit selector records, outputs staged through LDS */
 using FvW6 = p2k::FvGeo<6, 4, 4, 2>;  /*  96 × 256, 2 stages: K <= 1024 */
-using FvW8 = p2k::FvGeo<8, 2, 4, 3>;  /* 128 × 128, 3 stages: K > 1024, unsplit */
+using FvWK = p2k::FvGeo<6, 2, 4, 2>;  /*  96 × 128, 2 stages: K > 1024, unsplit (504 tiles at M = 6000, N = 1024) */
 /* Small-M tiles (gemm_fvs): operands straight to registers, K split across the four waves, 4-bit records */
 using SmS = p2k::SmGeo<2, 2, true>;     /*  32 ×  32 */
 using SmW = p2k::SmGeo<3, 4, true>;     /*  48 ×  64 (int8w) */
-enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_W8 = 9,
+enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_WK = 9,
        FV_SS = 10, FV_SW = 11, FV_COUNT = 12 };
 const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
-                             FvW8::BM, SmS::BM, SmW::BM};
+                             FvWK::BM, SmS::BM, SmW::BM};
 const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN, FvW6::BN,
-                             FvW8::BN, SmS::BN, SmW::BN};
+                             FvWK::BN, SmS::BN, SmW::BN};
 /* gemm_fvs splits K among the four waves of a workgroup: at most four K segments, so K <= 4096 */
 inline bool small_ok(int K) { return K <= 4 * p2k::kFoldRows; }
 inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW; }
-inline bool uses_rec4(int cfg) { return cfg == FV_W6 || cfg == FV_W8 || cfg == FV_SS || cfg == FV_SW; }
+inline bool uses_rec4(int cfg) { return cfg == FV_W6 || cfg == FV_WK || cfg == FV_SS || cfg == FV_SW; }
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -606,14 +606,14 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     if (M <= 1024)   /* small M: the register-streaming kernel, 48 × 64 for wide outputs at a few hundred rows */
         cfg = !small_ok(K) ? FV_T : (K <= p2k::kFoldRows && N >= 2048 && M >= 256) ? FV_SW : FV_SS;
     else
-        cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_W8 : FV_W6) : FV_L;
+        cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_WK : FV_W6) : FV_L;
     cfg = env_int("P2H_TILE", cfg);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
-    if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_W8)) cfg = FV_L;
+    if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_WK)) cfg = FV_L;
     if (mode == P2H_INT8 && cfg == FV_SW) cfg = FV_SS;
     if (is_small(cfg) && !small_ok(K)) cfg = FV_T;
     /* these never split K across workgroups: the fold stays in the kernel */
-    const bool large = cfg == FV_W6 || cfg == FV_W8 || is_small(cfg);
+    const bool large = cfg == FV_W6 || cfg == FV_WK || is_small(cfg);
     p.cfg = cfg;
     p.tiles_m = (M + kFvBM[cfg] - 1) / kFvBM[cfg];
     p.tiles_n = (N + kFvBN[cfg] - 1) / kFvBN[cfg];
@@ -705,7 +705,7 @@ void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
     case FV_S8: launch_fv<FvS8, MODE>(g, p, s); break;
     case FV_T6: launch_fv<FvT6, MODE>(g, p, s); break;
     case FV_W6: if (MODE == p2k::MODE_INT8W) { launch_fv_large<FvW6>(g, p, s); break; } /* fall through */
-    case FV_W8: if (MODE == p2k::MODE_INT8W) { launch_fv_large<FvW8>(g, p, s); break; } /* fall through */
+    case FV_WK: if (MODE == p2k::MODE_INT8W) { launch_fv_large<FvWK>(g, p, s); break; } /* fall through */
     case FV_X: if (MODE == p2k::MODE_INT8W) { launch_fv<FvX, p2k::MODE_INT8W>(g, p, s); break; } /* fall through */
     default: launch_fv<FvL, MODE>(g, p, s); break;
     }
