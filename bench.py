@@ -383,17 +383,27 @@ def measured_traffic(L, plan):
 
 
 def exact_config(stream):
-    """Config: one exact-mode five-value GEMM, M=375, K=1024, N=1024 (bench_gemm.c's route)."""
-    M, K, N = 375, 1024, 1024
-    signs, flags, lo, hi = P.gen_fv_weight(SEED, 77, K, N)
-    w = P.FvWeight(signs, flags, lo, hi, K, N)
-    dA = P.to_device(P.gen_activations(SEED, 78, M, K))
-    dC = P.DeviceBuffer(M * N * 4)
-    with P.Graph(stream) as g:
-        P.fvb_gemm_dev("exact", M, N, K, 1.0, dA.ptr, K, w, 0.0, dC.ptr, N, None, 0, stream.ptr)
-    ms, _ = time_graph(g, stream, 200, 20)
-    tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
-    return {"ms": round(ms, 5), "tflops": round(tf, 2), "pct_fp32_peak": round(100 * tf / PEAK_FP32_TFLOPS, 2)}
+    """The exact-mode five-value GEMM at M=375, K=1024, N=1024 (bench_gemm.c's route) on the fp32 matrix cores and on
+    the bit-exact fmaf-chain route (P2H_EXACT_CHAIN=1), and at the M=6000 FFN shapes on the matrix cores."""
+    out = {}
+    for name, (M, K, N), chain, reps in (("m375", (375, 1024, 1024), False, 200), ("m375_fmaf_chain", (375, 1024, 1024), True, 50),
+                                         ("m6000_up", (6000, 1024, 4096), False, 10),
+                                         ("m6000_down", (6000, 4096, 1024), False, 10)):
+        signs, flags, lo, hi = P.gen_fv_weight(SEED, 77, K, N)
+        w = P.FvWeight(signs, flags, lo, hi, K, N)
+        dA = P.to_device(P.gen_activations(SEED, 78, M, K))
+        dC = P.DeviceBuffer(M * N * 4)
+        if chain:
+            os.environ["P2H_EXACT_CHAIN"] = "1"
+        try:
+            with P.Graph(stream) as g:
+                P.fvb_gemm_dev("exact", M, N, K, 1.0, dA.ptr, K, w, 0.0, dC.ptr, N, None, 0, stream.ptr)
+        finally:
+            os.environ.pop("P2H_EXACT_CHAIN", None)
+        ms, _ = time_graph(g, stream, reps, 3)
+        tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2), "pct_fp32_peak": round(100 * tf / PEAK_FP32_TFLOPS, 2)}
+    return out
 
 
 if __name__ == "__main__":

@@ -824,6 +824,40 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
     return P2H_OK;
 }
 
+/* The exact five-value route on the fp32 matrix cores (gemm_xf): 32 × 64 tiles, or 32 × 32 where 32 × 64 would leave
+ * fewer than two workgroups per CU. P2H_EXACT_CHAIN=1 selects gemm_exact instead, the reference's per-output fmaf
+ * chain bit for bit; P2H_XF_TILE = 32 or 64 forces the tile width. */
+}  // extern "C"
+
+namespace {
+
+template <int FN>
+void launch_xf_tile(const p2k::ExactArgs &g, hipStream_t s)
+{
+    const dim3 grid((unsigned)((size_t)g.tiles_n * ((g.M + 31) / 32))), block(256);
+    const bool vec = g.K % 4 == 0 && g.lda % 4 == 0 && aligned(g.A, 16);
+    if (vec) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((p2k::gemm_xf<2, FN, false>), grid, block, 0, s, g);
+}
+
+int launch_xf(const p2k::ExactArgs &g0, hipStream_t s)
+{
+    p2k::ExactArgs g = g0;
+    const int cus = g_cus > 0 ? g_cus : 256;
+    int bn = ((size_t)((g.N + 63) / 64) * ((g.M + 31) / 32) >= (size_t)2 * cus) ? 64 : 32;
+    const int forced = env_int("P2H_XF_TILE", 0);
+    if (forced == 32 || forced == 64) bn = forced;
+    g.tiles_n = (g.N + bn - 1) / bn;
+    if (bn == 64) launch_xf_tile<4>(g, s);
+    else launch_xf_tile<2>(g, s);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 static size_t quant_area(int M, int K) { return align_up(p2h_q_bytes(M, K), 256) + align_up((size_t)M * 4, 256); }
 
 /* Workspace of the fp32-input entries: [split partials][quantised rows][row scales]. */
@@ -881,7 +915,9 @@ int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
     g.A = dA; g.lda = lda;
     g.signs = w->signs; g.flags = w->flags; g.lo = w->lo; g.hi = w->hi;
     g.C = dC; g.ldc = ldc;
-    return launch_exact(p2k::EXB_FV, g, s);
+    g.rec = w->rec4; g.units = w->units;
+    if (env_int("P2H_EXACT_CHAIN", 0) != 0 || K == 0) return launch_exact(p2k::EXB_FV, g, s);
+    return launch_xf(g, s);
 }
 
 int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, int ldq, const float *dScales,

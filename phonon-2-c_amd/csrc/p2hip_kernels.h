@@ -1368,6 +1368,7 @@ struct ExactArgs {
     const float *Bf; int ldbf; int transA, transB;        /* plain fp32 B (p2_sgemm) */
     float *C; int ldc;
     int tiles_n;
+    const uint8_t *rec; int units;                        /* 4-bit selector records (fv_repack4) for gemm_xf */
 };
 
 constexpr int EBM = 64, EBN = 64, EBK = 32;
@@ -1505,6 +1506,128 @@ __global__ __launch_bounds__(256) void gemm_exact(ExactArgs g)
         for (int j = 0; j < 4; j++) {
             const int n = n0 + 4 * tn + j;
             if (m < M && n < N) g.C[(size_t)m * g.ldc + n] = c[i][j];
+        }
+    }
+}
+
+/* The exact-mode five-value GEMM on the fp32 matrix cores (sgemm_fvb_exact, blas.c:929-987): C = beta·C +
+ * alpha·A·W with every weight expanded to fp32 as the reference expands it, w = (code − 1)·fmaf(flag, hi − lo, lo)
+ * (blas.c:875-897), and the products summed in fp32 by v_mfma_f32_16x16x4_f32. The sum runs in a different order
+ * from the reference's per-output fmaf chain (which gemm_exact keeps bit for bit), so outputs agree to fp32 rounding.
+ * A workgroup of four waves owns a BM × BN tile and splits K among its waves, as gemm_fvs does: each wave streams its
+ * units' weight records (the 4-bit selectors of fv_repack4) and fp32 rows into registers, expands the weights in
+ * registers and multiplies; lane l of the step t MFMA takes k = 16·(l / 16) + t of a 64-row step, which is the
+ * record's own order. The four partial tiles meet in LDS and are added in wave order.
+ * VEC: K % 4 == 0, lda % 4 == 0 and A 16-byte aligned. */
+template <int FM, int FN, bool VEC>
+__global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
+{
+    constexpr int BM = 16 * FM, BN = 16 * FN, PITCH = BN + 4, TILE = BM * PITCH;
+    __shared__ __attribute__((aligned(16))) float part[4 * TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
+    const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
+    const int n0 = tile_n * BN, m0 = tile_m * BM;
+    const int M = g.M, N = g.N, K = g.K, units = g.units;
+    const int su = (units + 3) / 4;
+    const int nseg = (units + su - 1) / su;
+    const int u_begin = min(units, wave * su), u_end = min(units, u_begin + su);
+
+    /* per-lane column constants: lo and hi − lo of column n0 + 16·i + l % 16 */
+    float wlo[FN], wd[FN];
+    const uint8_t *b_base[FN];
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+        const int n = min(n0 + 16 * i + (lane & 15), N - 1);
+        wlo[i] = g.lo[n];
+        wd[i] = g.hi[n] - wlo[i];
+        b_base[i] = g.rec + (size_t)(n >> 4) * units * 1024 + lane * 16;
+    }
+    const float *a_row[FM];
+#pragma unroll
+    for (int j = 0; j < FM; j++) a_row[j] = g.A + (size_t)min(m0 + 16 * j + (lane & 15), M - 1) * g.lda;
+
+    v4f acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load_x = [&](int j, int k0, float x[16]) __attribute__((always_inline)) {
+        if (VEC) {
+            load16<true>(a_row[j], k0, K, x);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) x[e] = (k0 + e < K) ? a_row[j][k0 + e] : 0.0f;
+        }
+    };
+
+    /* units double-buffered in registers: unit u + 1 loads while unit u is expanded and multiplied */
+    uint32_t r[2][FN][4];
+    float x[2][2][FM][16];
+    auto load_unit = [&](int buf, int u) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(b_base[i] + (size_t)u * 1024);
+            r[buf][i][0] = v.x; r[buf][i][1] = v.y; r[buf][i][2] = v.z; r[buf][i][3] = v.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int j = 0; j < FM; j++) load_x(j, 128 * u + 64 * s + 16 * grp, x[buf][s][j]);
+    };
+    auto mma_unit = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int t = 0; t < 16; t++) {
+                const int d = t >> 2, b = t & 3;
+                float w[FN];
+#pragma unroll
+                for (int i = 0; i < FN; i++) {
+                    const uint32_t nib = r[buf][i][2 * s + (d >> 1)] >> (8 * b + 4 * (d & 1));
+                    const float mag = __builtin_fmaf((float)((nib >> 2) & 1u), wd[i], wlo[i]);
+                    w[i] = (float)((int)(nib & 3u) - 1) * mag;
+                }
+#pragma unroll
+                for (int j = 0; j < FM; j++)
+#pragma unroll
+                    for (int i = 0; i < FN; i++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[i], x[buf][s][j][t], acc[i][j], 0, 0, 0);
+            }
+    };
+    if (u_begin < u_end) load_unit(0, u_begin);
+    for (int u = u_begin; u < u_end; u += 2) {
+        if (u + 1 < u_end) load_unit(1, u + 1);
+        mma_unit(0);
+        if (u + 1 >= u_end) break;
+        if (u + 2 < u_end) load_unit(0, u + 2);
+        mma_unit(1);
+    }
+    if (wave < nseg) {
+        float *dst = part + wave * TILE;
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int j = 0; j < FM; j++)
+                *reinterpret_cast<v4f *>(dst + (16 * j + (lane & 15)) * PITCH + 16 * i + 4 * grp) = acc[i][j];
+    }
+    __syncthreads();
+
+    constexpr int TPR = BN / 4, RPP = 256 / TPR;
+    const int cq = tid % TPR, n = n0 + 4 * cq;
+    if (n >= N) return;
+    for (int row = tid / TPR; row < BM; row += RPP) {
+        const int m = m0 + row;
+        if (m >= M) break;
+        v4f sum = *reinterpret_cast<const v4f *>(part + row * PITCH + 4 * cq);
+        for (int sg = 1; sg < nseg; sg++) sum += *reinterpret_cast<const v4f *>(part + sg * TILE + row * PITCH + 4 * cq);
+        float *cp = g.C + (size_t)m * g.ldc + n;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (n + e >= N) break;
+            const float c0 = g.beta == 0.0f ? 0.0f : (g.beta == 1.0f ? cp[e] : cp[e] * g.beta);
+            cp[e] = __builtin_fmaf(g.alpha, sum[e], c0);
         }
     }
 }

@@ -59,6 +59,16 @@ def main():
              O.EXACT: "fp32 expansion (exact)"}
     expect(L.p2_gemm_mode().decode() == names[mode_env], "p2_gemm_mode string")
 
+    chain = os.environ.get("P2H_EXACT_CHAIN", "0") not in ("", "0")
+
+    def same(out, ref, K):
+        """Bit-exact, except the five-value exact route (exact mode, or K % 4 != 0 in any mode, blas.c:1490-1493) on
+        the matrix cores: within 1e-4 of the reference's."""
+        if (mode_env == O.EXACT or K % 4 != 0) and not chain:
+            rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2, axis=1, keepdims=True))
+            return bool(np.all(np.abs(out.astype(np.float64) - ref) <= 1e-4 * np.maximum(np.abs(ref), rms)))
+        return np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
     seed = 7
     for (M, K, N, alpha, beta) in [(375, 1024, 1024, 1.0, 0.0), (38, 4096, 1024, 0.5, 1.0), (38, 1024, 1024, 1.0, 0.3),
                                    (5, 100, 48, 1.0, 0.0), (13, 6, 16, 1.0, 1.0)]:
@@ -69,11 +79,11 @@ def main():
         out = C0.copy()
         L.p2_sgemm_fvb(M, N, K, alpha, A.ctypes.data, K, C.byref(b), beta, out.ctypes.data, N)
         ref = O.sgemm_fvb(mode_env, A, signs, flags, lo, hi, N, alpha=alpha, beta=beta, C0=C0)
-        expect(np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"p2_sgemm_fvb {M}x{K}x{N}")
+        expect(same(out, ref, K), f"p2_sgemm_fvb {M}x{K}x{N}")
         # second call on the same weight: served from the device cache
         out2 = C0.copy()
         L.p2_sgemm_fvb(M, N, K, alpha, A.ctypes.data, K, C.byref(b), beta, out2.ctypes.data, N)
-        expect(np.array_equal(out2.view(np.uint32), ref.view(np.uint32)), f"p2_sgemm_fvb cached {M}x{K}x{N}")
+        expect(same(out2, ref, K), f"p2_sgemm_fvb cached {M}x{K}x{N}")
 
         qa = QuantA()
         rc = L.p2_quant_prepare(C.byref(qa), M, K)
@@ -94,7 +104,7 @@ def main():
     out = C0.copy()
     L.p2_sgemm_fvb(M, N, K, 1.5, A.ctypes.data, K + 3, C.byref(b), 1.0, out.ctypes.data, N + 5)
     ref = O.sgemm_fvb(mode_env, A, signs, flags, lo, hi, N, alpha=1.5, beta=1.0, C0=C0, K=K)
-    expect(np.array_equal(out.view(np.uint32), ref.view(np.uint32)), "p2_sgemm_fvb strided")
+    expect(same(out, ref, K), "p2_sgemm_fvb strided")
 
     # the pre-packed codes
     K, N = 64, 32

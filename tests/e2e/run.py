@@ -18,12 +18,16 @@ def have(*names):
 
 
 def env_for(mode):
+    """Environment of an engine run: mode "exact-chain" is exact mode with the GPU's five-value exact route on the
+    reference's per-output fmaf chain (P2H_EXACT_CHAIN=1), "exact" on the fp32 matrix cores."""
     e = dict(os.environ)
-    for k in ("P2_GEMM", "P2_EXACT", "P2_CACHE_CODES"):
+    for k in ("P2_GEMM", "P2_EXACT", "P2_CACHE_CODES", "P2H_EXACT_CHAIN"):
         e.pop(k, None)
     e["P2_THREADS"] = "8"
-    if mode == "exact":
+    if mode in ("exact", "exact-chain"):
         e["P2_EXACT"] = "1"
+        if mode == "exact-chain":
+            e["P2H_EXACT_CHAIN"] = "1"
     else:
         e["P2_GEMM"] = mode
     return e

@@ -11,11 +11,12 @@ pytestmark = pytest.mark.gpu
 CHILD = os.path.join(os.path.dirname(__file__), "dropin_child.py")
 
 
-@pytest.mark.parametrize("env", [{}, {"P2_GEMM": "int8"}, {"P2_GEMM": "exact"}, {"P2_GEMM": "int8", "P2_EXACT": "1"}])
+@pytest.mark.parametrize("env", [{}, {"P2_GEMM": "int8"}, {"P2_GEMM": "exact"}, {"P2_GEMM": "int8", "P2_EXACT": "1"},
+                                 {"P2_GEMM": "exact", "P2H_EXACT_CHAIN": "1"}])
 def test_dropin_mode(env):
     e = dict(os.environ)
-    e.pop("P2_GEMM", None)
-    e.pop("P2_EXACT", None)
+    for k in ("P2_GEMM", "P2_EXACT", "P2H_EXACT_CHAIN"):
+        e.pop(k, None)
     e.update(env)
     print(f"drop-in child with {env}", flush=True)
     r = subprocess.run([sys.executable, CHILD], env=e, capture_output=True, text=True, timeout=300)

@@ -3,8 +3,10 @@ GEMMs bound to libphonon2_gemm.so, against the same engine with its own GEMMs (e
 (int8w, int8), on a synthetic model in the reference's weights.bin format.
 
 The encoder frames – the output of all 24 blocks' 216 five-value linears, the int8 subsampling and projector
-linears and everything between them – must be bit-identical, and the greedy TDT decoder must emit the same token
-ids; the reference CLI (main.c --tokens, through p2_engine_open / p2_transcribe) must print the same ids."""
+linears and everything between them – must be bit-identical (exact mode on the fmaf-chain route, P2H_EXACT_CHAIN=1,
+and the int8 modes), and the greedy TDT decoder must emit the same token ids; the reference CLI (main.c --tokens,
+through p2_engine_open / p2_transcribe) must print the same ids. Exact mode on the fp32 matrix cores sums in another
+order: its frames agree to fp32 rounding and its token ids are identical."""
 import numpy as np
 import pytest
 
@@ -26,7 +28,7 @@ def fx(tmp_path_factory):
     return str(d)
 
 
-@pytest.mark.parametrize("mode,reference", [("exact", "cpu"), ("int8w", "oracle"), ("int8", "oracle")])
+@pytest.mark.parametrize("mode,reference", [("exact-chain", "cpu"), ("int8w", "oracle"), ("int8", "oracle")])
 def test_encoder_frames_and_tokens(fx, mode, reference):
     print(f"encdump_gpu vs encdump_{reference}, {mode}", flush=True)
     got, got_ids = run.encdump("gpu", mode, fx + "/model", fx + "/a.wav", fx + f"/gpu_{mode}.f32")
@@ -37,7 +39,20 @@ def test_encoder_frames_and_tokens(fx, mode, reference):
     assert len(ref_ids) >= 8 and len(set(ref_ids)) >= 5, ref_ids
 
 
-@pytest.mark.parametrize("mode,reference", [("exact", "cpu"), ("int8w", "oracle")])
+def test_encoder_exact_on_matrix_cores(fx):
+    """Exact mode on the fp32 matrix cores: the products are summed in another order than the reference's fmaf
+    chain, so frames agree to fp32 rounding carried through 24 blocks, and the token ids are identical."""
+    print("encdump_gpu (exact, matrix cores) vs encdump_cpu", flush=True)
+    got, got_ids = run.encdump("gpu", "exact", fx + "/model", fx + "/a.wav", fx + "/gpu_exact_mfma.f32")
+    ref, ref_ids = run.encdump("cpu", "exact", fx + "/model", fx + "/a.wav", fx + "/cpu_exact.f32")
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    err = np.max(np.abs(got.astype(np.float64) - ref)) / rms
+    print(f"max |gpu - cpu| / rms(frames) = {err:.3g}", flush=True)
+    assert err < 1e-3
+    assert got_ids == ref_ids
+
+
+@pytest.mark.parametrize("mode,reference", [("exact-chain", "cpu"), ("exact", "cpu"), ("int8w", "oracle")])
 def test_cli_token_ids(fx, mode, reference):
     wavs = [fx + "/a.wav", fx + "/b.wav"]
     print(f"phonon2_gpu vs phonon2_{reference}, {mode}", flush=True)
