@@ -145,7 +145,7 @@ def build_chain(spec, M_default):
     linears, inputs, fresh = [], [], {}
     for tid, K, N, M, src in spec:
         lin = Linear(tid, K, N, M)
-        if src == "x":
+        if src in ("x", "pos"):
             if (M, K) not in fresh:
                 fresh[(M, K)] = P.to_device(P.gen_activations(SEED, 10_000 + K + M, M, K))
             inputs.append((fresh[(M, K)].ptr, K))
@@ -165,7 +165,8 @@ def ffn_spec(M, base=1):
 def sweep_spec(M=375):
     """24 FastConformer blocks × 9 five-value linears at their real shapes (weights.c:371-379, encoder.c:333-613):
     ff1.l1, ff1.l2, qkv, pos (M = 2T−1), out, pw1, pw2, ff2.l1, ff2.l2. The d = 1024 stream chains through
-    ff1 → out → pw2 → ff2; qkv and pw1 read it; pos reads the positional rows."""
+    ff1 → out → pw2 → ff2; qkv and pw1 read it; pos reads the positional rows, the same for every block
+    (encoder.c:500), so the 24 positional projections run as one quantisation and one grouped launch."""
     spec = []
     for b in range(24):
         t = 100 + 16 * b
@@ -175,7 +176,7 @@ def sweep_spec(M=375):
             (t + 0, 1024, 4096, M, prev),         # i+0 ff1.linear1
             (t + 1, 4096, 1024, M, i + 0),        # i+1 ff1.linear2
             (t + 2, 1024, 3072, M, i + 1),        # i+2 qkv
-            (t + 3, 1024, 1024, 2 * M - 1, "x"),  # i+3 pos
+            (t + 3, 1024, 1024, 2 * M - 1, "pos"),  # i+3 pos
             (t + 4, 1024, 1024, M, i + 1),        # i+4 out
             (t + 5, 1024, 2048, M, i + 4),        # i+5 pw1
             (t + 6, 1024, 1024, M, i + 4),        # i+6 pw2
@@ -190,9 +191,22 @@ def measure_chain(spec, stream, steps, warmup, kreps):
     on its own. (A parallel graph branch for the positional projections, whose input is the positional table
     rather than an earlier linear's output, measured slower on MI355X than the single chain.)"""
     linears, inputs, ws, keep = build_chain(spec, None)
+    pos = [i for i, sp in enumerate(spec) if sp[4] == "pos"]
+    if pos:
+        P0 = linears[pos[0]]
+        pq = P.DeviceBuffer(P.q_bytes(P0.M, P0.K))
+        ps = P.DeviceBuffer(4 * P0.M)
+        keep["pos_q"] = (pq, ps)
     with P.Graph(stream) as graph:
-        for lin, (dA, lda) in zip(linears, inputs):
-            run_linear(lin, dA, lda, ws, stream)
+        if pos:   # the positional rows quantised once, every block's projection in one launch
+            P.quant_rows_dev(P0.M, P0.K, inputs[pos[0]][0], inputs[pos[0]][1], pq.ptr, P.q_ld(P0.K), ps.ptr,
+                             stream.ptr)
+            P.fvb_gemm_q8a_grouped_dev("int8w", P0.M, P0.N, P0.K, 1.0, pq.ptr, P.q_ld(P0.K), ps.ptr,   # alpha 1: encoder.c:500
+                                       [linears[i].w for i in pos], 0.0, [linears[i].out.ptr for i in pos], P0.N,
+                                       stream.ptr)
+        for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
+            if i not in pos:
+                run_linear(lin, dA, lda, ws, stream)
     ms, wall = time_graph(graph, stream, steps, warmup)
     if kreps > 0:
         qt, gt = kernel_times(linears, inputs, ws, stream, kreps)

@@ -118,6 +118,14 @@ size_t p2h_q_bytes(int M, int K); /* bytes of Q for M rows at ldq = p2h_q_ld(K) 
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                      const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
                      size_t workspace_bytes, void *stream);
+/* The same product for `groups` (<= 32) weights of one shape [K, N] against the same quantised rows, C_q = alpha·A·W_q
+ * + beta·C_q, in one launch where the small-M kernel serves the shape (M <= 1024, K <= 4096), otherwise one call per
+ * weight; results are those of p2h_fvb_gemm_q8a per weight. No counterpart in the reference: it batches products
+ * that share their activation rows, such as the 24 blocks' positional projections, which the reference runs as
+ * p2_sgemm_fvb calls on the same positional rows (encoder.c:500). */
+int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                             const float *dScales, const P2hWeight *const *w, int groups, float beta,
+                             float *const *dC, int ldc, void *stream);
 /* Bytes of workspace that let p2h_fvb_gemm_q8a split K across workgroups (0 when the call would not split). With
  * workspace NULL the call runs unsplit. A split call writes int32 partial sums per 1024-row block and a second
  * kernel adds them (exact) and folds the blocks in order, so results do not depend on the split. Calls sharing a

@@ -777,6 +777,58 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
     return P2H_OK;
 }
 
+int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                             const float *dScales, const P2hWeight *const *w, int groups, float beta,
+                             float *const *dC, int ldc, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_grouped: mode %d is not an int8 mode", mode);
+    if (groups < 0 || groups > p2k::kMaxGroups || (groups > 0 && (!w || !dC)))
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_grouped: %d groups (at most %d, non-NULL arrays)", groups,
+                    p2k::kMaxGroups);
+    for (int q = 0; q < groups; q++) {
+        if (!w[q] || w[q]->N != N || w[q]->K != K)
+            return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_grouped: weight %d is not [%d, %d]", q, K, N);
+        if (M > 0 && (!dC[q] || ldc < N)) return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_grouped: C %d or ldc invalid", q);
+    }
+    if (int rc = check_q("p2h_fvb_gemm_q8a_grouped", M, K, dQ, ldq, dScales)) return rc;
+    hipStream_t s = stream_of(stream);
+    if (M == 0 || groups == 0) return P2H_OK;
+    Plan p = make_plan(mode, M, N, K, false);
+    if (alpha == 0.0f || K == 0 || !is_small(p.cfg)) {   /* one call per weight: the same kernels, unsplit */
+        for (int q = 0; q < groups; q++)
+            if (int rc = p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, ldq, dScales, w[q], beta, dC[q], ldc, nullptr, 0,
+                                          stream))
+                return rc;
+        return P2H_OK;
+    }
+    if (beta != 0.0f && beta != 1.0f) {   /* pre-scale, as the single entry does (blas.c:1436) */
+        for (int q = 0; q < groups; q++)
+            if (int rc = p2h_scale_c(M, N, beta, dC[q], ldc, s)) return rc;
+        beta = 1.0f;
+    }
+    p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC[0], ldc, p, nullptr);
+    p2k::GroupArgs ga;
+    memset(&ga, 0, sizeof ga);
+    for (int q = 0; q < groups; q++) {
+        ga.rec[q] = w[q]->rec4; ga.clo[q] = w[q]->clo; ga.C[q] = dC[q];
+        ga.c1[q] = mode == P2H_INT8W ? w[q]->c1w : w[q]->lo;
+        ga.c2[q] = w[q]->c2;
+        if (!aligned(dC[q], 16)) g.c_vec4 = 0;
+    }
+    g.units = w[0]->units;
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n), (unsigned)groups), block(256);
+    if (mode == P2H_INT8)
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8>), grid, block, 0, s, g, ga);
+    else if (p.cfg == FV_SW)
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmW, p2k::MODE_INT8W>), grid, block, 0, s, g, ga);
+    else
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8W>), grid, block, 0, s, g, ga);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
 int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ldq, const P2hWeight *w,
                     int32_t *dAcc, int32_t *dAcc2, int ldacc, void *stream)
 {

@@ -1172,7 +1172,7 @@ __device__ __forceinline__ void sm_unit_mma(const v4i (&a)[2][G::FM], const uint
  * (exact in int32) and folds the blocks into fp32 in order, exactly as the reference does per K block
  * (blas.c:1355-1366), storing C as whole row segments. */
 template <class G, int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_fvs(GemmArgs g)
+__device__ __forceinline__ void fvs_tile(const GemmArgs &g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
     constexpr int FM = G::FM, FN = G::FN, BM = G::BM, BN = G::BN, PITCH = G::PITCH, CH = G::CH;
@@ -1311,6 +1311,32 @@ __global__ __launch_bounds__(256, 2) void gemm_fvs(GemmArgs g)
             for (int e = 0; e < 4; e++) cp[e] = run[e];
         }
     }
+}
+
+template <class G, int MODE>
+__global__ __launch_bounds__(256, 2) void gemm_fvs(GemmArgs g)
+{
+    fvs_tile<G, MODE>(g);
+}
+
+/* Several five-value weights of one shape against the same quantised activations, one launch: blockIdx.y picks the
+ * weight (its records, tables and output); everything else is gemm_fvs's. */
+constexpr int kMaxGroups = 32;
+struct GroupArgs {
+    const uint8_t *rec[kMaxGroups];
+    const uint8_t *clo[kMaxGroups];
+    const float *c1[kMaxGroups];
+    const float *c2[kMaxGroups];
+    float *C[kMaxGroups];
+};
+
+template <class G, int MODE>
+__global__ __launch_bounds__(256, 2) void gemm_fvs_grouped(GemmArgs g, GroupArgs ga)
+{
+    GemmArgs h = g;
+    const int q = blockIdx.y;
+    h.rec = ga.rec[q]; h.clo = ga.clo[q]; h.c1 = ga.c1[q]; h.c2 = ga.c2[q]; h.C = ga.C[q];
+    fvs_tile<G, MODE>(h);
 }
 
 /* The fold after a split GEMM: per output, the int32 partial sums of the splits inside each 1024-row block are

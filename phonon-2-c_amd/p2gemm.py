@@ -67,6 +67,7 @@ _HIP_SIG = {
     "p2h_q_ld": (_i, [_i]),
     "p2h_q_bytes": (C.c_size_t, [_i, _i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
+    "p2h_fvb_gemm_q8a_grouped": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _f, _vp, _i, _vp]),
     "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_plan": (C.c_char_p, [_i, _i, _i, _i, _i]),
     "p2h_fvb_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
@@ -338,6 +339,16 @@ def quant_rows_dev(M, K, dA, lda, dQ, ldq, dS, stream=None):
 def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=None, ws_bytes=0, stream=None):
     _ok(hip().p2h_fvb_gemm_q8a(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, ws,
                                ws_bytes, stream), "p2h_fvb_gemm_q8a")
+
+
+def fvb_gemm_q8a_grouped_dev(mode, M, N, K, alpha, dQ, ldq, dS, weights, beta, dCs, ldc, stream=None):
+    """p2h_fvb_gemm_q8a_grouped: one product per weight against the same quantised rows, outputs dCs[i]."""
+    n = len(weights)
+    assert len(dCs) == n
+    wa = (C.c_void_p * max(n, 1))(*[w.ptr for w in weights])
+    ca = (C.c_void_p * max(n, 1))(*dCs)
+    _ok(hip().p2h_fvb_gemm_q8a_grouped(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, wa, n, beta, ca, ldc,
+                                       stream), "p2h_fvb_gemm_q8a_grouped")
 
 
 def fvb_gemm_dev(mode, M, N, K, alpha, dA, lda, w, beta, dC, ldc, ws, ws_bytes, stream=None):

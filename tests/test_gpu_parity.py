@@ -232,6 +232,35 @@ def test_sgemm_fp32(tA, tB):
     assert np.allclose(got, ref, rtol=1e-4, atol=1e-4)
 
 
+# ── several weights against the same quantised rows in one launch ─────────────────────────────────────────────────
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+@pytest.mark.parametrize("M,K,N,groups,beta", [(749, 1024, 1024, 24, 0.0), (375, 1024, 4096, 3, 1.0),
+                                               (38, 4096, 1024, 5, 0.5), (2000, 1024, 256, 2, 0.0)])
+def test_grouped_q8a(mode, M, K, N, groups, beta):
+    """Each group's output equals its own p2h_fvb_gemm_q8a call bit for bit (2000 rows: the per-weight path)."""
+    A = P.gen_activations(SEED, 1500 + M, M, K)
+    q, sc = O.quant_rows(A)
+    ws = [P.FvWeight(*_weight(K, N, 1600 + i), K, N) for i in range(groups)]
+    C0 = P.gen_activations(SEED, 1700 + N, M, N)
+    ldq = P.q_ld(K)
+    dQ, dS = P.to_device(P.q_tile(q, ldq)), P.to_device(sc)
+    outs = [P.to_device(C0) for _ in range(groups)]
+    P.fvb_gemm_q8a_grouped_dev(mode, M, N, K, 0.8, dQ.ptr, ldq, dS.ptr, ws, beta, [o.ptr for o in outs], N)
+    for i, (w, o) in enumerate(zip(ws, outs)):
+        got = o.download((M, N), np.float32)
+        single = P.fvb_gemm_q8a(mode, q, sc, w, alpha=0.8, beta=beta, C0=C0)
+        assert _bits_equal(got, single), f"group {i}"
+    signs, flags, lo, hi = _weight(K, N, 1600 + groups - 1)
+    rows = np.arange(min(M, 64))
+    if beta == 0.0:
+        ref = O.gemm_i8_run(mode, q[rows], sc[rows], signs, flags, lo, hi, N, alpha=0.8)
+    else:   # beta outside {0, 1} pre-scales C in fp32 (blas.c:1436), then the product accumulates
+        C0s = C0[rows] if beta == 1.0 else (C0[rows] * np.float32(beta)).astype(np.float32)
+        ref = O.gemm_i8_run(mode, q[rows], sc[rows], signs, flags, lo, hi, N, alpha=0.8, C0=C0s, beta_zero=False)
+    _assert_fp32(outs[-1].download((M, N), np.float32)[rows], ref)
+
+
 # ── full-size shapes, sampled rows ──────────────────────────────────────────────────────────────────────────────
 
 @pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024), (749, 1024, 1024), (375, 1024, 3072)])
