@@ -344,6 +344,7 @@ def main():
             extra[name] = rr
         extra["sweep_ms_per_30s_window"] = (results["sweep"][1]["ms_per_step"] if "sweep" in results else None)
         extra["exact375"] = exact_config(stream)
+        extra["attention375"] = attention_config(stream)
 
     # dominant kernel of the headline workload: the GEMM with the longest duration
     gt = r["gemm_kernels_ms"]
@@ -418,6 +419,26 @@ def exact_config(stream):
         tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
         out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2), "pct_fp32_peak": round(100 * tf / PEAK_FP32_TFLOPS, 2)}
     return out
+
+
+def attention_config(stream, H=16, T=375, Dh=64):
+    """The fp32 per-head products of one block's relative-position attention at T = 375 (encoder.c:505-519), every
+    head in one p2h_sgemm_batched launch each: Q_u·K_t [T, T], Q_v·P_t [T, 2T−1], scores·V [T, Dh]."""
+    rng = np.random.default_rng(SEED)
+    L = 2 * T - 1
+    bufs = {k: P.to_device(rng.standard_normal(sh).astype(np.float32)) for k, sh in
+            (("qu", (H, T, Dh)), ("kt", (H, Dh, T)), ("pt", (H, Dh, L)), ("s", (H, T, T)), ("v", (H, T, Dh)))}
+    out = {k: P.DeviceBuffer(H * T * n * 4) for k, n in (("ac", T), ("bd", L), ("ctx", Dh))}
+    calls = ((T, T, Dh, "qu", "kt", "ac"), (T, L, Dh, "qu", "pt", "bd"), (T, Dh, T, "s", "v", "ctx"))
+    with P.Graph(stream) as g:
+        for M, N, K, a, b, c in calls:
+            P.sgemm_batched_dev(False, False, M, N, K, 1.0, bufs[a].ptr, K, M * K, bufs[b].ptr, N, K * N, 0.0,
+                                out[c].ptr, N, M * N, H, stream.ptr)
+    ms, _ = time_graph(g, stream, 200, 10)
+    flops = sum(2.0 * H * M * N * K for M, N, K, *_ in calls)
+    return {"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "pct_fp32_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 2),
+            "what": f"{H} heads, T={T}, Dh={Dh}: 3 batched fp32 products per block"}
 
 
 if __name__ == "__main__":

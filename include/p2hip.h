@@ -158,9 +158,16 @@ int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
                  int ldb, const float *dBscales, float beta, float *dC, int ldc, void *workspace,
                  size_t workspace_bytes, void *stream);
 
-/* ── fp32 GEMM (p2_sgemm, blas.h:25-29): C = alpha · op(A) · op(B) + beta · C, row-major, trans 0/1 ──────── */
+/* ── fp32 GEMM (p2_sgemm, blas.h:25-29): C = alpha · op(A) · op(B) + beta · C, row-major, trans 0/1 ──────── *
+ *  On the fp32 matrix cores: sums in their order, within fp32 rounding of the reference's. */
 int p2h_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
               const float *dB, int ldb, float beta, float *dC, int ldc, void *stream);
+/* The same for `batch` (<= 65535) products in one launch, entry b at A + b·strideA, B + b·strideB, C + b·strideC
+ * (strides in floats): the per-head products of attention, which the reference runs as one p2_sgemm_st per
+ * (head, row block) (heads_gemm, encoder.c:279-316, 505-519). */
+int p2h_sgemm_batched(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
+                      long long strideA, const float *dB, int ldb, long long strideB, float beta, float *dC, int ldc,
+                      long long strideC, int batch, void *stream);
 
 #ifdef __cplusplus
 }

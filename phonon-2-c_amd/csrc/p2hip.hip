@@ -868,10 +868,8 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
     if (tiles == 0) return P2H_OK;
     if (bkind == p2k::EXB_FV)
         hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_FV>, dim3((unsigned)tiles), dim3(256), 0, s, g);
-    else if (bkind == p2k::EXB_Q8)
-        hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_Q8>, dim3((unsigned)tiles), dim3(256), 0, s, g);
     else
-        hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_F32>, dim3((unsigned)tiles), dim3(256), 0, s, g);
+        hipLaunchKernelGGL(p2k::gemm_exact<p2k::EXB_Q8>, dim3((unsigned)tiles), dim3(256), 0, s, g);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -1044,25 +1042,41 @@ int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
     return launch_exact(p2k::EXB_Q8, g, s);
 }
 
-int p2h_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
-              const float *dB, int ldb, float beta, float *dC, int ldc, void *stream)
+int p2h_sgemm_batched(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
+                      long long strideA, const float *dB, int ldb, long long strideB, float beta, float *dC, int ldc,
+                      long long strideC, int batch, void *stream)
 {
     if (int rc = ensure_init()) return rc;
-    if (M < 0 || N < 0 || K < 0) return fail(P2H_E_ARG, "p2h_sgemm: negative shape");
-    if (M > 0 && N > 0 && (!dC || ldc < N)) return fail(P2H_E_ARG, "p2h_sgemm: bad C");
-    if (M > 0 && N > 0 && K > 0 &&
+    if (M < 0 || N < 0 || K < 0 || batch < 0 || batch > 65535)
+        return fail(P2H_E_ARG, "p2h_sgemm_batched: shape %d x %d x %d, batch %d", M, N, K, batch);
+    if (M > 0 && N > 0 && batch > 0 && (!dC || ldc < N)) return fail(P2H_E_ARG, "p2h_sgemm: bad C");
+    if (M > 0 && N > 0 && K > 0 && batch > 0 &&
         (!dA || !dB || lda < (transA ? M : K) || ldb < (transB ? K : N)))
         return fail(P2H_E_ARG, "p2h_sgemm: bad A/B");
     hipStream_t s = stream_of(stream);
-    if (M == 0 || N == 0) return P2H_OK;
-    if (alpha == 0.0f || K == 0) return p2h_scale_c(M, N, beta, dC, ldc, s);   /* blas.c:748-749 */
-    p2k::ExactArgs g;
+    if (M == 0 || N == 0 || batch == 0) return P2H_OK;
+    if (alpha == 0.0f || K == 0) {   /* blas.c:748-749 */
+        for (int b = 0; b < batch; b++)
+            if (int rc = p2h_scale_c(M, N, beta, dC + (size_t)b * strideC, ldc, s)) return rc;
+        return P2H_OK;
+    }
+    p2k::SgemmArgs g;
     memset(&g, 0, sizeof g);
     g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
-    g.A = dA; g.lda = lda; g.transA = transA ? 1 : 0;
-    g.Bf = dB; g.ldbf = ldb; g.transB = transB ? 1 : 0;
-    g.C = dC; g.ldc = ldc;
-    return launch_exact(p2k::EXB_F32, g, s);
+    g.A = dA; g.lda = lda; g.sA = strideA; g.transA = transA ? 1 : 0;
+    g.B = dB; g.ldb = ldb; g.sB = strideB; g.transB = transB ? 1 : 0;
+    g.C = dC; g.ldc = ldc; g.sC = strideC;
+    g.tiles_n = (N + 63) / 64;
+    const dim3 grid((unsigned)((size_t)g.tiles_n * ((M + 63) / 64)), (unsigned)batch);
+    hipLaunchKernelGGL(p2k::sgemm_f32, grid, dim3(256), 0, s, g);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float *dA, int lda,
+              const float *dB, int ldb, float beta, float *dC, int ldc, void *stream)
+{
+    return p2h_sgemm_batched(transA, transB, M, N, K, alpha, dA, lda, 0, dB, ldb, 0, beta, dC, ldc, 0, 1, stream);
 }
 
 }  // extern "C"

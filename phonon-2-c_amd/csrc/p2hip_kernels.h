@@ -1114,14 +1114,15 @@ __global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
  * registers – the tiled activations and the operand records are already in matrix-core order – two 128-row units
  * per load batch, the next batch in flight while the current one is decoded and multiplied. No LDS staging and no
  * barrier in the K loop. */
-template <int FM_, int FN_, bool REC4_>
+template <int FM_, int FN_, bool REC4_, int CH_ = 2>
 struct SmGeo {
     static constexpr int FM = FM_, FN = FN_;
     static constexpr bool REC4 = REC4_;
     static constexpr int BM = 16 * FM, BN = 16 * FN;
     static constexpr int PITCH = BN + 4;     /* int32 per row of a partial tile in LDS */
     static constexpr int MAXSEG = 4;         /* K segments per tile (one per wave; K <= 4096) */
-    static constexpr int CH = 2;             /* 128-row units per load batch */
+    static constexpr int CH = CH_;           /* 128-row units per load batch (two batches in registers) */
+    static_assert(CH == 1 || CH == 2 || CH == 4 || CH == 8, "batches divide a segment's 8 units");
 };
 
 /* K segments of a small-M call: up to 1024 rows, four segments of ceil(units / 4) units inside the one fold block;
@@ -1236,10 +1237,10 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
                 acc[i][j] = v4i{0, 0, 0, 0};
                 if (TWO) accT[TWO ? i : 0][TWO ? j : 0] = v4i{0, 0, 0, 0};
             }
-        /* batches of CH units, the next batch loading while the current one is multiplied (at most 8 units, 4 batches) */
+        /* batches of CH units, the next batch loading while the current one is multiplied (at most 8 units) */
         load_batch(0, u_begin, min(CH, u_end - u_begin));
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
+        for (int b = 0; b < 8 / CH; b++) {
             const int u0 = u_begin + b * CH;
             if (u0 >= u_end) break;
             if (u0 + CH < u_end) load_batch((b + 1) & 1, u0 + CH, min(CH, u_end - u0 - CH));
@@ -1391,7 +1392,6 @@ struct ExactArgs {
     const float *A; int lda; int a_vec4;                  /* a_vec4: lda % 4 == 0 and A 16-B aligned */
     const uint8_t *signs; const uint8_t *flags; const float *lo; const float *hi;   /* five-value */
     const int8_t *B8; int ldb; const float *bscales;      /* int8 table */
-    const float *Bf; int ldbf; int transA, transB;        /* plain fp32 B (p2_sgemm) */
     float *C; int ldc;
     int tiles_n;
     const uint8_t *rec; int units;                        /* 4-bit selector records (fv_repack4) for gemm_xf */
@@ -1399,7 +1399,7 @@ struct ExactArgs {
 
 constexpr int EBM = 64, EBN = 64, EBK = 32;
 
-enum { EXB_FV = 0, EXB_Q8 = 1, EXB_F32 = 2 };
+enum { EXB_FV = 0, EXB_Q8 = 1 };
 
 /* 256 threads; thread (tm, tn) owns rows 4tm..4tm+3 and columns 4tn..4tn+3 of a 64 × 64 tile. The B panel is
  * expanded to fp32 in LDS as blas.c:877-897 expands it (w = (code−1) · fmaf(flag, hi − lo, lo)), A enters LDS as
@@ -1446,7 +1446,7 @@ __global__ __launch_bounds__(256) void gemm_exact(ExactArgs g)
         for (int c = 0; c < 8; c++) {
             const int k = k0 + ak + c;
             float v = 0.0f;
-            if (m < M && k < K) v = g.transA ? g.A[(size_t)k * g.lda + m] : g.A[(size_t)m * g.lda + k];
+            if (m < M && k < K) v = g.A[(size_t)m * g.lda + k];
             ra[c] = g.alpha * v;
         }
         const int k = k0 + wk;
@@ -1461,19 +1461,11 @@ __global__ __launch_bounds__(256) void gemm_exact(ExactArgs g)
                 const int code = (s >> (2 * c)) & 3, fl = (f >> c) & 1;
                 rw[c] = (float)(code - 1) * __builtin_fmaf((float)fl, wd[c], wlo[c]);
             }
-        } else if (BKIND == EXB_Q8) {
+        } else {
 #pragma unroll
             for (int c = 0; c < 8; c++) {
                 const int8_t q = (wcol_ok && k < K) ? g.B8[(size_t)k * g.ldb + n0 + wn + c] : (int8_t)0;
                 rw[c] = (float)q * wlo[c];
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const int n = n0 + wn + c;
-                float v = 0.0f;
-                if (n < N && k < K) v = g.transB ? g.Bf[(size_t)n * g.ldbf + k] : g.Bf[(size_t)k * g.ldbf + n];
-                rw[c] = v;
             }
         }
     };
@@ -1656,6 +1648,108 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
             cp[e] = __builtin_fmaf(g.alpha, sum[e], c0);
         }
     }
+}
+
+/* fp32 GEMMs on the matrix cores, batched with strides (p2_sgemm / p2_sgemm_st, blas.h:25-36, and the per-head
+ * products of attention, encoder.c:279-316, 505-519): C_b = alpha·op(A_b)·op(B_b) + beta·C_b for b < batch, all
+ * row-major. A workgroup of four waves (2 × 2) owns a 64 × 64 tile of one batch entry; K advances 16 columns per
+ * stage, the A and B panels staged k-major in LDS (double-buffered, one barrier per stage) so that the step-t MFMA's
+ * lane l reads A[m = l % 16][k = 4t + l / 16] and B[k][n = l % 16] conflict-free. B is the MFMA's first operand, so a
+ * lane's four results are four consecutive n of one row. Sums run in the matrix cores' order (fp32 rounding, not the
+ * reference's order). */
+struct SgemmArgs {
+    int M, N, K;
+    float alpha, beta;
+    const float *A; int lda; long long sA; int transA;
+    const float *B; int ldb; long long sB; int transB;
+    float *C; int ldc; long long sC;
+    int tiles_n;
+};
+
+__global__ __launch_bounds__(256, 2) void sgemm_f32(SgemmArgs g)
+{
+    constexpr int BMS = 64, BNS = 64, BKS = 16;
+    __shared__ __attribute__((aligned(16))) float sA[2][BKS][BMS + 4];
+    __shared__ __attribute__((aligned(16))) float sB[2][BKS][BNS + 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;                        /* this wave's 32 × 32 quarter */
+    const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
+    const int m0 = tile_m * BMS, n0 = tile_n * BNS;
+    const float *A = g.A + (size_t)blockIdx.y * g.sA;
+    const float *B = g.B + (size_t)blockIdx.y * g.sB;
+    float *C = g.C + (size_t)blockIdx.y * g.sC;
+    const int M = g.M, N = g.N, K = g.K;
+
+    /* loader: thread tid brings 4 values of each panel per stage */
+    float ra[4], rb[4];
+    auto load = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            int m, k;
+            if (g.transA) { k = tid / 16; m = 4 * (tid % 16) + e; }   /* A stored [k][m]: rows of m contiguous */
+            else { m = tid / 4; k = 4 * (tid % 4) + e; }               /* A stored [m][k] */
+            const int gm = m0 + m, gk = k0 + k;
+            ra[e] = (gm < M && gk < K) ? (g.transA ? A[(size_t)gk * g.lda + gm] : A[(size_t)gm * g.lda + gk]) : 0.0f;
+            int n, kb;
+            if (g.transB) { n = tid / 4; kb = 4 * (tid % 4) + e; }     /* B stored [n][k] */
+            else { kb = tid / 16; n = 4 * (tid % 16) + e; }            /* B stored [k][n] */
+            const int gn = n0 + n, gkb = k0 + kb;
+            rb[e] = (gn < N && gkb < K) ? (g.transB ? B[(size_t)gn * g.ldb + gkb] : B[(size_t)gkb * g.ldb + gn]) : 0.0f;
+        }
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (g.transA) sA[buf][tid / 16][4 * (tid % 16) + e] = ra[e];
+            else sA[buf][4 * (tid % 4) + e][tid / 4] = ra[e];
+            if (g.transB) sB[buf][4 * (tid % 4) + e][tid / 4] = rb[e];
+            else sB[buf][tid / 16][4 * (tid % 16) + e] = rb[e];
+        }
+    };
+
+    v4f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const int nk = (K + BKS - 1) / BKS;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < nk; t++) {
+        const int buf = t & 1;
+        if (t + 1 < nk) load((t + 1) * BKS);
+#pragma unroll
+        for (int ks = 0; ks < BKS / 4; ks++) {
+            const int kk = 4 * ks + (lane >> 4);
+            float a[2], b[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) a[j] = sA[buf][kk][32 * wm + 16 * j + (lane & 15)];
+#pragma unroll
+            for (int i = 0; i < 2; i++) b[i] = sB[buf][kk][32 * wn + 16 * i + (lane & 15)];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[i], a[j], acc[i][j], 0, 0, 0);
+        }
+        if (t + 1 < nk) store(buf ^ 1);
+        __syncthreads();
+    }
+    /* lane l holds C[m][n .. n + 3] with m = m0 + 32·wm + 16·j + l % 16, n = n0 + 32·wn + 16·i + 4·(l / 16) */
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int m = m0 + 32 * wm + 16 * j + (lane & 15), n = n0 + 32 * wn + 16 * i + 4 * (lane >> 4);
+            if (m >= M) continue;
+            float *cp = C + (size_t)m * g.ldc + n;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (n + e >= N) break;
+                const float c0 = g.beta == 0.0f ? 0.0f : (g.beta == 1.0f ? cp[e] : cp[e] * g.beta);
+                cp[e] = __builtin_fmaf(g.alpha, acc[i][j][e], c0);
+            }
+        }
 }
 
 /* ── small kernels ─────────────────────────────────────────────────────────────────────────────────────────── */

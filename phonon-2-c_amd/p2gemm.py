@@ -77,6 +77,8 @@ _HIP_SIG = {
     "p2h_q8b_gemm_q8a": (_i, [_i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _vp, _f, _vp, _i, _vp]),
     "p2h_q8b_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
+    "p2h_sgemm_batched": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, C.c_longlong, _vp, _i, C.c_longlong, _f, _vp, _i,
+                               C.c_longlong, _i, _vp]),
 }
 
 _hip = None
@@ -452,6 +454,27 @@ def sgemm(A, B, transA=False, transB=False, alpha=1.0, beta=0.0, C0=None):
     dA, dB, dC = to_device(A), to_device(B), to_device(C0)
     _ok(hip().p2h_sgemm(int(transA), int(transB), M, N, K, alpha, dA.ptr, A.shape[1], dB.ptr, B.shape[1], beta,
                         dC.ptr, C0.shape[1], None), "p2h_sgemm")
+    return dC.download(C0.shape, np.float32)
+
+
+def sgemm_batched_dev(transA, transB, M, N, K, alpha, dA, lda, sA, dB, ldb, sB, beta, dC, ldc, sC, batch,
+                      stream=None):
+    _ok(hip().p2h_sgemm_batched(int(transA), int(transB), M, N, K, alpha, dA, lda, sA, dB, ldb, sB, beta, dC, ldc,
+                                sC, batch, stream), "p2h_sgemm_batched")
+
+
+def sgemm_batched(A, B, transA=False, transB=False, alpha=1.0, beta=0.0, C0=None):
+    """p2h_sgemm_batched on host arrays A [b, ., .], B [b, ., .] (contiguous per entry)."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    b = A.shape[0]
+    M = A.shape[2] if transA else A.shape[1]
+    K = A.shape[1] if transA else A.shape[2]
+    N = B.shape[1] if transB else B.shape[2]
+    C0 = np.zeros((b, M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
+    dA, dB, dC = to_device(A), to_device(B), to_device(C0)
+    sgemm_batched_dev(transA, transB, M, N, K, alpha, dA.ptr, A.shape[2], A.shape[1] * A.shape[2], dB.ptr,
+                      B.shape[2], B.shape[1] * B.shape[2], beta, dC.ptr, N, M * N, b)
     return dC.download(C0.shape, np.float32)
 
 

@@ -232,6 +232,37 @@ def test_sgemm_fp32(tA, tB):
     assert np.allclose(got, ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("H,T,Dh", [(16, 375, 64), (4, 37, 64), (2, 129, 40)])
+def test_sgemm_batched_attention_shapes(H, T, Dh):
+    """The per-head products of relative-position attention (encoder.c:505-519): Q_u·K_t [T, T], Q_v·P_t [T, 2T−1]
+    and scores·V [T, Dh], every head in one launch, against float64."""
+    rng = np.random.default_rng(H * T)
+    L = 2 * T - 1
+    Qu = rng.standard_normal((H, T, Dh)).astype(np.float32)
+    Kt = rng.standard_normal((H, Dh, T)).astype(np.float32)
+    Pt = rng.standard_normal((H, Dh, L)).astype(np.float32)
+    S = rng.random((H, T, T)).astype(np.float32)
+    V = rng.standard_normal((H, T, Dh)).astype(np.float32)
+    for A, B in ((Qu, Kt), (Qu, Pt), (S, V)):
+        got = P.sgemm_batched(A, B)
+        _assert_exact(got.reshape(-1, got.shape[2]),
+                      np.matmul(A.astype(np.float64), B.astype(np.float64)).reshape(-1, got.shape[2]))
+
+
+@pytest.mark.parametrize("tA,tB", [(False, True), (True, False)])
+def test_sgemm_batched_transposed_beta(tA, tB):
+    rng = np.random.default_rng(7)
+    b, M, K, N = 3, 70, 33, 90
+    A = rng.standard_normal((b, K, M) if tA else (b, M, K)).astype(np.float32)
+    B = rng.standard_normal((b, N, K) if tB else (b, K, N)).astype(np.float32)
+    C0 = rng.standard_normal((b, M, N)).astype(np.float32)
+    got = P.sgemm_batched(A, B, tA, tB, alpha=-0.5, beta=1.0, C0=C0)
+    opA = np.swapaxes(A, 1, 2) if tA else A
+    opB = np.swapaxes(B, 1, 2) if tB else B
+    ref = -0.5 * np.matmul(opA.astype(np.float64), opB.astype(np.float64)) + C0
+    _assert_exact(got.reshape(-1, N), ref.reshape(-1, N))
+
+
 # ── several weights against the same quantised rows in one launch ─────────────────────────────────────────────────
 
 @pytest.mark.parametrize("mode", ["int8w", "int8"])
