@@ -33,6 +33,10 @@ enum {
 /* Row padding of quantised activations: Q rows hold K int8 values, zero-filled up to a multiple of this. */
 #define P2H_Q_KALIGN 128
 
+/* Longest row a producer (p2h_*_quant_rows below) makes: the reference's widest producer row, P2_FF_DIM
+ * (phonon2.h:76, the SiLU row buffer at tensor_ops.c:502). */
+#define P2H_PROD_KMAX 4096
+
 /* ── runtime ────────────────────────────────────────────────────────────────────────────────────────────────── */
 
 int         p2h_init(void);                 /* device 0 must be gfx950; idempotent, thread-safe */
@@ -109,6 +113,30 @@ int p2h_fv_pack_codes(const P2hWeight *w, signed char *d_codes, void *stream);
 int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int ldq, float *dScales, void *stream);
 int p2h_q_ld(int K);              /* the smallest valid ldq for K */
 size_t p2h_q_bytes(int M, int K); /* bytes of Q for M rows at ldq = p2h_q_ld(K) */
+
+/* Producers: the rows a quantised linear reads, made and quantised in one launch, into the same tiled Q and scales
+ * as p2h_quant_rows (same quantisation, same padding; ldq <= P2H_PROD_KMAX). Each computes in IEEE single precision
+ * with every operation rounded as written:
+ *   p2h_layer_norm_quant_rows     LayerNorm of each row of X [M][ldx] (eps 1e-5), then quantised
+ *                                 (p2_layer_norm_quant_rows, tensor_ops.c:329-350 with p2_layer_norm, :204-268):
+ *                                 the sums in the reference's AVX2 order (eight running lanes, then their
+ *                                 pairwise sum), inv_std = 1/sqrtf(var + 1e-5) correctly rounded,
+ *                                 y = fmaf((x − mean)·inv_std, gamma, beta). 1 <= D <= P2H_PROD_KMAX.
+ *   p2h_silu_quant_rows           x · (1/(1 + e^−x)) of each row of H [M][ldh], e^x as p2_exp_avx2
+ *                                 (tensor_ops.c:154-175), then quantised (p2_swish_quant_rows, tensor_ops.c:491-511).
+ *                                 K % 8 == 0 (the reference's eight-wide route; its scalar tail calls expf).
+ *   p2h_concat_heads_quant_rows   attention heads [H][T][Dh] as rows [T][H·Dh], quantised (concat_heads with a
+ *                                 QuantA, encoder.c:449-463).
+ *   p2h_channel_major_quant_rows  channel-major [D][T] as rows [T][D], quantised (channel_major_to_rows with a
+ *                                 QuantA, encoder.c:554-568).
+ * The reference's x86 build computes 1/sqrtf and 1/(1 + e) through approximate reciprocals refined by one Newton
+ * step, so its LayerNorm and SiLU values differ from these in the last bits and a quantised code, rarely, by one. */
+int p2h_layer_norm_quant_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta,
+                              signed char *dQ, int ldq, float *dScales, void *stream);
+int p2h_silu_quant_rows(int M, int K, const float *dH, int ldh, signed char *dQ, int ldq, float *dScales, void *stream);
+int p2h_concat_heads_quant_rows(int H, int T, int Dh, const float *dAttnH, signed char *dQ, int ldq, float *dScales,
+                                void *stream);
+int p2h_channel_major_quant_rows(int D, int T, const float *dDW, signed char *dQ, int ldq, float *dScales, void *stream);
 
 /* ── the five-value GEMM ─────────────────────────────────────────────────────────────────────────────────────── */
 

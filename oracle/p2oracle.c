@@ -154,6 +154,128 @@ void p2o_quant_rows(const float *A, int M, int K, int lda, int8_t *q, float *sca
     for (int m = 0; m < M; m++) quant_row(A + (size_t)m * lda, K, q + (size_t)m * K, scales + m);
 }
 
+/* ── producers: the rows a quantised linear reads, made and quantised in one pass (tensor_ops.c, encoder.c) ────── */
+
+/* The eight-lane horizontal sum of p2_hsum_avx2 (tensor_ops.c:182-190): v[i] + v[i+4], then pairs, then the two. */
+static float hsum8(const float v[8])
+{
+    float s4[4];
+    for (int i = 0; i < 4; i++) s4[i] = v[i] + v[i + 4];
+    const float s20 = s4[0] + s4[2], s21 = s4[1] + s4[3];
+    return s20 + s21;
+}
+
+/* p2_layer_norm, AVX2 route (tensor_ops.c:204-268): lane j of an 8-wide accumulator adds x[j], x[j+8], … in order,
+ * the lanes meet in hsum8, the tail (len % 8) adds one by one; mean = sum/len; the variance accumulates
+ * fmaf(d, d, ·) the same way; inv_std = 1/sqrtf(var + 1e-5); out = fmaf((x − mean)·inv_std, gamma, beta). Each
+ * operation rounds once, as written here (built with -ffp-contract=off); the scalar tails (len % 8) take fmaf where the
+ * source writes a product then a sum, as a contracting compiler builds them. The reference's -ffast-math x86 build
+ * computes 1/sqrtf as vrsqrtss plus a Newton step and may reassociate the tails, so it agrees with this restatement
+ * within 1e-6 of the row's rms, not bit for bit. */
+void p2o_layer_norm_row(const float *x, const float *gamma, const float *beta, float *out, int len)
+{
+    const int body = len / 8 * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < body; i += 8)
+        for (int j = 0; j < 8; j++) acc[j] = acc[j] + x[i + j];
+    float sum = hsum8(acc);
+    for (int i = body; i < len; i++) sum += x[i];
+    const float mean = sum / (float)len;
+    for (int j = 0; j < 8; j++) acc[j] = 0.0f;
+    for (int i = 0; i < body; i += 8)
+        for (int j = 0; j < 8; j++) {
+            const float d = x[i + j] - mean;
+            acc[j] = fmaf(d, d, acc[j]);
+        }
+    float var_sum = hsum8(acc);
+    for (int i = body; i < len; i++) {
+        const float d = x[i] - mean;
+        var_sum = fmaf(d, d, var_sum);
+    }
+    const float var = var_sum / (float)len;
+    const float inv_std = 1.0f / sqrtf(var + 1e-5f);
+    for (int i = 0; i < len; i++) out[i] = fmaf((x[i] - mean) * inv_std, gamma[i], beta[i]);
+}
+
+/* p2_exp_avx2 (tensor_ops.c:154-175): clamp to ±87, k = round-to-nearest-even(x·log2e), r = x − k·ln2 as one fmaf
+ * (the reference's -ffast-math build contracts the source's product and difference the same way), degree-5 Horner in
+ * fmaf, times 2^k built in the exponent. */
+static float exp_avx2_lane(float x)
+{
+    x = fminf(fmaxf(x, -87.0f), 87.0f);
+    const float kf = rintf(x * 1.44269504088896341f);
+    const float r = fmaf(-kf, 0.69314718055994529f, x);
+    float y = 1.0f / 120.0f;
+    y = fmaf(y, r, 1.0f / 24.0f);
+    y = fmaf(y, r, 1.0f / 6.0f);
+    y = fmaf(y, r, 0.5f);
+    y = fmaf(y, r, 1.0f);
+    y = fmaf(y, r, 1.0f);
+    union { uint32_t u; float f; } p;
+    p.u = (uint32_t)((int32_t)kf + 127) << 23;
+    return y * p.f;
+}
+
+/* swish_range, AVX2 route (tensor_ops.c:437-463): x · (1 / (1 + exp(−x))) in groups of eight, each operation rounded
+ * as written; a tail uses p2_sigmoid (phonon2.h:38-46), expf clamped at 87. The reference's x86 build fuses 1 + y·2^k
+ * into one fma and divides by vrcpps plus a Newton step, so its values agree with these within a few ulp. */
+void p2o_swish_row(float *x, int len)
+{
+    const int body = len / 8 * 8;
+    for (int i = 0; i < body; i++) {
+        const float e = exp_avx2_lane(0.0f - x[i]);
+        x[i] = x[i] * (1.0f / (1.0f + e));
+    }
+    for (int i = body; i < len; i++) x[i] *= 1.0f / (1.0f + expf(x[i] < -87.0f ? 87.0f : -x[i]));
+}
+
+/* LayerNorm then quantise each row (p2_layer_norm_quant_rows, tensor_ops.c:329-350) */
+void p2o_ln_quant_rows(const float *X, int M, int D, int ldx, const float *gamma, const float *beta, int8_t *q,
+                       float *scales)
+{
+    float *row = (float *)malloc((size_t)D * sizeof(float));
+    for (int m = 0; m < M; m++) {
+        p2o_layer_norm_row(X + (size_t)m * ldx, gamma, beta, row, D);
+        quant_row(row, D, q + (size_t)m * D, scales + m);
+    }
+    free(row);
+}
+
+/* SiLU then quantise each row (p2_swish_quant_rows, tensor_ops.c:491-511) */
+void p2o_silu_quant_rows(const float *H, int M, int K, int ldh, int8_t *q, float *scales)
+{
+    float *row = (float *)malloc((size_t)K * sizeof(float));
+    for (int m = 0; m < M; m++) {
+        memcpy(row, H + (size_t)m * ldh, (size_t)K * sizeof(float));
+        p2o_swish_row(row, K);
+        quant_row(row, K, q + (size_t)m * K, scales + m);
+    }
+    free(row);
+}
+
+/* Heads [H, T, Dh] → rows [T, H·Dh], then quantise (concat_heads, encoder.c:449-463) */
+void p2o_concat_heads_quant_rows(const float *attn_h, int H, int T, int Dh, int8_t *q, float *scales)
+{
+    const int D = H * Dh;
+    float *row = (float *)malloc((size_t)D * sizeof(float));
+    for (int t = 0; t < T; t++) {
+        for (int h = 0; h < H; h++) memcpy(row + h * Dh, attn_h + ((size_t)h * T + t) * Dh, (size_t)Dh * sizeof(float));
+        quant_row(row, D, q + (size_t)t * D, scales + t);
+    }
+    free(row);
+}
+
+/* Channel-major [D, T] → rows [T, D], then quantise (channel_major_to_rows, encoder.c:554-568) */
+void p2o_channel_major_quant_rows(const float *dw, int D, int T, int8_t *q, float *scales)
+{
+    float *row = (float *)malloc((size_t)D * sizeof(float));
+    for (int t = 0; t < T; t++) {
+        for (int d = 0; d < D; d++) row[d] = dw[(size_t)d * T + t];
+        quant_row(row, D, q + (size_t)t * D, scales + t);
+    }
+    free(row);
+}
+
 /* blas.c:1319-1326 */
 static inline int clo_of(float lo, float hi)
 {

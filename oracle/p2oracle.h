@@ -68,6 +68,16 @@ void p2o_sgemm_fvb(int mode, int M, int N, int K, float alpha, const float *A, i
 void p2o_sgemm_q8b(int mode, int M, int N, int K, float alpha, const float *A, int lda,
                    const int8_t *B, const float *scales, int ldb, float beta, float *C, int ldc);
 
+/* Producers (tensor_ops.c:204-268, 329-350, 437-463, 491-511; encoder.c:449-463, 554-568): LayerNorm and SiLU in the
+ * reference's AVX2 order, and the four row producers that quantise what they make (q [rows][len], scales [rows]). */
+void p2o_layer_norm_row(const float *x, const float *gamma, const float *beta, float *out, int len);
+void p2o_swish_row(float *x, int len);
+void p2o_ln_quant_rows(const float *X, int M, int D, int ldx, const float *gamma, const float *beta, int8_t *q,
+                       float *scales);
+void p2o_silu_quant_rows(const float *H, int M, int K, int ldh, int8_t *q, float *scales);
+void p2o_concat_heads_quant_rows(const float *attn_h, int H, int T, int Dh, int8_t *q, float *scales);
+void p2o_channel_major_quant_rows(const float *dw, int D, int T, int8_t *q, float *scales);
+
 /* The mode latch's decision for given P2_GEMM / P2_EXACT strings (NULL = unset), without the CPU-feature clause
  * (blas.c:1032-1047). */
 int p2o_mode_from_env(const char *p2_gemm, const char *p2_exact);

@@ -522,6 +522,90 @@ int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int 
     return P2H_OK;
 }
 
+/* ── producers ──────────────────────────────────────────────────────────────────────────────────────────────── */
+
+/* Checks shared by the four producers, then one produce_rows launch over the padded rows [0, roundup(M, 16)). */
+static int produce(const char *name, int kind, p2k::ProdArgs a, bool vec, hipStream_t s)
+{
+    if (a.M < 0 || a.K < 0 || (a.M > 0 && a.K == 0) || a.K > P2H_PROD_KMAX)
+        return fail(P2H_E_ARG, "%s: %d rows of %d columns (columns 1..%d)", name, a.M, a.K, P2H_PROD_KMAX);
+    if (a.M == 0) return P2H_OK;
+    if (!a.X || !a.Q || !a.scales) return fail(P2H_E_ARG, "%s: null pointer", name);
+    if (a.ldq < p2h_q_ld(a.K) || a.ldq % P2H_Q_KALIGN != 0 || a.ldq > P2H_PROD_KMAX || !aligned(a.Q, 16))
+        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d, <= %d and a multiple of %d, Q 16-byte aligned", name,
+                    a.ldq, p2h_q_ld(a.K), P2H_PROD_KMAX, P2H_Q_KALIGN);
+    a.Mp = (int)align_up((size_t)a.M, 16);
+    const dim3 grid((unsigned)((a.Mp + 3) / 4)), block(256);
+    auto launch = [&](auto kind_tag, auto nch_tag, auto vec_tag) {
+        hipLaunchKernelGGL((p2k::produce_rows<decltype(kind_tag)::value, decltype(nch_tag)::value,
+                                              decltype(vec_tag)::value>),
+                           grid, block, 0, s, a);
+    };
+    auto by_width = [&](auto kind_tag, auto vec_tag) {
+        switch ((a.ldq + 1023) / 1024) {   /* 16-column chunks per lane, the row kept in registers */
+        case 1: launch(kind_tag, std::integral_constant<int, 1>{}, vec_tag); break;
+        case 2: launch(kind_tag, std::integral_constant<int, 2>{}, vec_tag); break;
+        case 3: launch(kind_tag, std::integral_constant<int, 3>{}, vec_tag); break;
+        default: launch(kind_tag, std::integral_constant<int, 4>{}, vec_tag); break;
+        }
+    };
+    auto by_vec = [&](auto kind_tag) {
+        if (vec) by_width(kind_tag, std::true_type{});
+        else by_width(kind_tag, std::false_type{});
+    };
+    switch (kind) {
+    case p2k::PROD_SILU: by_vec(std::integral_constant<int, p2k::PROD_SILU>{}); break;
+    case p2k::PROD_LN: by_vec(std::integral_constant<int, p2k::PROD_LN>{}); break;
+    case p2k::PROD_HEADS: by_vec(std::integral_constant<int, p2k::PROD_HEADS>{}); break;
+    default: by_width(std::integral_constant<int, p2k::PROD_CMAJOR>{}, std::false_type{}); break;
+    }
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_layer_norm_quant_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta,
+                              signed char *dQ, int ldq, float *dScales, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (M > 0 && (ldx < D || !dGamma || !dBeta))
+        return fail(P2H_E_ARG, "p2h_layer_norm_quant_rows: ldx = %d < D = %d or null gamma / beta", ldx, D);
+    p2k::ProdArgs a{};
+    a.M = M; a.K = D; a.X = dX; a.ldx = ldx; a.gamma = dGamma; a.beta = dBeta;
+    a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
+    return produce("p2h_layer_norm_quant_rows", p2k::PROD_LN, a, D % 4 == 0 && ldx % 4 == 0 && aligned(dX, 16),
+                   stream_of(stream));
+}
+
+int p2h_silu_quant_rows(int M, int K, const float *dH, int ldh, signed char *dQ, int ldq, float *dScales, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (K % 8 != 0) return fail(P2H_E_ARG, "p2h_silu_quant_rows: K = %d must be a multiple of 8", K);
+    if (M > 0 && ldh < K) return fail(P2H_E_ARG, "p2h_silu_quant_rows: ldh = %d < K = %d", ldh, K);
+    p2k::ProdArgs a{};
+    a.M = M; a.K = K; a.X = dH; a.ldx = ldh; a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
+    return produce("p2h_silu_quant_rows", p2k::PROD_SILU, a, ldh % 4 == 0 && aligned(dH, 16), stream_of(stream));
+}
+
+int p2h_concat_heads_quant_rows(int H, int T, int Dh, const float *dAttnH, signed char *dQ, int ldq, float *dScales,
+                                void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (H < 0 || Dh < 0 || (long long)H * Dh > P2H_PROD_KMAX)
+        return fail(P2H_E_ARG, "p2h_concat_heads_quant_rows: H = %d, Dh = %d (H·Dh <= %d)", H, Dh, P2H_PROD_KMAX);
+    p2k::ProdArgs a{};
+    a.M = T; a.K = H * Dh; a.X = dAttnH; a.T = T; a.Dh = Dh; a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
+    return produce("p2h_concat_heads_quant_rows", p2k::PROD_HEADS, a, Dh % 16 == 0 && aligned(dAttnH, 16),
+                   stream_of(stream));
+}
+
+int p2h_channel_major_quant_rows(int D, int T, const float *dDW, signed char *dQ, int ldq, float *dScales, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    p2k::ProdArgs a{};
+    a.M = T; a.K = D; a.X = dDW; a.T = T; a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
+    return produce("p2h_channel_major_quant_rows", p2k::PROD_CMAJOR, a, false, stream_of(stream));
+}
+
 /* ── GEMMs ──────────────────────────────────────────────────────────────────────────────────────────────────── */
 
 int p2h_scale_c(int M, int N, float beta, float *dC, int ldc, void *stream)

@@ -184,6 +184,153 @@ __global__ __launch_bounds__(256) void quant_rows(int M, int Mp, int K, const fl
     if (lane == 0) scales[m] = scale;
 }
 
+/* ── producers: make a quantised linear's input rows and quantise them in one pass ────────────────────────────── */
+
+enum { PROD_SILU = 1, PROD_HEADS = 2, PROD_CMAJOR = 3, PROD_LN = 4 };
+
+struct ProdArgs {
+    int M, Mp, K;
+    const float *X; int ldx;                  /* SILU, LN: rows [M][ldx]; HEADS: [H][T][Dh]; CMAJOR: [K][T] */
+    int T, Dh;
+    const float *gamma, *beta;                /* LN */
+    int8_t *Q; int ldq; float *scales;
+};
+
+/* e^x as the reference's AVX2 exp (tensor_ops.c:154-175) in IEEE operations: clamp to ±87, k = rint(x·log2e),
+ * r = fmaf(−k, ln2, x), degree-5 Horner in fmaf, times 2^k assembled in the exponent field. */
+__device__ __forceinline__ float exp_p2(float x)
+{
+    x = fminf(fmaxf(x, -87.0f), 87.0f);
+    const float kf = __builtin_rintf(__fmul_rn(x, 1.44269504088896341f));
+    const float r = __builtin_fmaf(-kf, 0.69314718055994529f, x);
+    float y = 1.0f / 120.0f;
+    y = __builtin_fmaf(y, r, 1.0f / 24.0f);
+    y = __builtin_fmaf(y, r, 1.0f / 6.0f);
+    y = __builtin_fmaf(y, r, 0.5f);
+    y = __builtin_fmaf(y, r, 1.0f);
+    y = __builtin_fmaf(y, r, 1.0f);
+    return __fmul_rn(y, __uint_as_float((uint32_t)((int)kf + 127) << 23));
+}
+
+/* x · sigmoid(x) = x · (1 / (1 + e^{−x})) (swish_range, tensor_ops.c:437-463), no operation contracted */
+__device__ __forceinline__ float silu_p2(float x)
+{
+    return __fmul_rn(x, __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_p2(0.0f - x))));
+}
+
+/* One wave per row of the padded row range, the quantised row into the tiled layout as quant_rows does; the row is
+ * made on the way in:
+ *   PROD_SILU    SiLU of row m of X (p2_swish_quant_rows, tensor_ops.c:491-511; K % 8 == 0)
+ *   PROD_HEADS   row t of the head concatenation: element k = h·Dh + d is X[h][t][d] (encoder.c:449-463)
+ *   PROD_CMAJOR  row t of the transpose of the channel-major X [K][T] (encoder.c:554-568)
+ *   PROD_LN      LayerNorm of row m (p2_layer_norm_quant_rows, tensor_ops.c:204-268, 329-350): eight running sums,
+ *                lane j adding elements j, j + 8, … in order, meet as p2_hsum_avx2 does (v[i] + v[i+4], then pairs);
+ *                the same for fmaf(d, d, ·) with d = x − mean; inv_std = 1/sqrtf(var + 1e-5), square root and
+ *                quotient correctly rounded (__builtin_sqrtf; the v_sqrt_f32 behind __fsqrt_rn is not);
+ *                y = fmaf((x − mean)·inv_std, gamma, beta). The row is staged in LDS for the eight sums.
+ * NCH chunks of 16 columns per lane (ldq <= 1024·NCH). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
+ * ldx % 4 == 0; HEADS with Dh % 16 == 0; X 16-byte aligned. */
+template <int KIND, int NCH, bool VEC>
+__global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
+{
+    __shared__ float stage[KIND == PROD_LN ? 4 * 1024 * NCH : 1];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int m = blockIdx.x * 4 + w;
+    if (m >= a.Mp) return;
+    const int K = a.K, kst = a.ldq / 64, k16 = K / 16 * 16;
+    if (m >= a.M) {
+        for (int k0 = 16 * lane; k0 < a.ldq; k0 += 1024)
+            *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
+        return;
+    }
+    float x[NCH][16];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int k0 = 16 * (lane + 64 * c);
+        if ((KIND == PROD_SILU || KIND == PROD_LN) && VEC) {
+            load16<true>(a.X + (size_t)m * a.ldx, k0, K, x[c]);
+        } else if (KIND == PROD_SILU || KIND == PROD_LN) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) x[c][e] = k0 + e < K ? a.X[(size_t)m * a.ldx + k0 + e] : 0.0f;
+        } else if (KIND == PROD_HEADS && VEC) {   /* Dh % 16 == 0: the chunk lies in one head */
+            const bool ok = k0 < K;
+            const int h = ok ? k0 / a.Dh : 0;
+            load16<true>(a.X + ((size_t)h * a.T + m) * a.Dh, ok ? k0 - h * a.Dh : 0, ok ? a.Dh : 0, x[c]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int k = k0 + e;
+                float v = 0.0f;
+                if (k < K) v = KIND == PROD_HEADS ? a.X[((size_t)(k / a.Dh) * a.T + m) * a.Dh + k % a.Dh]
+                                                  : a.X[(size_t)k * a.T + m];
+                x[c][e] = v;
+            }
+        }
+        if (KIND == PROD_SILU) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) x[c][e] = silu_p2(x[c][e]);
+        }
+    }
+    if (KIND == PROD_LN) {
+        float *row = stage + w * 1024 * NCH;
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                if (16 * (lane + 64 * c) + e < K) row[16 * (lane + 64 * c) + e] = x[c][e];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const int body = K / 8 * 8;
+        float part = 0.0f;
+        if (lane < 8)
+            for (int k = lane; k < body; k += 8) part = __fadd_rn(part, row[k]);
+        float v8[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j);
+        float sum = __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
+                              __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+        for (int k = body; k < K; k++) sum = __fadd_rn(sum, row[k]);
+        const float mean = __fdiv_rn(sum, (float)K);
+        part = 0.0f;
+        if (lane < 8)
+            for (int k = lane; k < body; k += 8) {
+                const float d = __fsub_rn(row[k], mean);
+                part = __builtin_fmaf(d, d, part);
+            }
+#pragma unroll
+        for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j);
+        float var_sum = __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
+                                  __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+        for (int k = body; k < K; k++) {
+            const float d = __fsub_rn(row[k], mean);
+            var_sum = __builtin_fmaf(d, d, var_sum);
+        }
+        const float inv_std = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(var_sum, (float)K), 1e-5f)));
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int k = min(16 * (lane + 64 * c) + e, K - 1);
+                const float y = __builtin_fmaf(__fmul_rn(__fsub_rn(x[c][e], mean), inv_std), a.gamma[k], a.beta[k]);
+                x[c][e] = (16 * (lane + 64 * c) + e < K) ? y : 0.0f;
+            }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[c][e]));
+    amax = wave_max_dpp(amax);
+    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / scale;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int k0 = 16 * (lane + 64 * c);
+        if (k0 < a.ldq) *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = quant16(x[c], k0, K, k16, scale, inv);
+    }
+    if (lane == 0) a.scales[m] = scale;
+}
+
 /* ── the int8 GEMM ─────────────────────────────────────────────────────────────────────────────────────────── */
 
 struct GemmArgs {

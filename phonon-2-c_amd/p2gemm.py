@@ -65,6 +65,10 @@ _HIP_SIG = {
     "p2h_fv_pack_codes": (_i, [_vp, _vp, _vp]),
     "p2h_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_q_ld": (_i, [_i]),
+    "p2h_layer_norm_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    "p2h_silu_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
+    "p2h_concat_heads_quant_rows": (_i, [_i, _i, _i, _vp, _vp, _i, _vp, _vp]),
+    "p2h_channel_major_quant_rows": (_i, [_i, _i, _vp, _vp, _i, _vp, _vp]),
     "p2h_q_bytes": (C.c_size_t, [_i, _i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_gemm_q8a_grouped": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _f, _vp, _i, _vp]),
@@ -338,6 +342,23 @@ def quant_rows_dev(M, K, dA, lda, dQ, ldq, dS, stream=None):
     _ok(hip().p2h_quant_rows(M, K, dA, lda, dQ, ldq, dS, stream), "p2h_quant_rows")
 
 
+def layer_norm_quant_rows_dev(M, D, dX, ldx, dGamma, dBeta, dQ, ldq, dS, stream=None):
+    _ok(hip().p2h_layer_norm_quant_rows(M, D, dX, ldx, dGamma, dBeta, dQ, ldq, dS, stream),
+        "p2h_layer_norm_quant_rows")
+
+
+def silu_quant_rows_dev(M, K, dH, ldh, dQ, ldq, dS, stream=None):
+    _ok(hip().p2h_silu_quant_rows(M, K, dH, ldh, dQ, ldq, dS, stream), "p2h_silu_quant_rows")
+
+
+def concat_heads_quant_rows_dev(H, T, Dh, dAttnH, dQ, ldq, dS, stream=None):
+    _ok(hip().p2h_concat_heads_quant_rows(H, T, Dh, dAttnH, dQ, ldq, dS, stream), "p2h_concat_heads_quant_rows")
+
+
+def channel_major_quant_rows_dev(D, T, dDW, dQ, ldq, dS, stream=None):
+    _ok(hip().p2h_channel_major_quant_rows(D, T, dDW, dQ, ldq, dS, stream), "p2h_channel_major_quant_rows")
+
+
 def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=None, ws_bytes=0, stream=None):
     _ok(hip().p2h_fvb_gemm_q8a(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, ws,
                                ws_bytes, stream), "p2h_fvb_gemm_q8a")
@@ -375,6 +396,51 @@ def quant_rows(A, K=None):
     q = q_untile(dQ.download((q_bytes(M, K),), np.int8), M, ldq) if M > 0 else np.zeros((0, ldq), np.int8)
     s = dS.download((M,), np.float32)
     return q, s
+
+
+def _produced(M, K, run):
+    """Run a producer into fresh device buffers (every byte preset, so pads must be written) and download."""
+    ldq = q_ld(K)
+    nbytes = max(q_bytes(M, K), 16)
+    dQ = DeviceBuffer(nbytes)
+    dQ.upload(np.full(nbytes, 0x5A, np.uint8))
+    dS = DeviceBuffer(max(M, 1) * 4)
+    run(dQ.ptr, ldq, dS.ptr)
+    q = q_untile(dQ.download((q_bytes(M, K),), np.int8), M, ldq) if M > 0 else np.zeros((0, ldq), np.int8)
+    return q, dS.download((M,), np.float32)
+
+
+def layer_norm_quant_rows(X, gamma, beta, D=None):
+    """p2h_layer_norm_quant_rows on host arrays X [M, ldx] (first D columns): q untiled [roundup(M, 16), ldq]."""
+    X = np.ascontiguousarray(X, np.float32)
+    M, ldx = X.shape
+    D = ldx if D is None else D
+    dX, dG, dB = to_device(X), to_device(np.ascontiguousarray(gamma, np.float32)), \
+        to_device(np.ascontiguousarray(beta, np.float32))
+    return _produced(M, D, lambda dQ, ldq, dS: layer_norm_quant_rows_dev(M, D, dX.ptr, ldx, dG.ptr, dB.ptr, dQ, ldq,
+                                                                         dS))
+
+
+def silu_quant_rows(H, K=None):
+    H = np.ascontiguousarray(H, np.float32)
+    M, ldh = H.shape
+    K = ldh if K is None else K
+    dH = to_device(H)
+    return _produced(M, K, lambda dQ, ldq, dS: silu_quant_rows_dev(M, K, dH.ptr, ldh, dQ, ldq, dS))
+
+
+def concat_heads_quant_rows(attn_h):
+    attn_h = np.ascontiguousarray(attn_h, np.float32)
+    H, T, Dh = attn_h.shape
+    dA = to_device(attn_h)
+    return _produced(T, H * Dh, lambda dQ, ldq, dS: concat_heads_quant_rows_dev(H, T, Dh, dA.ptr, dQ, ldq, dS))
+
+
+def channel_major_quant_rows(dw):
+    dw = np.ascontiguousarray(dw, np.float32)
+    D, T = dw.shape
+    dW = to_device(dw)
+    return _produced(T, D, lambda dQ, ldq, dS: channel_major_quant_rows_dev(D, T, dW.ptr, dQ, ldq, dS))
 
 
 def fvb_gemm(mode, A, w, alpha=1.0, beta=0.0, C0=None, K=None, ws=None):

@@ -46,6 +46,12 @@ def lib():
             "p2o_sgemm_fvb": [_i, _i, _i, _i, _f, _f32p, _i, _u8p, _u8p, _f32p, _f32p, _f, _f32p, _i],
             "p2o_sgemm_q8b": [_i, _i, _i, _i, _f, _f32p, _i, _i8p, _f32p, _i, _f, _f32p, _i],
             "p2o_mode_from_env": [C.c_char_p, C.c_char_p],
+            "p2o_layer_norm_row": [_f32p, _f32p, _f32p, _f32p, _i],
+            "p2o_swish_row": [_f32p, _i],
+            "p2o_ln_quant_rows": [_f32p, _i, _i, _i, _f32p, _f32p, _i8p, _f32p],
+            "p2o_silu_quant_rows": [_f32p, _i, _i, _i, _i8p, _f32p],
+            "p2o_concat_heads_quant_rows": [_f32p, _i, _i, _i, _i8p, _f32p],
+            "p2o_channel_major_quant_rows": [_f32p, _i, _i, _i8p, _f32p],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -184,11 +190,70 @@ def ref_available():
     return os.path.exists(REF_SO)
 
 
+def layer_norm_rows(X, gamma, beta):
+    X = _c(X, np.float32)
+    out = np.empty_like(X)
+    g, b = _c(gamma, np.float32), _c(beta, np.float32)
+    for m in range(X.shape[0]):
+        row = np.empty(X.shape[1], np.float32)
+        lib().p2o_layer_norm_row(_c(X[m], np.float32), g, b, row, X.shape[1])
+        out[m] = row
+    return out
+
+
+def swish_rows(X):
+    out = _c(X, np.float32).copy()
+    for m in range(out.shape[0]):
+        row = out[m].copy()
+        lib().p2o_swish_row(row, row.size)
+        out[m] = row
+    return out
+
+
+def ln_quant_rows(X, gamma, beta, D=None):
+    X = _c(X, np.float32)
+    M, ldx = X.shape
+    D = ldx if D is None else D
+    q, sc = np.zeros((M, D), np.int8), np.zeros(M, np.float32)
+    lib().p2o_ln_quant_rows(X, M, D, ldx, _c(gamma, np.float32), _c(beta, np.float32), q, sc)
+    return q, sc
+
+
+def silu_quant_rows(H, K=None):
+    H = _c(H, np.float32)
+    M, ldh = H.shape
+    K = ldh if K is None else K
+    q, sc = np.zeros((M, K), np.int8), np.zeros(M, np.float32)
+    lib().p2o_silu_quant_rows(H, M, K, ldh, q, sc)
+    return q, sc
+
+
+def concat_heads_quant_rows(attn_h):
+    attn_h = _c(attn_h, np.float32)
+    H, T, Dh = attn_h.shape
+    q, sc = np.zeros((T, H * Dh), np.int8), np.zeros(T, np.float32)
+    lib().p2o_concat_heads_quant_rows(attn_h, H, T, Dh, q, sc)
+    return q, sc
+
+
+def channel_major_quant_rows(dw):
+    dw = _c(dw, np.float32)
+    D, T = dw.shape
+    q, sc = np.zeros((T, D), np.int8), np.zeros(T, np.float32)
+    lib().p2o_channel_major_quant_rows(dw, D, T, q, sc)
+    return q, sc
+
+
 def ref():
-    """The reference's p2_sgemm_fvb / p2_sgemm_q8b (x86: the exact fp32 AVX2 route, blas.c:1043-1045)."""
+    """The reference's p2_sgemm_fvb / p2_sgemm_q8b (x86: the exact fp32 AVX2 route, blas.c:1043-1045), and its
+    p2_layer_norm / p2_swish (tensor_ops.c, AVX2 routes)."""
     global _ref
     if _ref is None:
         L = C.CDLL(REF_SO)
+        L.p2_layer_norm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _i]
+        L.p2_layer_norm.restype = None
+        L.p2_swish.argtypes = [C.c_void_p, _i]
+        L.p2_swish.restype = None
         L.p2_sgemm_fvb.argtypes = [_i, _i, _i, _f, C.c_void_p, _i, C.POINTER(FiveValueB), _f, C.c_void_p, _i]
         L.p2_sgemm_fvb.restype = None
         L.p2_sgemm_q8b.argtypes = [_i, _i, _i, _f, C.c_void_p, _i, C.c_void_p, C.c_void_p, _i, _f, C.c_void_p, _i]
@@ -218,4 +283,26 @@ def ref_sgemm_q8b(A, B, scales, N, alpha, beta, C0, K=None):
     sc = _c(scales, np.float32)
     ref().p2_sgemm_q8b(M, N, K, alpha, A.ctypes.data, lda, B.ctypes.data, sc.ctypes.data, B.shape[1],
                        beta, out.ctypes.data, out.shape[1])
+    return out
+
+
+def ref_layer_norm_rows(X, gamma, beta):
+    X = _c(X, np.float32)
+    out = np.empty_like(X)
+    g, b = _c(gamma, np.float32), _c(beta, np.float32)
+    for m in range(X.shape[0]):
+        row = _c(X[m], np.float32)
+        o = np.empty(X.shape[1], np.float32)
+        ref().p2_layer_norm(row.ctypes.data, g.ctypes.data, b.ctypes.data, o.ctypes.data, X.shape[1])
+        out[m] = o
+    return out
+
+
+def ref_swish_rows(X):
+    """p2_swish row by row (rows below its 32768-element threading threshold run swish_range directly)."""
+    out = _c(X, np.float32).copy()
+    for m in range(out.shape[0]):
+        row = out[m].copy()
+        ref().p2_swish(row.ctypes.data, row.size)
+        out[m] = row
     return out
