@@ -106,3 +106,70 @@ def test_producer_feeds_the_gemm():
     q, s = O.silu_quant_rows(Hh)
     ref = O.gemm_i8_run("int8w", q, s, signs, flags, lo, hi, N)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _fvw(K, N, tid):
+    signs, flags, lo, hi = P.gen_fv_weight(SEED, tid, K, N)
+    return (signs, flags, lo, hi), P.FvWeight(signs, flags, lo, hi, K, N)
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+def test_feed_forward_module_on_device(mode):
+    """encoder.c:340-348 with every step on the device: x += ½ · W2 · SiLU(W1 · LN(x)), the LayerNorm and the SiLU
+    quantised as produced and the residual added in the second GEMM's epilogue (alpha 0.5, beta 1). Bit-exact
+    against the oracle's chain of the same steps."""
+    T, D, FF = 375, 1024, 4096
+    print(f"feed_forward {mode} T={T} D={D} FF={FF}", flush=True)
+    rng = np.random.default_rng(SEED + 17)
+    x = _rows(rng, T, D, 1.0)
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    b = rng.uniform(-0.2, 0.2, D).astype(np.float32)
+    (s1, f1, l1, h1), w1 = _fvw(D, FF, 21)
+    (s2, f2, l2, h2), w2 = _fvw(FF, D, 22)
+
+    dx, dg, db = P.to_device(x), P.to_device(g), P.to_device(b)
+    ldq1, ldq2 = P.q_ld(D), P.q_ld(FF)
+    dQ1, dS1 = P.DeviceBuffer(P.q_bytes(T, D)), P.DeviceBuffer(T * 4)
+    dH = P.DeviceBuffer(T * FF * 4)
+    dQ2, dS2 = P.DeviceBuffer(P.q_bytes(T, FF)), P.DeviceBuffer(T * 4)
+    P.layer_norm_quant_rows_dev(T, D, dx.ptr, D, dg.ptr, db.ptr, dQ1.ptr, ldq1, dS1.ptr)
+    P.fvb_gemm_q8a_dev(mode, T, FF, D, 1.0, dQ1.ptr, ldq1, dS1.ptr, w1, 0.0, dH.ptr, FF)
+    P.silu_quant_rows_dev(T, FF, dH.ptr, FF, dQ2.ptr, ldq2, dS2.ptr)
+    P.fvb_gemm_q8a_dev(mode, T, D, FF, 0.5, dQ2.ptr, ldq2, dS2.ptr, w2, 1.0, dx.ptr, D)
+    got = dx.download((T, D), np.float32)
+
+    q1, sc1 = O.ln_quant_rows(x, g, b)
+    h = O.gemm_i8_run(mode, q1, sc1, s1, f1, l1, h1, FF)
+    q2, sc2 = O.silu_quant_rows(h)
+    ref = O.gemm_i8_run(mode, q2, sc2, s2, f2, l2, h2, D, alpha=0.5, C0=x, beta_zero=False)
+    neq = got.view(np.uint32) != ref.view(np.uint32)
+    assert not neq.any(), f"{int(neq.sum())} of {neq.size} differ"
+
+
+def test_attention_and_conv_outputs_on_device():
+    """The two other residual linears: x += concat(heads) · W_o (encoder.c:525-527) and x += rows(dw) · W_pw2
+    (encoder.c:600-604), each producer feeding the GEMM with alpha 1, beta 1."""
+    T, D, H, Dh = 375, 1024, 8, 128
+    print(f"attention/conv outputs T={T} D={D}", flush=True)
+    rng = np.random.default_rng(SEED + 23)
+    x = _rows(rng, T, D, 1.0)
+    attn_h = rng.standard_normal((H, T, Dh)).astype(np.float32)
+    dw = rng.standard_normal((D, T)).astype(np.float32)
+    (so, fo, lo_, ho), wo = _fvw(D, D, 31)
+    (sp, fp, lp, hp), wp = _fvw(D, D, 32)
+
+    dx, dA, dW = P.to_device(x), P.to_device(attn_h), P.to_device(dw)
+    ldq = P.q_ld(D)
+    dQ, dS = P.DeviceBuffer(P.q_bytes(T, D)), P.DeviceBuffer(T * 4)
+    P.concat_heads_quant_rows_dev(H, T, Dh, dA.ptr, dQ.ptr, ldq, dS.ptr)
+    P.fvb_gemm_q8a_dev("int8w", T, D, D, 1.0, dQ.ptr, ldq, dS.ptr, wo, 1.0, dx.ptr, D)
+    P.channel_major_quant_rows_dev(D, T, dW.ptr, dQ.ptr, ldq, dS.ptr)
+    P.fvb_gemm_q8a_dev("int8w", T, D, D, 1.0, dQ.ptr, ldq, dS.ptr, wp, 1.0, dx.ptr, D)
+    got = dx.download((T, D), np.float32)
+
+    q, sc = O.concat_heads_quant_rows(attn_h)
+    ref = O.gemm_i8_run("int8w", q, sc, so, fo, lo_, ho, D, alpha=1.0, C0=x, beta_zero=False)
+    q, sc = O.channel_major_quant_rows(dw)
+    ref = O.gemm_i8_run("int8w", q, sc, sp, fp, lp, hp, D, alpha=1.0, C0=ref, beta_zero=False)
+    neq = got.view(np.uint32) != ref.view(np.uint32)
+    assert not neq.any(), f"{int(neq.sum())} of {neq.size} differ"
