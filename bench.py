@@ -345,6 +345,8 @@ def main():
         extra["sweep_ms_per_30s_window"] = (results["sweep"][1]["ms_per_step"] if "sweep" in results else None)
         extra["exact375"] = exact_config(stream)
         extra["attention375"] = attention_config(stream)
+        extra["producers"] = producer_config(stream)
+        extra["ffn_module375"] = ffn_module_config(stream)
 
     # dominant kernel of the headline workload: the GEMM with the longest duration
     gt = r["gemm_kernels_ms"]
@@ -421,7 +423,74 @@ def exact_config(stream):
     return out
 
 
-def attention_config(stream, H=16, T=375, Dh=64):
+def producer_config(stream, reps=200):
+    """The four row producers (LayerNorm, SiLU, head concatenation, channel-major transpose, each quantised as
+    produced) at the encoder's shapes for T = 375 and T = 6000, each timed on its own by time_launches, against the
+    HBM roofline: algorithmic bytes = fp32 rows read + int8 rows and fp32 scales written (+ gamma, beta)."""
+    rng = np.random.default_rng(SEED)
+    out = {}
+    for T in (375, 6000):
+        D, FF, H, Dh = 1024, 4096, 8, 128
+        x = P.to_device(rng.standard_normal((T, D)).astype(np.float32))
+        h = P.to_device(rng.standard_normal((T, FF)).astype(np.float32))
+        heads = P.to_device(rng.standard_normal((H, T, Dh)).astype(np.float32))
+        cm = P.to_device(rng.standard_normal((D, T)).astype(np.float32))
+        g = P.to_device(rng.uniform(0.5, 1.5, D).astype(np.float32))
+        b = P.to_device(rng.uniform(-0.2, 0.2, D).astype(np.float32))
+        q = P.DeviceBuffer(P.q_bytes(T, FF))
+        s = P.DeviceBuffer(4 * T)
+        ldD, ldF = P.q_ld(D), P.q_ld(FF)
+        cases = (
+            ("layer_norm", D, 8 * D,
+             lambda: P.layer_norm_quant_rows_dev(T, D, x.ptr, D, g.ptr, b.ptr, q.ptr, ldD, s.ptr, stream.ptr)),
+            ("silu", FF, 0, lambda: P.silu_quant_rows_dev(T, FF, h.ptr, FF, q.ptr, ldF, s.ptr, stream.ptr)),
+            ("concat_heads", D, 0,
+             lambda: P.concat_heads_quant_rows_dev(H, T, Dh, heads.ptr, q.ptr, ldD, s.ptr, stream.ptr)),
+            ("channel_major", D, 0, lambda: P.channel_major_quant_rows_dev(D, T, cm.ptr, q.ptr, ldD, s.ptr, stream.ptr)),
+            ("plain_quant", D, 0, lambda: P.quant_rows_dev(T, D, x.ptr, D, q.ptr, ldD, s.ptr, stream.ptr)),
+        )
+        for name, K, extra_bytes, fn in cases:
+            ms = time_launches(fn, stream, reps)
+            alg = quant_bytes(T, K) + extra_bytes
+            out[f"{name}_T{T}"] = {"us": round(ms * 1e3, 2), "gbs": round(alg / (ms * 1e-3) / 1e9, 1),
+                                   "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                   "algorithmic_bytes": int(alg)}
+    stream.sync()
+    return out
+
+
+def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200):
+    """One conformer feed-forward module as the encoder runs it in the int8 modes (encoder.c:340-348), every step on
+    the device and replayed from one graph: LayerNorm quantised as produced, up-projection 1024 -> 4096, SiLU
+    quantised as produced, down-projection 4096 -> 1024 with the residual in its epilogue (alpha 0.5, beta 1)."""
+    D, FF = 1024, 4096
+    rng = np.random.default_rng(SEED + 5)
+    l1, l2 = Linear(41, D, FF, M), Linear(42, FF, D, M)
+    x = P.to_device(P.gen_activations(SEED, 10_000 + D + M, M, D))
+    g = P.to_device(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    b = P.to_device(rng.uniform(-0.2, 0.2, D).astype(np.float32))
+    ws = Scratch(M, FF, max(P.q8a_workspace_bytes("int8w", M, FF, D), P.q8a_workspace_bytes("int8w", M, D, FF)))
+    ldD, ldF = P.q_ld(D), P.q_ld(FF)
+    steps_fns = (
+        lambda: P.layer_norm_quant_rows_dev(M, D, x.ptr, D, g.ptr, b.ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr),
+        lambda: P.fvb_gemm_q8a_dev("int8w", M, FF, D, 1.0, ws.q.ptr, ldD, ws.s.ptr, l1.w, 0.0, l1.out.ptr, FF,
+                                   ws.ws.ptr, ws.ws.nbytes, stream.ptr),
+        lambda: P.silu_quant_rows_dev(M, FF, l1.out.ptr, FF, ws.q.ptr, ldF, ws.s.ptr, stream.ptr),
+        lambda: P.fvb_gemm_q8a_dev("int8w", M, D, FF, 0.5, ws.q.ptr, ldF, ws.s.ptr, l2.w, 1.0, x.ptr, D,
+                                   ws.ws.ptr, ws.ws.nbytes, stream.ptr),
+    )
+    with P.Graph(stream) as graph:
+        for fn in steps_fns:
+            fn()
+    ms, _ = time_graph(graph, stream, steps, warmup)
+    kt = [round(time_launches(fn, stream, reps), 5) for fn in steps_fns] if reps > 0 else None
+    ops = gemm_ops(M, FF, D) + gemm_ops(M, D, FF)
+    return {"ms_per_step": round(ms, 6), "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+            "kernels_ms": dict(zip(("layer_norm_quant", "gemm_up", "silu_quant", "gemm_down_residual"), kt))
+            if kt else None}
+
+
+def attention_config(stream, H=8, T=375, Dh=128):
     """The fp32 per-head products of one block's relative-position attention at T = 375 (encoder.c:505-519), every
     head in one p2h_sgemm_batched launch each: Q_u·K_t [T, T], Q_v·P_t [T, 2T−1], scores·V [T, Dh]."""
     rng = np.random.default_rng(SEED)

@@ -535,6 +535,11 @@ static int produce(const char *name, int kind, p2k::ProdArgs a, bool vec, hipStr
         return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d, <= %d and a multiple of %d, Q 16-byte aligned", name,
                     a.ldq, p2h_q_ld(a.K), P2H_PROD_KMAX, P2H_Q_KALIGN);
     a.Mp = (int)align_up((size_t)a.M, 16);
+    if (kind == p2k::PROD_CMAJOR && a.K <= 1024 && a.ldq <= 1024) {   /* 16 rows per workgroup through LDS */
+        hipLaunchKernelGGL(p2k::cmajor_tile, dim3((unsigned)(a.Mp / 16)), dim3(1024), 0, s, a);
+        HIPCHK(hipGetLastError());
+        return P2H_OK;
+    }
     const dim3 grid((unsigned)((a.Mp + 3) / 4)), block(256);
     auto launch = [&](auto kind_tag, auto nch_tag, auto vec_tag) {
         hipLaunchKernelGGL((p2k::produce_rows<decltype(kind_tag)::value, decltype(nch_tag)::value,
@@ -572,7 +577,8 @@ int p2h_layer_norm_quant_rows(int M, int D, const float *dX, int ldx, const floa
     p2k::ProdArgs a{};
     a.M = M; a.K = D; a.X = dX; a.ldx = ldx; a.gamma = dGamma; a.beta = dBeta;
     a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
-    return produce("p2h_layer_norm_quant_rows", p2k::PROD_LN, a, D % 4 == 0 && ldx % 4 == 0 && aligned(dX, 16),
+    return produce("p2h_layer_norm_quant_rows", p2k::PROD_LN, a,
+                   D % 4 == 0 && ldx % 4 == 0 && aligned(dX, 16) && aligned(dGamma, 16) && aligned(dBeta, 16),
                    stream_of(stream));
 }
 

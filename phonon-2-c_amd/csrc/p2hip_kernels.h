@@ -229,11 +229,11 @@ __device__ __forceinline__ float silu_p2(float x)
  *                quotient correctly rounded (__builtin_sqrtf; the v_sqrt_f32 behind __fsqrt_rn is not);
  *                y = fmaf((x − mean)·inv_std, gamma, beta). The row is staged in LDS for the eight sums.
  * NCH chunks of 16 columns per lane (ldq <= 1024·NCH). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
- * ldx % 4 == 0; HEADS with Dh % 16 == 0; X 16-byte aligned. */
+ * ldx % 4 == 0 (LN: gamma and beta 16-byte aligned too); HEADS with Dh % 16 == 0; X 16-byte aligned. */
 template <int KIND, int NCH, bool VEC>
 __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
 {
-    __shared__ float stage[KIND == PROD_LN ? 4 * 1024 * NCH : 1];
+    __shared__ __align__(16) float stage[KIND == PROD_LN ? 4 * 8 * (128 * NCH + 20) : 1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int m = blockIdx.x * 4 + w;
     if (m >= a.Mp) return;
@@ -244,6 +244,25 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
         return;
     }
     float x[NCH][16];
+    /* LN: gamma and beta for the lane's columns, requested before the row's statistics need the wave for a while */
+    constexpr int GB = KIND == PROD_LN && NCH <= 2 ? NCH : 1;
+    float gam[GB][16], bet[GB][16];
+    if (KIND == PROD_LN && NCH <= 2) {
+#pragma unroll
+        for (int c = 0; c < GB; c++) {
+            const int k0 = 16 * (lane + 64 * c);
+            if (VEC) {
+                load16<true>(a.gamma, k0, K, gam[c]);
+                load16<true>(a.beta, k0, K, bet[c]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    gam[c][e] = k0 + e < K ? a.gamma[k0 + e] : 0.0f;
+                    bet[c][e] = k0 + e < K ? a.beta[k0 + e] : 0.0f;
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
         const int k0 = 16 * (lane + 64 * c);
@@ -272,37 +291,64 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
         }
     }
     if (KIND == PROD_LN) {
-        float *row = stage + w * 1024 * NCH;
+        /* The row in LDS by chain: element k at rt[(k % 8)·S + k / 8], so chain j's elements are contiguous and read
+         * as float4; S = 128·NCH + 20 leaves each chain 16 elements of padding past its 128·NCH (a prefetch of one
+         * batch past the end stays inside the chain's row) and puts the eight chains in different banks. Lane L's
+         * element e of chunk c is k = 16·(L + 64c) + e: x[e] and x[e + 8] are neighbours in chain e. Zeros beyond
+         * K. */
+        constexpr int S = 128 * NCH + 20;
+        float *rt = stage + w * 8 * S;
 #pragma unroll
         for (int c = 0; c < NCH; c++)
 #pragma unroll
-            for (int e = 0; e < 16; e++)
-                if (16 * (lane + 64 * c) + e < K) row[16 * (lane + 64 * c) + e] = x[c][e];
+            for (int e = 0; e < 8; e++)
+                *reinterpret_cast<float2 *>(rt + e * S + 2 * (lane + 64 * c)) = make_float2(x[c][e], x[c][e + 8]);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const int body = K / 8 * 8;
-        float part = 0.0f;
-        if (lane < 8)
-            for (int k = lane; k < body; k += 8) part = __fadd_rn(part, row[k]);
-        float v8[8];
+        const int body = K / 8 * 8, n8 = body / 8, nb = n8 / 16;
+        /* chain j = lane (j < 8): rt[j·S + 0 .. n8 − 1] in order, in batches of 16, the next batch's LDS reads in
+         * flight while the current one is added */
+        auto chain = [&](auto add) {
+            float p = 0.0f;
+            if (lane < 8) {
+                const float *cj = rt + lane * S;
+                auto add16 = [&](float p, const float4 (&v)[4]) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j);
-        float sum = __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
-                              __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
-        for (int k = body; k < K; k++) sum = __fadd_rn(sum, row[k]);
-        const float mean = __fdiv_rn(sum, (float)K);
-        part = 0.0f;
-        if (lane < 8)
-            for (int k = lane; k < body; k += 8) {
-                const float d = __fsub_rn(row[k], mean);
-                part = __builtin_fmaf(d, d, part);
+                    for (int u = 0; u < 4; u++) p = add(add(add(add(p, v[u].x), v[u].y), v[u].z), v[u].w);
+                    return p;
+                };
+                float4 va[4], vb[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) va[u] = *reinterpret_cast<const float4 *>(cj + 4 * u);
+                int b = 0;
+                for (; b + 2 <= nb; b += 2) {   /* loads are unconditional: batch nb lies in the row's padding */
+#pragma unroll
+                    for (int u = 0; u < 4; u++) vb[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 1) + 4 * u);
+                    p = add16(p, va);
+#pragma unroll
+                    for (int u = 0; u < 4; u++) va[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 2) + 4 * u);
+                    p = add16(p, vb);
+                }
+                if (b < nb) p = add16(p, va);
+                for (int i = 16 * nb; i < n8; i++) p = add(p, cj[i]);
             }
+            /* p2_hsum_avx2: lanes i and i + 4, then pairs */
+            float v8[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j);
-        float var_sum = __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
-                                  __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+            for (int j = 0; j < 8; j++) v8[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+            return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
+                             __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+        };
+        auto at = [&](int k) { return rt[(k & 7) * S + (k >> 3)]; };
+        float sum = chain([](float p, float v) { return __fadd_rn(p, v); });
+        for (int k = body; k < K; k++) sum = __fadd_rn(sum, at(k));
+        const float mean = __fdiv_rn(sum, (float)K);
+        float var_sum = chain([mean](float p, float v) {
+            const float d = __fsub_rn(v, mean);
+            return __builtin_fmaf(d, d, p);
+        });
         for (int k = body; k < K; k++) {
-            const float d = __fsub_rn(row[k], mean);
+            const float d = __fsub_rn(at(k), mean);
             var_sum = __builtin_fmaf(d, d, var_sum);
         }
         const float inv_std = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(var_sum, (float)K), 1e-5f)));
@@ -311,7 +357,9 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int k = min(16 * (lane + 64 * c) + e, K - 1);
-                const float y = __builtin_fmaf(__fmul_rn(__fsub_rn(x[c][e], mean), inv_std), a.gamma[k], a.beta[k]);
+                const float g = NCH <= 2 ? gam[NCH <= 2 ? c : 0][e] : a.gamma[k];
+                const float b = NCH <= 2 ? bet[NCH <= 2 ? c : 0][e] : a.beta[k];
+                const float y = __builtin_fmaf(__fmul_rn(__fsub_rn(x[c][e], mean), inv_std), g, b);
                 x[c][e] = (16 * (lane + 64 * c) + e < K) ? y : 0.0f;
             }
     }
@@ -329,6 +377,52 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
         if (k0 < a.ldq) *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = quant16(x[c], k0, K, k16, scale, inv);
     }
     if (lane == 0) a.scales[m] = scale;
+}
+
+/* PROD_CMAJOR for K <= 1024, ldq <= 1024: a workgroup of 16 waves takes 16 consecutive rows t0..t0+15 of the
+ * transpose of X [K][T]. Its threads read the 16 values X[d][t0..t0+15] of one channel d as one 64-byte segment
+ * (produce_rows reads them a column element per lane), store them transposed into LDS (row stride 1028 floats, so
+ * the 64 lanes of a store hit distinct banks and rows stay 16-byte aligned), then wave w quantises row t0 + w from
+ * LDS exactly as produce_rows does. Rows at or beyond T read zeros and so write zero codes, as the padding needs. */
+__global__ __launch_bounds__(1024) void cmajor_tile(ProdArgs a)
+{
+    constexpr int LD = 1024 + 4;
+    __shared__ __align__(16) float tile[16 * LD];
+    const int tid = threadIdx.x, t0 = blockIdx.x * 16;
+    const int K = a.K, T = a.T;
+    {
+        const int tr = tid & 15, dr = tid >> 4;
+        const int t = t0 + tr;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int d = dr + 64 * i;
+            v[i] = (d < K && t < T) ? a.X[(size_t)d * T + t] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) tile[tr * LD + dr + 64 * i] = v[i];
+    }
+    __syncthreads();
+    const int lane = tid & 63, w = tid >> 6;
+    const int m = t0 + w;
+    const int kst = a.ldq / 64, k16 = K / 16 * 16, k0 = 16 * lane;
+    float x[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 v = *reinterpret_cast<const float4 *>(&tile[w * LD + k0 + 4 * q]);
+        x[4 * q] = v.x;
+        x[4 * q + 1] = v.y;
+        x[4 * q + 2] = v.z;
+        x[4 * q + 3] = v.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[e]));
+    amax = wave_max_dpp(amax);
+    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    if (k0 < a.ldq) *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = quant16(x, k0, K, k16, scale, inv);
+    if (lane == 0 && m < a.M) a.scales[m] = scale;
 }
 
 /* ── the int8 GEMM ─────────────────────────────────────────────────────────────────────────────────────────── */

@@ -66,7 +66,7 @@ def test_concat_heads_quant_rows(H, T, Dh):
     _same(P.concat_heads_quant_rows(A), O.concat_heads_quant_rows(A), T, H * Dh)
 
 
-@pytest.mark.parametrize("D,T", [(1024, 375), (1024, 6000), (100, 7), (1, 3)])
+@pytest.mark.parametrize("D,T", [(1024, 375), (1024, 6000), (100, 7), (1, 3), (1500, 37), (4096, 20)])
 def test_channel_major_quant_rows(D, T):
     print(f"channel_major_quant_rows D={D} T={T}", flush=True)
     rng = np.random.default_rng(SEED + D + T)
