@@ -658,16 +658,17 @@ using FvWK = p2k::FvGeo<6, 2, 4, 2>;  /*  96 × 128, 2 stages: K > 1024, unsplit
 /* Small-M tiles (gemm_fvs): operands straight to registers, K split across the four waves, 4-bit records */
 using SmS = p2k::SmGeo<2, 2, true>;     /*  32 ×  32 */
 using SmW = p2k::SmGeo<3, 4, true>;     /*  48 ×  64 (int8w) */
+using SmD = p2k::SmGeo<2, 4, true, 2, 8>;    /*  32 ×  64, eight waves of four units each, all in flight: K > 1024 (int8w) */
 enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_WK = 9,
-       FV_SS = 10, FV_SW = 11, FV_COUNT = 12 };
+       FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_COUNT = 13 };
 const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
-                             FvWK::BM, SmS::BM, SmW::BM};
+                             FvWK::BM, SmS::BM, SmW::BM, SmD::BM};
 const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN, FvW6::BN,
-                             FvWK::BN, SmS::BN, SmW::BN};
+                             FvWK::BN, SmS::BN, SmW::BN, SmD::BN};
 /* gemm_fvs splits K among the four waves of a workgroup: at most four K segments, so K <= 4096 */
 inline bool small_ok(int K) { return K <= 4 * p2k::kFoldRows; }
-inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW; }
-inline bool uses_rec4(int cfg) { return cfg == FV_W6 || cfg == FV_WK || cfg == FV_SS || cfg == FV_SW; }
+inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW || cfg == FV_SD; }
+inline bool uses_rec4(int cfg) { return cfg == FV_W6 || cfg == FV_WK || is_small(cfg); }
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -694,13 +695,22 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
      * tiles on 4-bit records (int8w) or 128 × 128 (the two-plane mode needs twice the accumulators) */
     int cfg;
     if (M <= 1024)   /* small M: the register-streaming kernel, 48 × 64 for wide outputs at a few hundred rows */
-        cfg = !small_ok(K) ? FV_T : (K <= p2k::kFoldRows && N >= 2048 && M >= 256) ? FV_SW : FV_SS;
+    {
+        /* K > 1024 (int8w): eight waves of a 32 × 64 tile keep a whole segment's loads in flight, one workgroup per
+         * CU, so only where those tiles fill the CUs in one round without leaving most of them idle */
+        const int cus_ = g_cus > 0 ? g_cus : 256;
+        const int sd_tiles = ((M + SmD::BM - 1) / SmD::BM) * ((N + SmD::BN - 1) / SmD::BN);
+        cfg = !small_ok(K) ? FV_T
+              : (K <= p2k::kFoldRows && N >= 2048 && M >= 256) ? FV_SW
+              : (K > p2k::kFoldRows && mode == P2H_INT8W && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
+              : FV_SS;
+    }
     else
         cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_WK : FV_W6) : FV_L;
     cfg = env_int("P2H_TILE", cfg);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
     if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_WK)) cfg = FV_L;
-    if (mode == P2H_INT8 && cfg == FV_SW) cfg = FV_SS;
+    if (mode == P2H_INT8 && (cfg == FV_SW || cfg == FV_SD)) cfg = FV_SS;
     if (is_small(cfg) && !small_ok(K)) cfg = FV_T;
     /* these never split K across workgroups: the fold stays in the kernel */
     const bool large = cfg == FV_W6 || cfg == FV_WK || is_small(cfg);
@@ -777,7 +787,7 @@ void launch_fv(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 template <class G, int MODE>
 void launch_fvs(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
-    hipLaunchKernelGGL((p2k::gemm_fvs<G, MODE>), dim3((unsigned)((size_t)p.tiles_m * p.tiles_n)), dim3(256), 0, s,
+    hipLaunchKernelGGL((p2k::gemm_fvs<G, MODE>), dim3((unsigned)((size_t)p.tiles_m * p.tiles_n)), dim3(G::NT), 0, s,
                        g);
 }
 
@@ -787,6 +797,8 @@ void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
     switch (p.cfg) {
     case FV_SS: launch_fvs<SmS, MODE>(g, p, s); break;
     case FV_SW: if (MODE == p2k::MODE_INT8W) { launch_fvs<SmW, p2k::MODE_INT8W>(g, p, s); break; }
+                launch_fvs<SmS, MODE>(g, p, s); break;
+    case FV_SD: if (MODE == p2k::MODE_INT8W) { launch_fvs<SmD, p2k::MODE_INT8W>(g, p, s); break; }
                 launch_fvs<SmS, MODE>(g, p, s); break;
     case FV_T: launch_fv<FvT, MODE>(g, p, s); break;
     case FV_S: launch_fv<FvS, MODE>(g, p, s); break;

@@ -1350,25 +1350,33 @@ __global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
 
 /* ── the small-M five-value GEMM ─────────────────────────────────────────────────────────────────────────────── */
 
-/* Small-M tile: a workgroup of four waves owns one BM × BN output tile (BM = 16·FM activation rows, BN = 16·FN
- * weight columns) and splits K among its waves. Each wave loads its operands straight from global memory into
+/* Small-M tile: a workgroup of W waves (four, or sixteen for long K) owns one BM × BN output tile (BM = 16·FM
+ * activation rows, BN = 16·FN weight columns) and splits K among its waves. Each wave loads its operands straight from global memory into
  * registers – the tiled activations and the operand records are already in matrix-core order – two 128-row units
  * per load batch, the next batch in flight while the current one is decoded and multiplied. No LDS staging and no
  * barrier in the K loop. */
-template <int FM_, int FN_, bool REC4_, int CH_ = 2>
+template <int FM_, int FN_, bool REC4_, int CH_ = 2, int W_ = 4>
 struct SmGeo {
     static constexpr int FM = FM_, FN = FN_;
     static constexpr bool REC4 = REC4_;
     static constexpr int BM = 16 * FM, BN = 16 * FN;
+    static constexpr int WAVES = W_, NT = 64 * W_;
     static constexpr int PITCH = BN + 4;     /* int32 per row of a partial tile in LDS */
-    static constexpr int MAXSEG = 4;         /* K segments per tile (one per wave; K <= 4096) */
+    static constexpr int MAXSEG = W_;        /* K segments per tile (one per wave; K <= 4096) */
     static constexpr int CH = CH_;           /* 128-row units per load batch (two batches in registers) */
     static_assert(CH == 1 || CH == 2 || CH == 4 || CH == 8, "batches divide a segment's 8 units");
 };
 
-/* K segments of a small-M call: up to 1024 rows, four segments of ceil(units / 4) units inside the one fold block;
- * beyond, one segment per 1024-row fold block (so every segment's int32 sum belongs to one block). */
-__host__ __device__ __forceinline__ int sm_seg_units(int units) { return units <= 8 ? (units + 3) / 4 : 8; }
+/* 128-row units per K segment of a small-M call with `waves` waves: up to 1024 rows, ceil(units / waves) inside the
+ * one fold block; beyond, the smallest of 1, 2, 4, 8 that leaves at most one segment per wave, so that every
+ * segment lies inside one 1024-row fold block and its int32 sum belongs to that block. */
+__host__ __device__ __forceinline__ int sm_seg_units(int units, int waves)
+{
+    if (units <= 8) return (units + waves - 1) / waves;
+    int d = 1;
+    while (d < 8 && (units + d - 1) / d > waves) d *= 2;
+    return d;
+}
 
 template <class G, int MODE, bool TWO_OUT>
 __device__ __forceinline__ void sm_unit_mma(const v4i (&a)[2][G::FM], const uint32_t (&r)[G::FN][4],
@@ -1425,7 +1433,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
     const int n0 = tile_n * BN, m0 = tile_m * BM;
     const int M = g.M, N = g.N, units = g.units;
-    const int seg_units = sm_seg_units(units);
+    const int seg_units = sm_seg_units(units, G::WAVES);
     const int nseg = (units + seg_units - 1) / seg_units;
 
     /* per-lane operand addresses (row and column groups clamped into the padded operands; outputs are masked) */
@@ -1468,7 +1476,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
         }
     };
 
-    for (int seg = wave; seg < nseg; seg += 4) {
+    for (int seg = wave; seg < nseg; seg += G::WAVES) {
         const int u_begin = seg * seg_units, u_end = min(units, u_begin + seg_units);
         v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
 #pragma unroll
@@ -1504,7 +1512,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
 
     /* fold: thread t owns rows t / (BN / 4) + 256 / (BN / 4)·q and four consecutive columns 4·(t % (BN / 4)) */
     constexpr int TPR = BN / 4;                  /* threads per output row */
-    constexpr int RPP = 256 / TPR;               /* rows per pass */
+    constexpr int RPP = G::NT / TPR;             /* rows per pass */
     const int cq = tid % TPR, n = n0 + 4 * cq;
     if (n >= N) return;
     v4f c1 = *reinterpret_cast<const v4f *>(g.c1 + n);
@@ -1512,6 +1520,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     if (TWO) c2 = *reinterpret_cast<const v4f *>(g.c2 + n);
     const bool beta_zero = g.beta == 0.0f;
     const int nblocks = (units + 7) / 8;
+    const int spb = units <= 8 ? nseg : 8 / seg_units;   /* segments per fold block */
     for (int row = tid / TPR; row < BM; row += RPP) {
         const int m = m0 + row;
         if (m >= M) break;
@@ -1533,7 +1542,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
         }
         for (int blk = 0; blk < nblocks; blk++) {
             /* the segments of this block: all of them below 1024 rows, else exactly the block's own */
-            const int s0 = units <= 8 ? 0 : blk, s1 = units <= 8 ? nseg : blk + 1;
+            const int s0 = units <= 8 ? 0 : blk * spb, s1 = units <= 8 ? nseg : min(nseg, s0 + spb);
             v4i sum = v4i{0, 0, 0, 0}, sumT = v4i{0, 0, 0, 0};
             for (int sg = s0; sg < s1; sg++) {
                 sum += *reinterpret_cast<const v4i *>(part + sg * TILE + row * PITCH + 4 * cq);
@@ -1556,7 +1565,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
 }
 
 template <class G, int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_fvs(GemmArgs g)
+__global__ __launch_bounds__(G::NT, G::NT > 256 ? 1 : 2) void gemm_fvs(GemmArgs g)
 {
     fvs_tile<G, MODE>(g);
 }

@@ -313,7 +313,7 @@ def test_full_size_sampled_rows(M, K, N):
 _TILE_CASES = {}
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 8, 9, 10, 11])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("split_rows", [-1, 0, 256, 512, 1024])
 @pytest.mark.parametrize("M,K,N", [(375, 4096, 1024), (130, 1028, 272), (38, 1024, 4096), (300, 2048, 512)])
 def test_tiles_and_splits_int8w(monkeypatch, tile, split_rows, M, K, N):
