@@ -218,8 +218,8 @@ __device__ __forceinline__ float silu_p2(float x)
     return __fmul_rn(x, __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_p2(0.0f - x))));
 }
 
-/* One wave per row of the padded row range, the quantised row into the tiled layout as quant_rows does; the row is
- * made on the way in:
+/* One wave per row of the padded row range (WPR = 4: a workgroup of four waves per row, for few long rows), the
+ * quantised row into the tiled layout as quant_rows does; the row is made on the way in:
  *   PROD_SILU    SiLU of row m of X (p2_swish_quant_rows, tensor_ops.c:491-511; K % 8 == 0)
  *   PROD_HEADS   row t of the head concatenation: element k = h·Dh + d is X[h][t][d] (encoder.c:449-463)
  *   PROD_CMAJOR  row t of the transpose of the channel-major X [K][T] (encoder.c:554-568)
@@ -228,18 +228,22 @@ __device__ __forceinline__ float silu_p2(float x)
  *                the same for fmaf(d, d, ·) with d = x − mean; inv_std = 1/sqrtf(var + 1e-5), square root and
  *                quotient correctly rounded (__builtin_sqrtf; the v_sqrt_f32 behind __fsqrt_rn is not);
  *                y = fmaf((x − mean)·inv_std, gamma, beta). The row is staged in LDS for the eight sums.
- * NCH chunks of 16 columns per lane (ldq <= 1024·NCH). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
+ * NCH chunks of 16 columns per lane (ldq <= 1024·WPR·NCH). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
  * ldx % 4 == 0 (LN: gamma and beta 16-byte aligned too); HEADS with Dh % 16 == 0; X 16-byte aligned. */
-template <int KIND, int NCH, bool VEC>
+template <int KIND, int NCH, bool VEC, int WPR = 1>
 __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
 {
+    static_assert(WPR == 1 || (WPR == 4 && KIND != PROD_LN), "LayerNorm keeps one wave per row");
     __shared__ __align__(16) float stage[KIND == PROD_LN ? 4 * 8 * (128 * NCH + 20) : 1];
+    __shared__ float wmax[4];
+    constexpr int STRIDE = 64 * WPR;                       /* lanes per row */
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int m = blockIdx.x * 4 + w;
+    const int m = blockIdx.x * (4 / WPR) + w / WPR;         /* with four waves per row, the workgroup's row */
+    const int lr = (w % WPR) * 64 + lane;                   /* the thread's place among its row's lanes */
     if (m >= a.Mp) return;
     const int K = a.K, kst = a.ldq / 64, k16 = K / 16 * 16;
     if (m >= a.M) {
-        for (int k0 = 16 * lane; k0 < a.ldq; k0 += 1024)
+        for (int k0 = 16 * lr; k0 < a.ldq; k0 += 16 * STRIDE)
             *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
         return;
     }
@@ -265,10 +269,11 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
     }
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int k0 = 16 * (lane + 64 * c);
-        if ((KIND == PROD_SILU || KIND == PROD_LN) && VEC) {
+        const int k0 = 16 * (lr + STRIDE * c);
+        constexpr bool ROWS = KIND == PROD_SILU || KIND == PROD_LN;
+        if (ROWS && VEC) {
             load16<true>(a.X + (size_t)m * a.ldx, k0, K, x[c]);
-        } else if (KIND == PROD_SILU || KIND == PROD_LN) {
+        } else if (ROWS) {
 #pragma unroll
             for (int e = 0; e < 16; e++) x[c][e] = k0 + e < K ? a.X[(size_t)m * a.ldx + k0 + e] : 0.0f;
         } else if (KIND == PROD_HEADS && VEC) {   /* Dh % 16 == 0: the chunk lies in one head */
@@ -369,14 +374,19 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
 #pragma unroll
         for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[c][e]));
     amax = wave_max_dpp(amax);
+    if (WPR > 1) {   /* the row's four waves meet in LDS (every wave of the workgroup is on this row) */
+        if (lane == 0) wmax[w] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    }
     const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / scale;
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        const int k0 = 16 * (lane + 64 * c);
+        const int k0 = 16 * (lr + STRIDE * c);
         if (k0 < a.ldq) *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = quant16(x[c], k0, K, k16, scale, inv);
     }
-    if (lane == 0) a.scales[m] = scale;
+    if (lr == 0) a.scales[m] = scale;
 }
 
 /* PROD_CMAJOR for K <= 1024, ldq <= 1024: a workgroup of 16 waves takes 16 consecutive rows t0..t0+15 of the

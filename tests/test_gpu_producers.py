@@ -49,7 +49,7 @@ def test_layer_norm_quant_rows(M, D, ldx):
 
 
 @pytest.mark.parametrize("M,K,ldh", [(375, 4096, 4096), (6000, 4096, 4096), (37, 1000, 1003), (3, 8, 8),
-                                     (17, 2048, 2048)])
+                                     (17, 2048, 2048), (21, 2056, 2059)])
 def test_silu_quant_rows(M, K, ldh):
     print(f"silu_quant_rows M={M} K={K} ldh={ldh}", flush=True)
     rng = np.random.default_rng(SEED + 3 * M + K)
@@ -58,7 +58,8 @@ def test_silu_quant_rows(M, K, ldh):
     _same(P.silu_quant_rows(H, K=K), O.silu_quant_rows(H, K=K), M, K)
 
 
-@pytest.mark.parametrize("H,T,Dh", [(8, 375, 128), (8, 6000, 128), (3, 20, 20), (8, 1, 128), (2, 33, 48)])
+@pytest.mark.parametrize("H,T,Dh", [(8, 375, 128), (8, 6000, 128), (3, 20, 20), (8, 1, 128), (2, 33, 48),
+                                     (16, 50, 128), (3, 20, 400), (5, 9, 250)])
 def test_concat_heads_quant_rows(H, T, Dh):
     print(f"concat_heads_quant_rows H={H} T={T} Dh={Dh}", flush=True)
     rng = np.random.default_rng(SEED + H * T + Dh)
@@ -72,6 +73,18 @@ def test_channel_major_quant_rows(D, T):
     rng = np.random.default_rng(SEED + D + T)
     W = rng.standard_normal((D, T)).astype(np.float32)
     _same(P.channel_major_quant_rows(W), O.channel_major_quant_rows(W), T, D)
+
+
+@pytest.mark.parametrize("M,K,lda", [(375, 4096, 4096), (37, 1028, 1028), (19, 2052, 2055), (5, 8192, 8192),
+                                     (3, 16384, 16388), (2, 20000, 20000)])
+def test_quant_rows_long_rows(M, K, lda):
+    """p2h_quant_rows on rows longer than 1024 (the row in registers up to ldq = 4096, read twice beyond)."""
+    print(f"quant_rows M={M} K={K} lda={lda}", flush=True)
+    rng = np.random.default_rng(SEED + M + K)
+    A = _rows(rng, M, lda, 2.0)
+    q, s = P.quant_rows(A, K=K)
+    qr, sr = O.quant_rows(np.ascontiguousarray(A[:, :K]))
+    _same((q, s), (qr, sr), M, K)
 
 
 def test_zero_rows_is_a_no_op():
