@@ -1180,8 +1180,36 @@ int p2h_sgemm_batched(int transA, int transB, int M, int N, int K, float alpha, 
     g.B = dB; g.ldb = ldb; g.sB = strideB; g.transB = transB ? 1 : 0;
     g.C = dC; g.ldc = ldc; g.sC = strideC;
     g.tiles_n = (N + 63) / 64;
-    const dim3 grid((unsigned)((size_t)g.tiles_n * ((M + 63) / 64)), (unsigned)batch);
-    hipLaunchKernelGGL(p2k::sgemm_f32, grid, dim3(256), 0, s, g);
+    g.batch = batch;
+    const size_t blocks = (size_t)g.tiles_n * ((M + 63) / 64) * batch;
+    if (blocks > 0x7fffffffu) return fail(P2H_E_ARG, "p2h_sgemm_batched: %zu tiles exceed one launch", blocks);
+    const dim3 grid((unsigned)blocks);
+    /* operand reads: 16-byte loads where every batch's rows are aligned and row lengths are multiples of 4, else
+     * buffer loads (operands under 2 GiB), else element loads */
+    const long long spanA = ((long long)((transA ? K : M) - 1) * lda + (transA ? M : K)) * 4;
+    const long long spanB = ((long long)((transB ? N : K) - 1) * ldb + (transB ? K : N)) * 4;
+    const bool va = lda % 4 == 0 && strideA % 4 == 0 && aligned(dA, 16) && (transA ? M : K) % 4 == 0;
+    const bool vb = ldb % 4 == 0 && strideB % 4 == 0 && aligned(dB, 16) && (transB ? K : N) % 4 == 0;
+    const bool small = spanA < (1ll << 31) && spanB < (1ll << 31);
+    using VecT = std::integral_constant<int, p2k::LD_VEC>;
+    using BufT = std::integral_constant<int, p2k::LD_BUF>;
+    using AnyT = std::integral_constant<int, p2k::LD_ANY>;
+    auto go = [&](auto ta, auto tb, auto la, auto lb) {
+        hipLaunchKernelGGL((p2k::sgemm_f32<decltype(ta)::value, decltype(tb)::value, decltype(la)::value,
+                                           decltype(lb)::value>),
+                           grid, dim3(256), 0, s, g);
+    };
+    auto by_load = [&](auto ta, auto tb) {
+        if (!small) go(ta, tb, AnyT{}, AnyT{});
+        else if (va && vb) go(ta, tb, VecT{}, VecT{});
+        else if (va) go(ta, tb, VecT{}, BufT{});
+        else if (vb) go(ta, tb, BufT{}, VecT{});
+        else go(ta, tb, BufT{}, BufT{});
+    };
+    if (transA && transB) by_load(std::true_type{}, std::true_type{});
+    else if (transA) by_load(std::true_type{}, std::false_type{});
+    else if (transB) by_load(std::false_type{}, std::true_type{});
+    else by_load(std::false_type{}, std::false_type{});
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }

@@ -1923,48 +1923,135 @@ struct SgemmArgs {
     const float *A; int lda; long long sA; int transA;
     const float *B; int ldb; long long sB; int transB;
     float *C; int ldc; long long sC;
-    int tiles_n;
+    int tiles_n, batch;
 };
 
-__global__ __launch_bounds__(256, 2) void sgemm_f32(SgemmArgs g)
+/* How an sgemm operand is read: LD_VEC, 16-byte loads (rows 16-byte aligned, row length a multiple of 4, so a run
+ * of four is all in range or all out); LD_BUF, buffer loads through a descriptor whose range ends at the operand's
+ * last element, an out-of-range element's offset pushed past that range so the hardware returns zero (no branch,
+ * so the loads stay in flight; the operand spans less than 2 GiB); LD_ANY, element loads behind range checks. */
+enum { LD_VEC = 0, LD_BUF = 1, LD_ANY = 2 };
+constexpr uint32_t kBufDword3 = 0x00020000u;   /* raw buffer descriptor word 3 for gfx9 */
+
+/* One operand's panel of a 32-row K stage in an sgemm workgroup of 256 threads. KMAJ: the panel is [k][x] (32 k-rows
+ * of 64 values, the operand stored with x contiguous); else [x][k] (64 x-rows of 32 values, k contiguous). The panel
+ * keeps that orientation in LDS: [k][x] rows 80 floats apart (≡ 16 mod 32: the 16-lane groups of an MFMA operand
+ * read, one k-row each, fall in disjoint halves of the banks), [x][k] rows 34 apart (≡ 2 mod 32: lane (x, g) reads
+ * bank 2x + g, distinct over a 32-lane pass), so no transpose happens at store time. Each thread moves 8 values:
+ *   LD_VEC: two runs of 4 along the contiguous dimension, 16-byte loads (rows aligned, length a multiple of 4);
+ *   else: 8 single values, consecutive lanes on consecutive columns, so each load instruction reads whole row
+ *   segments; LD_BUF through a buffer descriptor (out-of-range offsets return zero, no branches), LD_ANY with range
+ *   checks. Rows outside the operand, and columns past its row length, read as zeros. */
+template <bool KMAJ, int LD>
+struct SgPanel {
+    static constexpr int S = KMAJ ? 80 : 34;          /* LDS row stride */
+    static constexpr int CW = KMAJ ? 64 : 32;         /* panel row length */
+    static constexpr int SIZE = KMAJ ? 32 * 80 : 64 * 34;
+    const float *base;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int ld, rows, len;                                /* operand: leading dimension, rows, valid values per row */
+
+    /* panel origin: (row0, col0) in operand coordinates; thread tid; v: the thread's 8 values */
+    __device__ __forceinline__ void load(int row0, int col0, int tid, float (&v)[8]) const
+    {
+        if (LD == LD_VEC) {
+            const int r = KMAJ ? tid / 8 : tid / 4, c = KMAJ ? 8 * (tid % 8) : 8 * (tid % 4);
+            const int gr = row0 + r;
+            const bool rok = gr < rows;
+            const float *row = base + (size_t)min(gr, rows - 1) * ld;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int gc = col0 + c + 4 * h;
+                const bool ok = rok && gc < len;
+                const float4 x = *reinterpret_cast<const float4 *>(row + (ok ? gc : 0));
+                v[4 * h] = ok ? x.x : 0.0f;
+                v[4 * h + 1] = ok ? x.y : 0.0f;
+                v[4 * h + 2] = ok ? x.z : 0.0f;
+                v[4 * h + 3] = ok ? x.w : 0.0f;
+            }
+        } else {
+            const int c = tid % CW, gc = col0 + c;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int gr = row0 + q * (256 / CW) + tid / CW;
+                const bool ok = gr < rows && gc < len;
+                if (LD == LD_BUF) {
+                    const int off = ok ? 4 * (gr * ld + gc) : (int)0x80000000u;
+                    v[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+                } else {
+                    v[q] = ok ? base[(size_t)gr * ld + gc] : 0.0f;
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float *panel, int tid, const float (&v)[8]) const
+    {
+        if (LD == LD_VEC) {
+            const int r = KMAJ ? tid / 8 : tid / 4, c = KMAJ ? 8 * (tid % 8) : 8 * (tid % 4);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float *d = panel + r * S + c + 4 * h;
+                if (KMAJ) {
+                    *reinterpret_cast<float4 *>(d) = make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]);
+                } else {   /* rows 34 floats apart: 8-byte aligned */
+                    *reinterpret_cast<float2 *>(d) = make_float2(v[4 * h], v[4 * h + 1]);
+                    *reinterpret_cast<float2 *>(d + 2) = make_float2(v[4 * h + 2], v[4 * h + 3]);
+                }
+            }
+        } else {
+            const int c = tid % CW;
+#pragma unroll
+            for (int q = 0; q < 8; q++) panel[(q * (256 / CW) + tid / CW) * S + c] = v[q];
+        }
+    }
+    /* the MFMA operand element (k, x) */
+    __device__ __forceinline__ static int at(int k, int x) { return KMAJ ? k * S + x : x * S + k; }
+};
+
+/* fp32 GEMM, C = alpha·op(A)·op(B) + beta·C, batched (the attention heads of heads_gemm, encoder.c:279-316; batch
+ * index = workgroup id % batch). 64 × 64 tiles, four waves of 32 × 32, v_mfma_f32_16x16x4_f32 (B operand → lane
+ * rows n, so a lane's four results are four consecutive n of one row). K advances in stages of 32 through two LDS
+ * buffers per operand (SgPanel); each thread brings its 8 + 8 values of a stage into a three-slot register ring,
+ * two stages ahead of the one being multiplied, and a stage's LDS operands are all requested before its first
+ * MFMA (192 VGPRs would cost the third workgroup per CU that 576-tile launches need).
+ * Stages past the end are loaded too (as zeros), so that every iteration issues the same loads and the compiler's
+ * wait counts stay exact. TA: A stored [k][m]; TB: B stored [n][k]. LA / LB: how each operand is read (LD_*). */
+template <bool TA, bool TB, int LA, int LB>
+__global__ __launch_bounds__(256, 3) void sgemm_f32(SgemmArgs g)
 {
-    constexpr int BMS = 64, BNS = 64, BKS = 16;
-    __shared__ __attribute__((aligned(16))) float sA[2][BKS][BMS + 4];
-    __shared__ __attribute__((aligned(16))) float sB[2][BKS][BNS + 4];
+    constexpr int BMS = 64, BNS = 64, BKS = 32, RING = 3, AHEAD = 2;
+    using PA = SgPanel<TA, LA>;      /* A [k][m] is k-major */
+    using PB = SgPanel<!TB, LB>;     /* B [k][n] is k-major */
+    __shared__ __attribute__((aligned(16))) float sA[2][PA::SIZE];
+    __shared__ __attribute__((aligned(16))) float sB[2][PB::SIZE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;                        /* this wave's 32 × 32 quarter */
-    const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
+    /* workgroups reach the 8 XCDs round-robin by linear id, so the batch index is the id's low part: with 8 (or a
+     * multiple or divisor of 8) batches every XCD works on its own batches and their operands stay in its L2 */
+    const int bat = (int)(blockIdx.x % (unsigned)g.batch), tile = (int)(blockIdx.x / (unsigned)g.batch);
+    const int tile_n = tile % g.tiles_n, tile_m = tile / g.tiles_n;
     const int m0 = tile_m * BMS, n0 = tile_n * BNS;
-    const float *A = g.A + (size_t)blockIdx.y * g.sA;
-    const float *B = g.B + (size_t)blockIdx.y * g.sB;
-    float *C = g.C + (size_t)blockIdx.y * g.sC;
+    const float *A = g.A + (size_t)bat * g.sA;
+    const float *B = g.B + (size_t)bat * g.sB;
+    float *C = g.C + (size_t)bat * g.sC;
     const int M = g.M, N = g.N, K = g.K;
-
-    /* loader: thread tid brings 4 values of each panel per stage */
-    float ra[4], rb[4];
-    auto load = [&](int k0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            int m, k;
-            if (g.transA) { k = tid / 16; m = 4 * (tid % 16) + e; }   /* A stored [k][m]: rows of m contiguous */
-            else { m = tid / 4; k = 4 * (tid % 4) + e; }               /* A stored [m][k] */
-            const int gm = m0 + m, gk = k0 + k;
-            ra[e] = (gm < M && gk < K) ? (g.transA ? A[(size_t)gk * g.lda + gm] : A[(size_t)gm * g.lda + gk]) : 0.0f;
-            int n, kb;
-            if (g.transB) { n = tid / 4; kb = 4 * (tid % 4) + e; }     /* B stored [n][k] */
-            else { kb = tid / 16; n = 4 * (tid % 16) + e; }            /* B stored [k][n] */
-            const int gn = n0 + n, gkb = k0 + kb;
-            rb[e] = (gn < N && gkb < K) ? (g.transB ? B[(size_t)gn * g.ldb + gkb] : B[(size_t)gkb * g.ldb + gn]) : 0.0f;
-        }
+    PA pa;
+    pa.base = A; pa.ld = g.lda; pa.rows = TA ? K : M; pa.len = TA ? M : K;
+    pa.rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, LA == LD_BUF ? 4 * ((pa.rows - 1) * pa.ld + pa.len) : 0,
+                                                (int)kBufDword3);
+    PB pb;
+    pb.base = B; pb.ld = g.ldb; pb.rows = TB ? N : K; pb.len = TB ? K : N;
+    pb.rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, LB == LD_BUF ? 4 * ((pb.rows - 1) * pb.ld + pb.len) : 0,
+                                                (int)kBufDword3);
+    float ra[RING][8], rb[RING][8];
+    auto load = [&](int t, float (&xa)[8], float (&xb)[8]) __attribute__((always_inline)) {
+        const int k0 = t * BKS;
+        if (TA) pa.load(k0, m0, tid, xa); else pa.load(m0, k0, tid, xa);
+        if (TB) pb.load(n0, k0, tid, xb); else pb.load(k0, n0, tid, xb);
     };
-    auto store = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (g.transA) sA[buf][tid / 16][4 * (tid % 16) + e] = ra[e];
-            else sA[buf][4 * (tid % 4) + e][tid / 4] = ra[e];
-            if (g.transB) sB[buf][4 * (tid % 4) + e][tid / 4] = rb[e];
-            else sB[buf][tid / 16][4 * (tid % 16) + e] = rb[e];
-        }
+    auto store = [&](int buf, const float (&xa)[8], const float (&xb)[8]) __attribute__((always_inline)) {
+        pa.store(sA[buf], tid, xa);
+        pb.store(sB[buf], tid, xb);
     };
 
     v4f acc[2][2];
@@ -1973,29 +2060,42 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32(SgemmArgs g)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     const int nk = (K + BKS - 1) / BKS;
-    load(0);
-    store(0);
+    /* stages past the end are loaded too (they read as zeros, from clamped addresses), so that every iteration
+     * issues the same loads and the compiler's wait counts stay exact */
+#pragma unroll
+    for (int s = 0; s < AHEAD; s++) load(s, ra[s], rb[s]);
+    store(0, ra[0], rb[0]);
     __syncthreads();
-    for (int t = 0; t < nk; t++) {
-        const int buf = t & 1;
-        if (t + 1 < nk) load((t + 1) * BKS);
+    for (int t0 = 0; t0 < nk; t0 += RING) {
 #pragma unroll
-        for (int ks = 0; ks < BKS / 4; ks++) {
-            const int kk = 4 * ks + (lane >> 4);
-            float a[2], b[2];
+        for (int u = 0; u < RING; u++) {   /* stage t = t0 + u sits in ring slot u and LDS buffer t & 1 */
+            const int t = t0 + u, buf = t & 1;
+            if (t >= nk) break;
+            load(t + AHEAD, ra[(u + AHEAD) % RING], rb[(u + AHEAD) % RING]);
+            /* the stage's operands, all requested before the first MFMA (one LDS latency per stage, not per step) */
+            float a[BKS / 4][2], b[BKS / 4][2];
 #pragma unroll
-            for (int j = 0; j < 2; j++) a[j] = sA[buf][kk][32 * wm + 16 * j + (lane & 15)];
+            for (int ks = 0; ks < BKS / 4; ks++) {
+                const int kk = 4 * ks + (lane >> 4);
 #pragma unroll
-            for (int i = 0; i < 2; i++) b[i] = sB[buf][kk][32 * wn + 16 * i + (lane & 15)];
+                for (int j = 0; j < 2; j++) a[ks][j] = sA[buf][PA::at(kk, 32 * wm + 16 * j + (lane & 15))];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+                for (int i = 0; i < 2; i++) b[ks][i] = sB[buf][PB::at(kk, 32 * wn + 16 * i + (lane & 15))];
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[i], a[j], acc[i][j], 0, 0, 0);
+            for (int ks = 0; ks < BKS / 4; ks++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[ks][i], a[ks][j], acc[i][j], 0, 0, 0);
+            if (t + 1 < nk) store(buf ^ 1, ra[(u + 1) % RING], rb[(u + 1) % RING]);
+            __syncthreads();
         }
-        if (t + 1 < nk) store(buf ^ 1);
-        __syncthreads();
     }
     /* lane l holds C[m][n .. n + 3] with m = m0 + 32·wm + 16·j + l % 16, n = n0 + 32·wn + 16·i + 4·(l / 16) */
+    const bool vecC = g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -2003,11 +2103,23 @@ __global__ __launch_bounds__(256, 2) void sgemm_f32(SgemmArgs g)
             const int m = m0 + 32 * wm + 16 * j + (lane & 15), n = n0 + 32 * wn + 16 * i + 4 * (lane >> 4);
             if (m >= M) continue;
             float *cp = C + (size_t)m * g.ldc + n;
+            if (vecC && n + 3 < N) {
+                v4f c0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                if (g.beta != 0.0f) {
+                    c0 = *reinterpret_cast<const v4f *>(cp);
+                    if (g.beta != 1.0f) c0 = c0 * g.beta;
+                }
+                v4f r;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                if (n + e >= N) break;
-                const float c0 = g.beta == 0.0f ? 0.0f : (g.beta == 1.0f ? cp[e] : cp[e] * g.beta);
-                cp[e] = __builtin_fmaf(g.alpha, acc[i][j][e], c0);
+                for (int e = 0; e < 4; e++) r[e] = __builtin_fmaf(g.alpha, acc[i][j][e], c0[e]);
+                *reinterpret_cast<v4f *>(cp) = r;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if (n + e >= N) break;
+                    const float c0 = g.beta == 0.0f ? 0.0f : (g.beta == 1.0f ? cp[e] : cp[e] * g.beta);
+                    cp[e] = __builtin_fmaf(g.alpha, acc[i][j][e], c0);
+                }
             }
         }
 }
