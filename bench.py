@@ -290,6 +290,13 @@ def main():
     ap.add_argument("--workload", default="ffn375", choices=["ffn375", "m6000", "m38", "sweep", "exact375"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--eager-extras", action="store_true",
+                    help="extra configurations without HIP graphs: the producers, the attention products and the "
+                         "feed-forward module's kernels, each timed by back-to-back launches (what rocprofv3 traces "
+                         "without faulting in hipGraphLaunch)")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="leave the 216-linear sweep out of the extra configurations (its large graph cannot be "
+                         "traced by rocprofv3)")
     ap.add_argument("--kernel-reps", type=int, default=200,
                     help="back-to-back launches of each kernel for the per-kernel durations (0: skip them)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -335,9 +342,13 @@ def main():
     lins, r = run(main_wl, specs[main_wl](), args.steps, args.warmup, args.kernel_reps)
 
     extra = {}
-    if not args.no_extra:
+    if not args.no_extra and args.eager_extras:
+        extra["attention375"] = attention_config(stream, graph=False)
+        extra["producers"] = producer_config(stream)
+        extra["ffn_module375"] = ffn_module_config(stream, graph=False)
+    elif not args.no_extra:
         for name in ("m6000", "m38", "sweep"):
-            if name == main_wl:
+            if name == main_wl or (name == "sweep" and args.no_sweep):
                 continue
             steps = {"m6000": 200, "m38": 2000, "sweep": 50}[name]
             _, rr = run(name, specs[name](), steps, 20, 0 if name == "sweep" else args.kernel_reps)
@@ -459,7 +470,7 @@ def producer_config(stream, reps=200):
     return out
 
 
-def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200):
+def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=True):
     """One conformer feed-forward module as the encoder runs it in the int8 modes (encoder.c:340-348), every step on
     the device and replayed from one graph: LayerNorm quantised as produced, up-projection 1024 -> 4096, SiLU
     quantised as produced, down-projection 4096 -> 1024 with the residual in its epilogue (alpha 0.5, beta 1)."""
@@ -479,18 +490,20 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200):
         lambda: P.fvb_gemm_q8a_dev("int8w", M, D, FF, 0.5, ws.q.ptr, ldF, ws.s.ptr, l2.w, 1.0, x.ptr, D,
                                    ws.ws.ptr, ws.ws.nbytes, stream.ptr),
     )
-    with P.Graph(stream) as graph:
-        for fn in steps_fns:
-            fn()
-    ms, _ = time_graph(graph, stream, steps, warmup)
+    ms = None
+    if graph:
+        with P.Graph(stream) as g:
+            for fn in steps_fns:
+                fn()
+        ms, _ = time_graph(g, stream, steps, warmup)
     kt = [round(time_launches(fn, stream, reps), 5) for fn in steps_fns] if reps > 0 else None
     ops = gemm_ops(M, FF, D) + gemm_ops(M, D, FF)
-    return {"ms_per_step": round(ms, 6), "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+    return {"ms_per_step": round(ms, 6) if ms else None, "tops": round(ops / (ms * 1e-3) / 1e12, 2) if ms else None,
             "kernels_ms": dict(zip(("layer_norm_quant", "gemm_up", "silu_quant", "gemm_down_residual"), kt))
             if kt else None}
 
 
-def attention_config(stream, H=8, T=375, Dh=128):
+def attention_config(stream, H=8, T=375, Dh=128, graph=True, reps=200):
     """The fp32 per-head products of one block's relative-position attention at T = 375 (encoder.c:505-519), every
     head in one p2h_sgemm_batched launch each: Q_u·K_t [T, T], Q_v·P_t [T, 2T−1], scores·V [T, Dh]."""
     rng = np.random.default_rng(SEED)
@@ -499,15 +512,20 @@ def attention_config(stream, H=8, T=375, Dh=128):
             (("qu", (H, T, Dh)), ("kt", (H, Dh, T)), ("pt", (H, Dh, L)), ("s", (H, T, T)), ("v", (H, T, Dh)))}
     out = {k: P.DeviceBuffer(H * T * n * 4) for k, n in (("ac", T), ("bd", L), ("ctx", Dh))}
     calls = ((T, T, Dh, "qu", "kt", "ac"), (T, L, Dh, "qu", "pt", "bd"), (T, Dh, T, "s", "v", "ctx"))
-    with P.Graph(stream) as g:
-        for M, N, K, a, b, c in calls:
-            P.sgemm_batched_dev(False, False, M, N, K, 1.0, bufs[a].ptr, K, M * K, bufs[b].ptr, N, K * N, 0.0,
-                                out[c].ptr, N, M * N, H, stream.ptr)
-    ms, _ = time_graph(g, stream, 200, 10)
+    fns = [lambda M=M, N=N, K=K, a=a, b=b, c=c: P.sgemm_batched_dev(
+        False, False, M, N, K, 1.0, bufs[a].ptr, K, M * K, bufs[b].ptr, N, K * N, 0.0, out[c].ptr, N, M * N, H,
+        stream.ptr) for M, N, K, a, b, c in calls]
     flops = sum(2.0 * H * M * N * K for M, N, K, *_ in calls)
-    return {"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-            "pct_fp32_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 2),
-            "what": f"{H} heads, T={T}, Dh={Dh}: 3 batched fp32 products per block"}
+    res = {"what": f"{H} heads, T={T}, Dh={Dh}: 3 batched fp32 products per block"}
+    if graph:
+        with P.Graph(stream) as g:
+            for fn in fns:
+                fn()
+        ms, _ = time_graph(g, stream, 200, 10)
+        res.update({"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                    "pct_fp32_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 2)})
+    res["products_ms_back_to_back"] = [round(time_launches(fn, stream, reps), 5) for fn in fns]
+    return res
 
 
 if __name__ == "__main__":

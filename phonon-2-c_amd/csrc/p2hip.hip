@@ -536,7 +536,7 @@ static int produce(const char *name, int kind, p2k::ProdArgs a, bool vec, hipStr
                     a.ldq, p2h_q_ld(a.K), P2H_PROD_KMAX, P2H_Q_KALIGN);
     a.Mp = (int)align_up((size_t)a.M, 16);
     if (kind == p2k::PROD_CMAJOR && a.K <= 1024 && a.ldq <= 1024) {   /* 16 rows per workgroup through LDS */
-        hipLaunchKernelGGL(p2k::cmajor_tile, dim3((unsigned)(a.Mp / 16)), dim3(1024), 0, s, a);
+        hipLaunchKernelGGL(p2k::cmajor_tile, dim3((unsigned)align_up((size_t)(a.Mp / 16), 16)), dim3(1024), 0, s, a);
         HIPCHK(hipGetLastError());
         return P2H_OK;
     }

@@ -398,7 +398,13 @@ __global__ __launch_bounds__(1024) void cmajor_tile(ProdArgs a)
 {
     constexpr int LD = 1024 + 4;
     __shared__ __align__(16) float tile[16 * LD];
-    const int tid = threadIdx.x, t0 = blockIdx.x * 16;
+    /* Tiles 2g and 2g + 1 read the two halves of the same 128-byte lines, so they go to workgroups 16p + x and
+     * 16p + 8 + x (g = 8p + x), which the round-robin dispatch puts on the same XCD x, and the second finds the
+     * lines in that XCD's L2. The grid is padded to a multiple of 16 workgroups; the padding ones exit. */
+    const int b = (int)blockIdx.x, xcd = b % 8, slot = b / 8;
+    const int tix = 2 * (8 * (slot / 2) + xcd) + slot % 2;
+    if (tix >= a.Mp / 16) return;
+    const int tid = threadIdx.x, t0 = tix * 16;
     const int K = a.K, T = a.T;
     {
         const int tr = tid & 15, dr = tid >> 4;
