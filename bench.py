@@ -492,10 +492,10 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=Tru
     )
     ms = None
     if graph:
-        with P.Graph(stream) as g:
+        with P.Graph(stream) as gr:
             for fn in steps_fns:
                 fn()
-        ms, _ = time_graph(g, stream, steps, warmup)
+        ms, _ = time_graph(gr, stream, steps, warmup)
     kt = [round(time_launches(fn, stream, reps), 5) for fn in steps_fns] if reps > 0 else None
     ops = gemm_ops(M, FF, D) + gemm_ops(M, D, FF)
     return {"ms_per_step": round(ms, 6) if ms else None, "tops": round(ops / (ms * 1e-3) / 1e12, 2) if ms else None,
@@ -518,10 +518,10 @@ def attention_config(stream, H=8, T=375, Dh=128, graph=True, reps=200):
     flops = sum(2.0 * H * M * N * K for M, N, K, *_ in calls)
     res = {"what": f"{H} heads, T={T}, Dh={Dh}: 3 batched fp32 products per block"}
     if graph:
-        with P.Graph(stream) as g:
+        with P.Graph(stream) as gr:
             for fn in fns:
                 fn()
-        ms, _ = time_graph(g, stream, 200, 10)
+        ms, _ = time_graph(gr, stream, 200, 10)
         res.update({"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
                     "pct_fp32_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 2)})
     res["products_ms_back_to_back"] = [round(time_launches(fn, stream, reps), 5) for fn in fns]
