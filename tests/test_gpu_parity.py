@@ -263,6 +263,27 @@ def test_sgemm_batched_transposed_beta(tA, tB):
     _assert_exact(got.reshape(-1, N), ref.reshape(-1, N))
 
 
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("shape", [(2, 96, 200, 128), (3, 45, 77, 50), (1, 64, 33, 100), (2, 130, 259, 66)])
+@pytest.mark.parametrize("loads", ["chosen", "element"])
+def test_sgemm_batched_every_load_route(monkeypatch, tA, tB, shape, loads):
+    """Every operand orientation with 16-byte loads (rows aligned, lengths multiples of 4), buffer loads (the rest) and
+    the element loads kept for operands of 2 GiB or more (forced by P2H_SGEMM_ANY); K spans several 32-row stages,
+    so the register ring wraps; against float64."""
+    if loads == "element":
+        monkeypatch.setenv("P2H_SGEMM_ANY", "1")
+    b, M, K, N = shape
+    rng = np.random.default_rng(M * K + N)
+    A = rng.standard_normal((b, K, M) if tA else (b, M, K)).astype(np.float32)
+    B = rng.standard_normal((b, N, K) if tB else (b, K, N)).astype(np.float32)
+    C0 = rng.standard_normal((b, M, N)).astype(np.float32)
+    got = P.sgemm_batched(A, B, tA, tB, alpha=0.75, beta=0.5, C0=C0)
+    opA = np.swapaxes(A, 1, 2) if tA else A
+    opB = np.swapaxes(B, 1, 2) if tB else B
+    ref = 0.75 * np.matmul(opA.astype(np.float64), opB.astype(np.float64)) + 0.5 * C0.astype(np.float64)
+    _assert_exact(got.reshape(-1, N), ref.reshape(-1, N))
+
+
 # ── several weights against the same quantised rows in one launch ─────────────────────────────────────────────────
 
 @pytest.mark.parametrize("mode", ["int8w", "int8"])
