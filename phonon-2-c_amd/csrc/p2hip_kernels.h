@@ -1918,11 +1918,7 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
 
 /* fp32 GEMMs on the matrix cores, batched with strides (p2_sgemm / p2_sgemm_st, blas.h:25-36, and the per-head
  * products of attention, encoder.c:279-316, 505-519): C_b = alpha·op(A_b)·op(B_b) + beta·C_b for b < batch, all
- * row-major. A workgroup of four waves (2 × 2) owns a 64 × 64 tile of one batch entry; K advances 16 columns per
- * stage, the A and B panels staged k-major in LDS (double-buffered, one barrier per stage) so that the step-t MFMA's
- * lane l reads A[m = l % 16][k = 4t + l / 16] and B[k][n = l % 16] conflict-free. B is the MFMA's first operand, so a
- * lane's four results are four consecutive n of one row. Sums run in the matrix cores' order (fp32 rounding, not the
- * reference's order). */
+ * row-major; sgemm_f32 below. Sums run in the matrix cores' order (fp32 rounding, not the reference's order). */
 struct SgemmArgs {
     int M, N, K;
     float alpha, beta;
