@@ -52,6 +52,23 @@ def test_encoder_exact_on_matrix_cores(fx):
     assert got_ids == ref_ids
 
 
+@pytest.mark.skipif(not run.have("encdump_gpuall"), reason="oracle/_ref/encdump_gpuall not built")
+@pytest.mark.parametrize("mode,reference", [("exact-chain", "cpu"), ("int8w", "oracle")])
+def test_encoder_every_gemm_on_gpu(fx, mode, reference):
+    """The engine with no blas.c at all: every blas.h function from the GPU library, so the fp32 GEMMs of attention
+    (p2_sgemm_st per head, encoder.c:279-316) and of the subsampling run on the matrix cores as well. They sum in
+    another order than the reference's CPU sgemm, so the frames agree to fp32 rounding carried through 24 blocks
+    (against the same mode with the CPU's fp32 GEMMs) and the token ids are identical."""
+    print(f"encdump_gpuall vs encdump_{reference}, {mode}", flush=True)
+    got, got_ids = run.encdump("gpuall", mode, fx + "/model", fx + "/a.wav", fx + f"/gpuall_{mode}.f32")
+    ref, ref_ids = run.encdump(reference, mode, fx + "/model", fx + "/a.wav", fx + f"/{reference}_{mode}_all.f32")
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    err = np.max(np.abs(got.astype(np.float64) - ref)) / rms
+    print(f"max |gpu - ref| / rms(frames) = {err:.3g}", flush=True)
+    assert err < 1e-3
+    assert got_ids == ref_ids
+
+
 @pytest.mark.parametrize("mode,reference", [("exact-chain", "cpu"), ("exact", "cpu"), ("int8w", "oracle")])
 def test_cli_token_ids(fx, mode, reference):
     wavs = [fx + "/a.wav", fx + "/b.wav"]
