@@ -358,6 +358,7 @@ def main():
         extra["attention375"] = attention_config(stream)
         extra["producers"] = producer_config(stream)
         extra["ffn_module375"] = ffn_module_config(stream)
+        extra["block375"] = block_config(stream)
 
     # dominant kernel of the headline workload: the GEMM with the longest duration
     gt = r["gemm_kernels_ms"]
@@ -501,6 +502,59 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=Tru
     return {"ms_per_step": round(ms, 6) if ms else None, "tops": round(ops / (ms * 1e-3) / 1e12, 2) if ms else None,
             "kernels_ms": dict(zip(("layer_norm_quant", "gemm_up", "silu_quant", "gemm_down_residual"), kt))
             if kt else None}
+
+
+def block_config(stream, T=375, steps=500, warmup=50):
+    """One conformer block's nine five-value linears as the encoder runs them in the int8 modes (encoder.c:333-613),
+    every input made by its producer and every residual added in a GEMM epilogue, on the device and replayed from
+    one graph: LN→int8, ff1.linear1, SiLU→int8, ff1.linear2 (x += ½·), LN→int8, qkv, the positional projection
+    (its rows quantised once per window, so not in the block), heads→int8, out (x += ), LN→int8, pw1,
+    channel-major→int8, pw2 (x += ), LN→int8, ff2.linear1, SiLU→int8, ff2.linear2 (x += ½·). What lies between the
+    linears and is not on this path (attention scores and softmax, GLU, the depthwise convolution) is replaced by
+    fixed buffers of the right shapes: the heads [8, T, 128] and the channel-major conv output [1024, T]."""
+    D, FF, H, Dh = 1024, 4096, 8, 128
+    rng = np.random.default_rng(SEED + 9)
+    x = P.to_device(P.gen_activations(SEED, 10_000 + D + T, T, D))
+    gb = [(P.to_device(rng.uniform(0.5, 1.5, D).astype(np.float32)),
+           P.to_device(rng.uniform(-0.2, 0.2, D).astype(np.float32))) for _ in range(4)]
+    heads = P.to_device((rng.standard_normal((H, T, Dh)) * 0.5).astype(np.float32))
+    cm = P.to_device((rng.standard_normal((D, T)) * 0.5).astype(np.float32))
+    lin = {name: Linear(60 + i, K, N, T) for i, (name, K, N) in enumerate(
+        (("ff1_l1", D, FF), ("ff1_l2", FF, D), ("qkv", D, 3 * D), ("out", D, D), ("pw1", D, 2 * D), ("pw2", D, D),
+         ("ff2_l1", D, FF), ("ff2_l2", FF, D)))}
+    split = max(P.q8a_workspace_bytes("int8w", T, l.N, l.K) for l in lin.values())
+    ws = Scratch(T, FF, split)
+    ldD, ldF = P.q_ld(D), P.q_ld(FF)
+
+    def gemm(l, ldq, alpha, beta, out):
+        P.fvb_gemm_q8a_dev("int8w", T, l.N, l.K, alpha, ws.q.ptr, ldq, ws.s.ptr, l.w, beta, out, l.N,
+                           ws.ws.ptr, ws.ws.nbytes, stream.ptr)
+
+    def ln(i):
+        P.layer_norm_quant_rows_dev(T, D, x.ptr, D, gb[i][0].ptr, gb[i][1].ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)
+
+    def silu(l):
+        P.silu_quant_rows_dev(T, FF, l.out.ptr, FF, ws.q.ptr, ldF, ws.s.ptr, stream.ptr)
+
+    def block():
+        ln(0); gemm(lin["ff1_l1"], ldD, 1.0, 0.0, lin["ff1_l1"].out.ptr)
+        silu(lin["ff1_l1"]); gemm(lin["ff1_l2"], ldF, 0.5, 1.0, x.ptr)
+        ln(1); gemm(lin["qkv"], ldD, 1.0, 0.0, lin["qkv"].out.ptr)
+        P.concat_heads_quant_rows_dev(H, T, Dh, heads.ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)
+        gemm(lin["out"], ldD, 1.0, 1.0, x.ptr)
+        ln(2); gemm(lin["pw1"], ldD, 1.0, 0.0, lin["pw1"].out.ptr)
+        P.channel_major_quant_rows_dev(D, T, cm.ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)
+        gemm(lin["pw2"], ldD, 1.0, 1.0, x.ptr)
+        ln(3); gemm(lin["ff2_l1"], ldD, 1.0, 0.0, lin["ff2_l1"].out.ptr)
+        silu(lin["ff2_l1"]); gemm(lin["ff2_l2"], ldF, 0.5, 1.0, x.ptr)
+
+    with P.Graph(stream) as gr:
+        block()
+    ms, _ = time_graph(gr, stream, steps, warmup)
+    ops = sum(gemm_ops(T, l.N, l.K) for l in lin.values())
+    return {"ms_per_block": round(ms, 6), "ms_per_30s_window_24_blocks": round(24 * ms, 4),
+            "tops": round(ops / (ms * 1e-3) / 1e12, 2), "kernels_per_block": 16,
+            "what": f"T={T}: 8 producers + 8 five-value GEMMs (int8w), residuals in the epilogues"}
 
 
 def attention_config(stream, H=8, T=375, Dh=128, graph=True, reps=200):
