@@ -131,6 +131,11 @@ size_t p2h_q_bytes(int M, int K); /* bytes of Q for M rows at ldq = p2h_q_ld(K) 
  *                                 QuantA, encoder.c:554-568).
  * The reference's x86 build computes 1/sqrtf and 1/(1 + e) through approximate reciprocals refined by one Newton
  * step, so its LayerNorm and SiLU values differ from these in the last bits and a quantised code, rarely, by one. */
+/* Self-check, no counterpart in the reference: the SiLU producer divides by 1 + e^-x (in [1, 2^126)) with the
+ * hardware reciprocal and one Newton step; this compares that with the IEEE quotient for every float of [1, 2^126)
+ * on the device and returns {mismatches, smallest mismatching bit pattern (or ~0), values checked}. Synchronous. */
+int p2h_recip_selftest(unsigned long long *result3);
+
 int p2h_layer_norm_quant_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta,
                               signed char *dQ, int ldq, float *dScales, void *stream);
 int p2h_silu_quant_rows(int M, int K, const float *dH, int ldh, signed char *dQ, int ldq, float *dScales, void *stream);

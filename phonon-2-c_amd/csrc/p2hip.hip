@@ -522,6 +522,26 @@ int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int 
     return P2H_OK;
 }
 
+/* ── self-checks ────────────────────────────────────────────────────────────────────────────────────────────── */
+
+int p2h_recip_selftest(unsigned long long *result3)
+{
+    if (int rc = ensure_init()) return rc;
+    if (!result3) return fail(P2H_E_ARG, "p2h_recip_selftest: null result");
+    unsigned long long init[3] = {0ull, ~0ull, 0ull}, *d = nullptr;
+    HIPCHK(hipMalloc(&d, sizeof init));
+    hipError_t e = hipMemcpy(d, init, sizeof init, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(p2k::recip_check, dim3(8192), dim3(256), 0, 0, 0x3F800000u, 0x7E800000u, d);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(result3, d, sizeof init, hipMemcpyDeviceToHost);
+    hipFree(d);
+    if (e != hipSuccess) return fail(P2H_E_DEVICE, "p2h_recip_selftest: %s", hipGetErrorString(e));
+    return P2H_OK;
+}
+
 /* ── producers ──────────────────────────────────────────────────────────────────────────────────────────────── */
 
 /* Checks shared by the four producers, then one produce_rows launch over the padded rows [0, roundup(M, 16)). */

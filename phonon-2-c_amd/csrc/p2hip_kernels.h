@@ -212,10 +212,38 @@ __device__ __forceinline__ float exp_p2(float x)
     return __fmul_rn(y, __uint_as_float((uint32_t)((int)kf + 127) << 23));
 }
 
-/* x · sigmoid(x) = x · (1 / (1 + e^{−x})) (swish_range, tensor_ops.c:437-463), no operation contracted */
+/* 1/d correctly rounded for d in [1, 2^126): the hardware reciprocal (within 1 ulp) and one Newton step in fmaf.
+ * recip_check compares it with the IEEE quotient for every float of that range (1,056,964,608 values, none differ on
+ * gfx950; p2h_recip_selftest runs it). */
+__device__ __forceinline__ float recip_ge1(float d)
+{
+    const float r = __builtin_amdgcn_rcpf(d);
+    return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+}
+
+/* x · sigmoid(x) = x · (1 / (1 + e^{−x})) (swish_range, tensor_ops.c:437-463), no operation contracted. exp_p2 clamps
+ * its argument to ±87, so 1 + e^{−x} lies in [1, 0.72·2^126] and recip_ge1 gives the IEEE quotient. */
 __device__ __forceinline__ float silu_p2(float x)
 {
-    return __fmul_rn(x, __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_p2(0.0f - x))));
+    return __fmul_rn(x, recip_ge1(__fadd_rn(1.0f, exp_p2(0.0f - x))));
+}
+
+/* Every float bit pattern b in [lo, hi): out[0] += how many recip_ge1 gets wrong against the IEEE quotient,
+ * out[1] = the smallest such pattern (min), out[2] += how many were checked. */
+__global__ void recip_check(uint32_t lo, uint32_t hi, unsigned long long *out)
+{
+    unsigned long long bad = 0, n = 0;
+    for (uint64_t b = lo + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < hi;
+         b += (uint64_t)gridDim.x * blockDim.x) {
+        const float d = __uint_as_float((uint32_t)b);
+        n++;
+        if (__float_as_uint(recip_ge1(d)) != __float_as_uint(__fdiv_rn(1.0f, d))) {
+            bad++;
+            atomicMin(&out[1], (unsigned long long)b);
+        }
+    }
+    atomicAdd(&out[0], bad);
+    atomicAdd(&out[2], n);
 }
 
 /* One wave per row of the padded row range (WPR = 4: a workgroup of four waves per row, for few long rows), the

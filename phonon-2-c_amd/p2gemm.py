@@ -66,6 +66,7 @@ _HIP_SIG = {
     "p2h_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_q_ld": (_i, [_i]),
     "p2h_layer_norm_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    "p2h_recip_selftest": (_i, [C.POINTER(C.c_ulonglong)]),
     "p2h_silu_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_concat_heads_quant_rows": (_i, [_i, _i, _i, _vp, _vp, _i, _vp, _vp]),
     "p2h_channel_major_quant_rows": (_i, [_i, _i, _vp, _vp, _i, _vp, _vp]),
@@ -340,6 +341,13 @@ class Workspace(DeviceBuffer):
 
 def quant_rows_dev(M, K, dA, lda, dQ, ldq, dS, stream=None):
     _ok(hip().p2h_quant_rows(M, K, dA, lda, dQ, ldq, dS, stream), "p2h_quant_rows")
+
+
+def recip_selftest():
+    """p2h_recip_selftest: (mismatches, smallest mismatching bit pattern or 2^64 - 1, values checked)."""
+    r = (C.c_ulonglong * 3)()
+    _ok(hip().p2h_recip_selftest(r), "p2h_recip_selftest")
+    return int(r[0]), int(r[1]), int(r[2])
 
 
 def layer_norm_quant_rows_dev(M, D, dX, ldx, dGamma, dBeta, dQ, ldq, dS, stream=None):

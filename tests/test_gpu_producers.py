@@ -87,6 +87,14 @@ def test_quant_rows_long_rows(M, K, lda):
     _same((q, s), (qr, sr), M, K)
 
 
+def test_silu_reciprocal_is_the_ieee_quotient_everywhere():
+    """The SiLU producer's 1/(1 + e^-x) (hardware reciprocal + one Newton step) equals the correctly rounded quotient
+    for every float of [1, 2^126), the whole range 1 + e^-x takes after the clamp at ±87."""
+    bad, first, checked = P.recip_selftest()
+    assert checked == 0x7E800000 - 0x3F800000
+    assert bad == 0, f"{bad} differ, first 0x{first:08x}"
+
+
 def test_zero_rows_is_a_no_op():
     q, s = P.silu_quant_rows(np.zeros((0, 64), np.float32))
     assert q.shape[0] == 0 and s.size == 0
