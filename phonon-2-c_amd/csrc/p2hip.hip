@@ -732,7 +732,7 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
         const int cus_ = g_cus > 0 ? g_cus : 256;
         const int sd_tiles = ((M + SmD::BM - 1) / SmD::BM) * ((N + SmD::BN - 1) / SmD::BN);
         cfg = !small_ok(K) ? FV_T
-              : (K <= p2k::kFoldRows && N >= 2048 && M >= 256) ? FV_SW
+              : (K <= p2k::kFoldRows && N >= 3072 && M >= 256) ? FV_SW   /* measured: 32 x 32 wins up to N = 2048 */
               : (K > p2k::kFoldRows && mode == P2H_INT8W && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
               : FV_SS;
     }
