@@ -357,9 +357,11 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
                 for (; b + 2 <= nb; b += 2) {   /* loads are unconditional: batch nb lies in the row's padding */
 #pragma unroll
                     for (int u = 0; u < 4; u++) vb[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 1) + 4 * u);
+                    __builtin_amdgcn_sched_barrier(0);   /* the next batch's reads stay ahead of these additions */
                     p = add16(p, va);
 #pragma unroll
                     for (int u = 0; u < 4; u++) va[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 2) + 4 * u);
+                    __builtin_amdgcn_sched_barrier(0);
                     p = add16(p, vb);
                 }
                 if (b < nb) p = add16(p, va);
