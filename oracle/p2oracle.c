@@ -1,6 +1,6 @@
 /*  p2oracle.c – CPU restatement of phonon-2-c's five-value GEMM (csrc/blas.c), scalar and sequential.
  *
- *  TEST INFRASTRUCTURE ONLY: the checker for the HIP path and nothing else. Only tests/, __graft_entry__.smoke()
+ *  TEST INFRASTRUCTURE ONLY: the reference for the HIP path's results and nothing else. Only tests/, __graft_entry__.smoke()
  *  and bench.py's cpu_baseline leg may load it.
  *
  *  Compiled without fast-math and with -ffp-contract=off: every rounding below is the one written.

@@ -1,7 +1,7 @@
 /*  p2oracle.h – CPU restatement of phonon-2-c's five-value GEMM arithmetic (csrc/blas.c), for checking only.
  *
  *  TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
- *  library, and only as the checker or the CPU baseline; the product never links it.
+ *  library, and only to check results against or as the CPU baseline; the product never links it.
  *
  *  Every function restates one piece of the reference and names the lines it follows. Pinning (what checks each
  *  function against something other than itself) is listed in the header comment of p2oracle.c.

@@ -1,6 +1,6 @@
 """ctypes wrapper over the CPU oracle (oracle/liboracle.so) and the reference build (oracle/_ref/libp2ref.so).
 
-Test infrastructure: the checker for the HIP path. Only tests/, __graft_entry__.smoke() and bench.py's
+Test infrastructure: the reference for the HIP path's results. Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg use it.
 """
 import ctypes as C
