@@ -304,7 +304,7 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE counter readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: the five-value GEMM path has no multi-GPU form in this build "
+        print(f"bench.py runs on one GPU: the five-value GEMM path has no multi-GPU form here "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
 
