@@ -1847,16 +1847,24 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
     const int nseg = (units + su - 1) / su;
     const int u_begin = min(units, wave * su), u_end = min(units, u_begin + su);
 
-    /* per-lane column constants: lo and hi − lo of column n0 + 16·i + l % 16 */
-    float wlo[FN], wd[FN];
+    /* Every weight of column n is one of eight values, w = (code − 1)·fmaf(flag, hi − lo, lo) for the 4-bit
+     * selector code | flag << 2: built once per tile into LDS (rows of 9 floats, so the 16 columns a wave reads
+     * spread over the banks), then one extract and one LDS read per weight. */
+    __shared__ float wtab[BN * 9];
+    for (int c = tid; c < BN * 8; c += 256) {
+        const int col = c >> 3, sel = c & 7, n = min(n0 + col, N - 1);
+        const float lo = g.lo[n], d = g.hi[n] - lo;
+        wtab[col * 9 + sel] = (float)((sel & 3) - 1) * __builtin_fmaf((float)(sel >> 2), d, lo);
+    }
+    int tcol[FN];
     const uint8_t *b_base[FN];
 #pragma unroll
     for (int i = 0; i < FN; i++) {
         const int n = min(n0 + 16 * i + (lane & 15), N - 1);
-        wlo[i] = g.lo[n];
-        wd[i] = g.hi[n] - wlo[i];
+        tcol[i] = (16 * i + (lane & 15)) * 9;
         b_base[i] = g.rec + (size_t)(n >> 4) * units * 1024 + lane * 16;
     }
+    __syncthreads();
     const float *a_row[FM];
 #pragma unroll
     for (int j = 0; j < FM; j++) a_row[j] = g.A + (size_t)min(m0 + 16 * j + (lane & 15), M - 1) * g.lda;
@@ -1898,11 +1906,8 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
                 const int d = t >> 2, b = t & 3;
                 float w[FN];
 #pragma unroll
-                for (int i = 0; i < FN; i++) {
-                    const uint32_t nib = r[buf][i][2 * s + (d >> 1)] >> (8 * b + 4 * (d & 1));
-                    const float mag = __builtin_fmaf((float)((nib >> 2) & 1u), wd[i], wlo[i]);
-                    w[i] = (float)((int)(nib & 3u) - 1) * mag;
-                }
+                for (int i = 0; i < FN; i++)
+                    w[i] = wtab[tcol[i] + ((r[buf][i][2 * s + (d >> 1)] >> (8 * b + 4 * (d & 1))) & 7u)];
 #pragma unroll
                 for (int j = 0; j < FM; j++)
 #pragma unroll
