@@ -73,6 +73,17 @@ def test_silu_against_float64():
     assert (np.abs(got - ref) <= 4e-6 * np.abs(ref) + 1e-30).all()
 
 
+def test_silu_tail_against_float64():
+    """Rows whose length is not a multiple of eight: the last len % 8 values take p2_sigmoid's expf route."""
+    rng = _rng(13)
+    X = (rng.standard_normal((4, 1027)) * 4).astype(np.float32)
+    got = O.swish_rows(X).astype(np.float64)
+    ref = _silu64(X)
+    assert (np.abs(got - ref) <= 4e-6 * np.abs(ref) + 1e-30).all()
+    tail = np.abs(got[:, 1024:] - ref[:, 1024:]) <= 2e-7 * np.abs(ref[:, 1024:]) + 1e-30   # libm expf: < 1 ulp
+    assert tail.all()
+
+
 def test_silu_special_values():
     X = np.array([[0.0, 100.0, 87.0, 30.0, -100.0, -87.5, -1e-30, 1e-30]], np.float32)
     got = O.swish_rows(X)[0]
