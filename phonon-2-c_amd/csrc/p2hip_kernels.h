@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void quant_rows(int M, int Mp, int K, const fl
                                                   int8_t *__restrict__ Q, int ldq, float *__restrict__ scales)
 {
     const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);   /* four rows per 256-thread workgroup */
     if (m >= Mp) return;
     const int kst = ldq / 64, k16 = K / 16 * 16;
     if (m >= M) {
@@ -1490,13 +1490,27 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
         a_base[j] = g.Q + (size_t)mg * g.kst * 1024 + lane * 16;
     }
     const uint8_t *b_base[FN];
-    uint32_t lo_tab[FN];
+    uint32_t clo[FN];   /* the columns' lo codes; their decode tables are built once the operand loads are issued */
 #pragma unroll
     for (int i = 0; i < FN; i++) {
         const int cg = min((n0 >> 4) + i, g.ng_last);
         b_base[i] = g.rec + (size_t)cg * units * (G::REC4 ? 1024 : 768) + lane * (G::REC4 ? 16 : 12);
-        lo_tab[i] = MODE == MODE_INT8W ? i8w_lo_table(g.clo[16 * cg + (lane & 15)]) : 0u;
+        clo[i] = MODE == MODE_INT8W ? g.clo[16 * cg + (lane & 15)] : 0u;
     }
+
+    /* fold geometry: thread t owns rows t / (BN / 4) + RPP·p and four consecutive columns 4·(t % (BN / 4)). Its
+     * epilogue factors are read here, ahead of the operands, so that their latency overlaps the operand loads'
+     * instead of following the barrier (addresses clamped; the fold skips what lies outside C). */
+    constexpr int TPR = BN / 4;                  /* threads per output row */
+    constexpr int RPP = G::NT / TPR;             /* rows per pass */
+    constexpr int PASSES = (BM + RPP - 1) / RPP;
+    const int cq = tid % TPR, n = n0 + 4 * cq, r0 = tid / TPR;
+    const v4f c1 = *reinterpret_cast<const v4f *>(g.c1 + min(n, N - 4));
+    v4f c2 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (TWO) c2 = *reinterpret_cast<const v4f *>(g.c2 + min(n, N - 4));
+    float row_scale[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) row_scale[p] = g.a_scales[min(m0 + r0 + RPP * p, M - 1)];
 
     v4i a[2][CH][2][FM];
     uint32_t r[2][CH][FN][4];
@@ -1522,7 +1536,10 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
         }
     };
 
-    for (int seg = wave; seg < nseg; seg += G::WAVES) {
+    /* one K segment per wave at most (K <= 4096), so no loop: a loop here makes the compiler wait for every load
+     * above before it, the lo codes and the epilogue factors included */
+    if (wave < nseg) {
+        const int seg = wave;
         const int u_begin = seg * seg_units, u_end = min(units, u_begin + seg_units);
         v4i acc[FN][FM], accT[TWO ? FN : 1][TWO ? FM : 1];
 #pragma unroll
@@ -1534,6 +1551,10 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
             }
         /* batches of CH units, the next batch loading while the current one is multiplied (at most 8 units) */
         load_batch(0, u_begin, min(CH, u_end - u_begin));
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t lo_tab[FN];
+#pragma unroll
+        for (int i = 0; i < FN; i++) lo_tab[i] = MODE == MODE_INT8W ? i8w_lo_table(clo[i]) : 0u;
 #pragma unroll
         for (int b = 0; b < 8 / CH; b++) {
             const int u0 = u_begin + b * CH;
@@ -1556,21 +1577,16 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     }
     __syncthreads();
 
-    /* fold: thread t owns rows t / (BN / 4) + 256 / (BN / 4)·q and four consecutive columns 4·(t % (BN / 4)) */
-    constexpr int TPR = BN / 4;                  /* threads per output row */
-    constexpr int RPP = G::NT / TPR;             /* rows per pass */
-    const int cq = tid % TPR, n = n0 + 4 * cq;
+    /* fold */
     if (n >= N) return;
-    v4f c1 = *reinterpret_cast<const v4f *>(g.c1 + n);
-    v4f c2 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if (TWO) c2 = *reinterpret_cast<const v4f *>(g.c2 + n);
     const bool beta_zero = g.beta == 0.0f;
     const int nblocks = (units + 7) / 8;
     const int spb = units <= 8 ? nseg : 8 / seg_units;   /* segments per fold block */
-    for (int row = tid / TPR; row < BM; row += RPP) {
-        const int m = m0 + row;
-        if (m >= M) break;
-        const float as = g.a_scales[m] * g.alpha;
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int row = r0 + RPP * p, m = m0 + row;
+        if (row >= BM || m >= M) break;
+        const float as = row_scale[p] * g.alpha;
         float *cp = g.C + (size_t)m * g.ldc + n;
         float run[4];
         if (!beta_zero) {
