@@ -929,6 +929,14 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
     hipStream_t s = stream_of(stream);
     if (M == 0 || groups == 0) return P2H_OK;
     Plan p = make_plan(mode, M, N, K, false);
+    /* the launch covers groups · N columns of the same rows: its tile follows the single-call rule at that width
+     * (measured, 24 weights of 1024 × 1024 at M = 749: 56.5 µs with 48 × 64 tiles against 63 µs with 32 × 32) */
+    if (is_small(p.cfg) && mode == P2H_INT8W &&
+        make_plan(mode, M, (int)std::min<long long>((long long)N * groups, 1 << 30), K, false).cfg == FV_SW) {
+        p.cfg = FV_SW;
+        p.tiles_m = (M + SmW::BM - 1) / SmW::BM;
+        p.tiles_n = (N + SmW::BN - 1) / SmW::BN;
+    }
     if (alpha == 0.0f || K == 0 || !is_small(p.cfg)) {   /* one call per weight: the same kernels, unsplit */
         for (int q = 0; q < groups; q++)
             if (int rc = p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, ldq, dScales, w[q], beta, dC[q], ldc, nullptr, 0,
