@@ -931,13 +931,16 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
     Plan p = make_plan(mode, M, N, K, false);
     /* the launch covers groups · N columns of the same rows: its tile follows the single-call rule at that width
      * (measured, 24 weights of 1024 × 1024 at M = 749: 56.5 µs with 48 × 64 tiles against 63 µs with 32 × 32) */
+    bool wide = false;   /* the large-M kernel's 96 × 256 tiles, where they number at least one per CU */
     if (is_small(p.cfg) && mode == P2H_INT8W &&
         make_plan(mode, M, (int)std::min<long long>((long long)N * groups, 1 << 30), K, false).cfg == FV_SW) {
-        p.cfg = FV_SW;
-        p.tiles_m = (M + SmW::BM - 1) / SmW::BM;
-        p.tiles_n = (N + SmW::BN - 1) / SmW::BN;
+        const long long w6_tiles = (long long)((M + FvW6::BM - 1) / FvW6::BM) * ((N + FvW6::BN - 1) / FvW6::BN) * groups;
+        wide = M >= 512 && w6_tiles >= (g_cus > 0 ? g_cus : 256) && env_int("P2H_TILE", -1) < 0;
+        p.cfg = wide ? FV_W6 : FV_SW;
+        p.tiles_m = wide ? (M + FvW6::BM - 1) / FvW6::BM : (M + SmW::BM - 1) / SmW::BM;
+        p.tiles_n = wide ? (N + FvW6::BN - 1) / FvW6::BN : (N + SmW::BN - 1) / SmW::BN;
     }
-    if (alpha == 0.0f || K == 0 || !is_small(p.cfg)) {   /* one call per weight: the same kernels, unsplit */
+    if (alpha == 0.0f || K == 0 || (!is_small(p.cfg) && !wide)) {   /* one call per weight: the same kernels, unsplit */
         for (int q = 0; q < groups; q++)
             if (int rc = p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, ldq, dScales, w[q], beta, dC[q], ldc, nullptr, 0,
                                           stream))
@@ -960,7 +963,9 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
     }
     g.units = w[0]->units;
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n), (unsigned)groups), block(256);
-    if (mode == P2H_INT8)
+    if (wide)
+        hipLaunchKernelGGL((p2k::gemm_fv_grouped<FvW6, false>), grid, dim3(FvW6::NT), 0, s, g, ga);
+    else if (mode == P2H_INT8)
         hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8>), grid, block, 0, s, g, ga);
     else if (p.cfg == FV_SW)
         hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmW, p2k::MODE_INT8W>), grid, block, 0, s, g, ga);

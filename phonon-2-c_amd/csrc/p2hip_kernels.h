@@ -1074,8 +1074,8 @@ __device__ __forceinline__ void lds_barrier()
  *  Operands stream through a ring of D LDS stages (two 64-row steps each) by direct global→LDS loads: stage t + D − 1
  *  is requested while stage t is computed, with one barrier per stage and no register staging.
  *  Folding into fp32 is as in gemm_i8: per 1024-row block in registers, or int32 partials per split for fold_splits. */
-template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC = 1, bool REC4 = false, bool CSHUF = false>
-__global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC, bool REC4, bool CSHUF>
+__device__ __forceinline__ void fv_tile(const GemmArgs &g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
     constexpr bool FOLD = OUT == OUT_F32 && !SPLIT;
@@ -1394,6 +1394,12 @@ __global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
     }
 }
 
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC = 1, bool REC4 = false, bool CSHUF = false>
+__global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
+{
+    fv_tile<G, MODE, OUT, MULTI, SPLIT, OCC, REC4, CSHUF>(g);
+}
+
 /* ── the small-M five-value GEMM ─────────────────────────────────────────────────────────────────────────────── */
 
 /* Small-M tile: a workgroup of W waves (four, or sixteen for long K) owns one BM × BN output tile (BM = 16·FM
@@ -1650,6 +1656,16 @@ __global__ __launch_bounds__(256, 2) void gemm_fvs_grouped(GemmArgs g, GroupArgs
     const int q = blockIdx.y;
     h.rec = ga.rec[q]; h.clo = ga.clo[q]; h.c1 = ga.c1[q]; h.c2 = ga.c2[q]; h.C = ga.C[q];
     fvs_tile<G, MODE>(h);
+}
+
+/* The same for the large-M kernel's tiles (int8w, 4-bit records, one split; blockIdx.x is the tile as in gemm_fv). */
+template <class G, bool MULTI>
+__global__ __launch_bounds__(G::NT, 2) void gemm_fv_grouped(GemmArgs g, GroupArgs ga)
+{
+    GemmArgs h = g;
+    const int q = blockIdx.y;
+    h.rec = ga.rec[q]; h.clo = ga.clo[q]; h.c1 = ga.c1[q]; h.c2 = ga.c2[q]; h.C = ga.C[q];
+    fv_tile<G, MODE_INT8W, OUT_F32, MULTI, false, 2, true, true>(h);
 }
 
 /* The fold after a split GEMM: per output, the int32 partial sums of the splits inside each 1024-row block are

@@ -288,9 +288,11 @@ def test_sgemm_batched_every_load_route(monkeypatch, tA, tB, shape, loads):
 
 @pytest.mark.parametrize("mode", ["int8w", "int8"])
 @pytest.mark.parametrize("M,K,N,groups,beta", [(749, 1024, 1024, 24, 0.0), (375, 1024, 4096, 3, 1.0),
-                                               (38, 4096, 1024, 5, 0.5), (2000, 1024, 256, 2, 0.0)])
+                                               (38, 4096, 1024, 5, 0.5), (2000, 1024, 256, 2, 0.0),
+                                               (600, 1024, 272, 20, 0.5)])
 def test_grouped_q8a(mode, M, K, N, groups, beta):
-    """Each group's output equals its own p2h_fvb_gemm_q8a call bit for bit (2000 rows: the per-weight path)."""
+    """Each group's output equals its own p2h_fvb_gemm_q8a call bit for bit (2000 rows: the per-weight path; int8w at
+    749 × 24 · 1024 and 600 × 20 · 272: the large-M kernel's tiles, ragged in both dimensions for the latter)."""
     A = P.gen_activations(SEED, 1500 + M, M, K)
     q, sc = O.quant_rows(A)
     ws = [P.FvWeight(*_weight(K, N, 1600 + i), K, N) for i in range(groups)]
