@@ -69,13 +69,13 @@ class Scratch:
         self.ws = P.Workspace(split_bytes)
 
 
-def run_linear(lin, dA, lda, ws, stream, alpha=None):
-    """Quantise A, then the q8a GEMM."""
+def run_linear(lin, dA, lda, ws, stream, alpha=None, next_w=None):
+    """Quantise A, then the q8a GEMM (which reads the records of next_w, the chain's next weight, ahead)."""
     a = lin.alpha if alpha is None else alpha
     ldq = P.q_ld(lin.K)   # the linear's own row pitch: the shared buffer is sized for the widest
     P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr)
-    P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, a, ws.q.ptr, ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr,
-                       lin.N, ws.ws.ptr, ws.ws.nbytes, stream.ptr)
+    P.fvb_gemm_q8a_next_dev("int8w", lin.M, lin.N, lin.K, a, ws.q.ptr, ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr,
+                            lin.N, ws.ws.ptr, ws.ws.nbytes, next_w, stream.ptr)
 
 
 def time_graph(graph, stream, steps, warmup):
@@ -118,16 +118,18 @@ def time_launches(launch, stream, reps):
 
 
 def kernel_times(linears, inputs, ws, stream, reps):
-    """Duration (ms) of each linear's quantise and GEMM kernels, each timed on its own by time_launches."""
+    """Duration (ms) of each linear's quantise and GEMM kernels, each timed on its own by time_launches (the GEMM
+    as the chain calls it, reading the next linear's records ahead)."""
     q = np.zeros(len(linears))
     t = np.zeros(len(linears))
     for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
         ldq = P.q_ld(lin.K)
+        nxt = linears[(i + 1) % len(linears)].w
         q[i] = time_launches(lambda: P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr),
                              stream, reps)
-        t[i] = time_launches(lambda: P.fvb_gemm_q8a_dev("int8w", lin.M, lin.N, lin.K, lin.alpha, ws.q.ptr, ldq,
-                                                        ws.s.ptr, lin.w, 0.0, lin.out.ptr, lin.N, ws.ws.ptr,
-                                                        ws.ws.nbytes, stream.ptr),
+        t[i] = time_launches(lambda: P.fvb_gemm_q8a_next_dev("int8w", lin.M, lin.N, lin.K, lin.alpha, ws.q.ptr, ldq,
+                                                             ws.s.ptr, lin.w, 0.0, lin.out.ptr, lin.N, ws.ws.ptr,
+                                                             ws.ws.nbytes, nxt, stream.ptr),
                              stream, reps)
     stream.sync()
     return q, t
@@ -204,9 +206,9 @@ def measure_chain(spec, stream, steps, warmup, kreps):
             P.fvb_gemm_q8a_grouped_dev("int8w", P0.M, P0.N, P0.K, 1.0, pq.ptr, P.q_ld(P0.K), ps.ptr,   # alpha 1: encoder.c:500
                                        [linears[i].w for i in pos], 0.0, [linears[i].out.ptr for i in pos], P0.N,
                                        stream.ptr)
-        for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
-            if i not in pos:
-                run_linear(lin, dA, lda, ws, stream)
+        order = [i for i in range(len(linears)) if i not in pos]
+        for x, i in enumerate(order):   # each GEMM reads the next one's records ahead (the last, the first's)
+            run_linear(linears[i], *inputs[i], ws, stream, next_w=linears[order[(x + 1) % len(order)]].w)
     ms, wall = time_graph(graph, stream, steps, warmup)
     if kreps > 0:
         qt, gt = kernel_times(linears, inputs, ws, stream, kreps)
@@ -486,11 +488,11 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=Tru
     ldD, ldF = P.q_ld(D), P.q_ld(FF)
     steps_fns = (
         lambda: P.layer_norm_quant_rows_dev(M, D, x.ptr, D, g.ptr, b.ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr),
-        lambda: P.fvb_gemm_q8a_dev("int8w", M, FF, D, 1.0, ws.q.ptr, ldD, ws.s.ptr, l1.w, 0.0, l1.out.ptr, FF,
-                                   ws.ws.ptr, ws.ws.nbytes, stream.ptr),
+        lambda: P.fvb_gemm_q8a_next_dev("int8w", M, FF, D, 1.0, ws.q.ptr, ldD, ws.s.ptr, l1.w, 0.0, l1.out.ptr, FF,
+                                        ws.ws.ptr, ws.ws.nbytes, l2.w, stream.ptr),
         lambda: P.silu_quant_rows_dev(M, FF, l1.out.ptr, FF, ws.q.ptr, ldF, ws.s.ptr, stream.ptr),
-        lambda: P.fvb_gemm_q8a_dev("int8w", M, D, FF, 0.5, ws.q.ptr, ldF, ws.s.ptr, l2.w, 1.0, x.ptr, D,
-                                   ws.ws.ptr, ws.ws.nbytes, stream.ptr),
+        lambda: P.fvb_gemm_q8a_next_dev("int8w", M, D, FF, 0.5, ws.q.ptr, ldF, ws.s.ptr, l2.w, 1.0, x.ptr, D,
+                                        ws.ws.ptr, ws.ws.nbytes, l1.w, stream.ptr),
     )
     ms = None
     if graph:
@@ -551,9 +553,13 @@ def block_config(stream, T=375, steps=500, warmup=50):
     ws = Scratch(T, FF, split)
     ldD, ldF = P.q_ld(D), P.q_ld(FF)
 
-    def gemm(l, ldq, alpha, beta, out):
-        P.fvb_gemm_q8a_dev("int8w", T, l.N, l.K, alpha, ws.q.ptr, ldq, ws.s.ptr, l.w, beta, out, l.N,
-                           ws.ws.ptr, ws.ws.nbytes, stream.ptr)
+    seq = ["ff1_l1", "ff1_l2", "qkv", "out", "pw1", "pw2", "ff2_l1", "ff2_l2"]   # the block's order of GEMMs
+
+    def gemm(l, ldq, alpha, beta, out):   # reads the records of the block's next GEMM (the last, the first's) ahead
+        name = next(k for k, v in lin.items() if v is l)
+        nxt = lin[seq[(seq.index(name) + 1) % len(seq)]].w
+        P.fvb_gemm_q8a_next_dev("int8w", T, l.N, l.K, alpha, ws.q.ptr, ldq, ws.s.ptr, l.w, beta, out, l.N,
+                                ws.ws.ptr, ws.ws.nbytes, nxt, stream.ptr)
 
     def ln(i):
         P.layer_norm_quant_rows_dev(T, D, x.ptr, D, gb[i][0].ptr, gb[i][1].ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)

@@ -151,6 +151,15 @@ int p2h_channel_major_quant_rows(int D, int T, const float *dDW, signed char *dQ
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                      const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/* p2h_fvb_gemm_q8a with the weight the caller multiplies next: while this product runs, its workgroups also read
+ * the operand records that product will read (for the same M) into the memory-side cache, so its first loads do
+ * not wait on HBM. Results are those of p2h_fvb_gemm_q8a; `next` may be NULL. No counterpart in the reference:
+ * for callers that run a known sequence of linears (an encoder's 216 per window). Only the small-M tiles
+ * (M <= 1024) read ahead. */
+int p2h_fvb_gemm_q8a_next(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                          const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
+                          size_t workspace_bytes, const P2hWeight *next, void *stream);
 /* The same product for `groups` (<= 32) weights of one shape [K, N] against the same quantised rows, C_q = alpha·A·W_q
  * + beta·C_q, in one launch where the small-M kernel serves the shape (M <= 1024, K <= 4096), otherwise one call per
  * weight; results are those of p2h_fvb_gemm_q8a per weight. No counterpart in the reference: it batches products

@@ -878,9 +878,29 @@ size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K)
     return p.part_bytes;   /* the split partials, or 0 when the call would not split */
 }
 
+static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                        const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
+                        size_t workspace_bytes, const P2hWeight *next, void *stream);
+
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                      const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
                      size_t workspace_bytes, void *stream)
+{
+    return fvb_gemm_q8a(mode, M, N, K, alpha, dQ, ldq, dScales, w, beta, dC, ldc, workspace, workspace_bytes,
+                        nullptr, stream);
+}
+
+int p2h_fvb_gemm_q8a_next(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                          const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
+                          size_t workspace_bytes, const P2hWeight *next, void *stream)
+{
+    return fvb_gemm_q8a(mode, M, N, K, alpha, dQ, ldq, dScales, w, beta, dC, ldc, workspace, workspace_bytes, next,
+                        stream);
+}
+
+static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                        const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
+                        size_t workspace_bytes, const P2hWeight *next, void *stream)
 {
     if (int rc = ensure_init()) return rc;
     if (mode != P2H_INT8W && mode != P2H_INT8)
@@ -899,6 +919,13 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
     g.rec = uses_rec4(p.cfg) ? w->rec4 : w->rec;
     g.units = w->units; g.clo = w->clo;
+    if (next && is_small(p.cfg)) {   /* the records the next call reads if it has this M */
+        const Plan pn = make_plan(mode, M, next->N, next->K, true);
+        const bool r4 = uses_rec4(pn.cfg);
+        const size_t bytes = (size_t)(next->N / 16) * next->units * (r4 ? 1024 : 768);
+        g.warm = r4 ? next->rec4 : next->rec;
+        g.warm_lines = (int)std::min<size_t>((bytes + 127) / 128, 0x7fffffff);
+    }
     if (mode == P2H_INT8W) {
         g.c1 = w->c1w;
         launch_fv_cfg<p2k::MODE_INT8W>(g, p, s);

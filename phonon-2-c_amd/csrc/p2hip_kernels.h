@@ -490,6 +490,7 @@ struct GemmArgs {
     int units;                                            /* 128-row K units of the records: K rounded up / 128 */
     int kst;                                              /* 64-column steps per 16-row group of Q: ldq / 64 */
     int mg_last, ng_last;                                 /* last 16-row group of Q, last 16-column group of C */
+    const uint8_t *warm; int warm_lines;                  /* 128-byte lines a later kernel reads, loaded meanwhile */
 };
 
 
@@ -1485,6 +1486,15 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
     const int n0 = tile_n * BN, m0 = tile_m * BM;
     const int M = g.M, N = g.N, units = g.units;
+    /* one 128-byte line per thread of the range a later kernel reads (the records of the caller's next weight),
+     * requested before this tile's own loads, so that waiting for those (the vector-memory counter retires in
+     * order) never waits behind it; the value is consumed as the wave ends */
+    uint32_t warm = 0;
+    if (g.warm) {
+        const int t = blockIdx.x * G::NT + tid;
+        if (t < g.warm_lines) warm = *reinterpret_cast<const uint32_t *>(g.warm + (size_t)t * 128);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const int seg_units = sm_seg_units(units, G::WAVES);
     const int nseg = (units + seg_units - 1) / seg_units;
 
@@ -1584,6 +1594,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     __syncthreads();
 
     /* fold */
+    asm volatile("" ::"v"(warm));
     if (n >= N) return;
     const bool beta_zero = g.beta == 0.0f;
     const int nblocks = (units + 7) / 8;

@@ -72,6 +72,7 @@ _HIP_SIG = {
     "p2h_channel_major_quant_rows": (_i, [_i, _i, _vp, _vp, _i, _vp, _vp]),
     "p2h_q_bytes": (C.c_size_t, [_i, _i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
+    "p2h_fvb_gemm_q8a_next": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp, _vp]),
     "p2h_fvb_gemm_q8a_grouped": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _f, _vp, _i, _vp]),
     "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_plan": (C.c_char_p, [_i, _i, _i, _i, _i]),
@@ -370,6 +371,14 @@ def channel_major_quant_rows_dev(D, T, dDW, dQ, ldq, dS, stream=None):
 def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=None, ws_bytes=0, stream=None):
     _ok(hip().p2h_fvb_gemm_q8a(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, ws,
                                ws_bytes, stream), "p2h_fvb_gemm_q8a")
+
+
+def fvb_gemm_q8a_next_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=None, ws_bytes=0, next_w=None,
+                          stream=None):
+    """fvb_gemm_q8a_dev that also reads the records of `next_w` (the next weight the caller runs) ahead."""
+    _ok(hip().p2h_fvb_gemm_q8a_next(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, beta, dC, ldc, ws,
+                                    ws_bytes, next_w.ptr if next_w is not None else None, stream),
+        "p2h_fvb_gemm_q8a_next")
 
 
 def fvb_gemm_q8a_grouped_dev(mode, M, N, K, alpha, dQ, ldq, dS, weights, beta, dCs, ldc, stream=None):

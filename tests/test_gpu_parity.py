@@ -284,6 +284,31 @@ def test_sgemm_batched_every_load_route(monkeypatch, tA, tB, shape, loads):
     _assert_exact(got.reshape(-1, N), ref.reshape(-1, N))
 
 
+# ── reading the next weight's records ahead ───────────────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+@pytest.mark.parametrize("M,K,N,Kn,Nn,beta", [(375, 1024, 4096, 4096, 1024, 0.0), (375, 4096, 1024, 1024, 3072, 1.0),
+                                              (38, 1024, 1024, 4096, 1024, 0.5), (2000, 1024, 1024, 1024, 4096, 0.0),
+                                              (200, 1024, 272, 0, 0, 0.0)])
+def test_q8a_next_matches_q8a(mode, M, K, N, Kn, Nn, beta):
+    """p2h_fvb_gemm_q8a_next gives p2h_fvb_gemm_q8a's outputs bit for bit: with a next weight of another shape, with
+    none (Kn = 0), at 2000 rows (the large-M kernel, which reads nothing ahead), and twice in a row (the second
+    call's first loads find the records the first read ahead)."""
+    A = P.gen_activations(SEED, 1800 + M, M, K)
+    q, sc = O.quant_rows(A)
+    w = P.FvWeight(*_weight(K, N, 1810), K, N)
+    nxt = P.FvWeight(*_weight(Kn, Nn, 1811), Kn, Nn) if Kn else None
+    C0 = P.gen_activations(SEED, 1820 + N, M, N)
+    ldq = P.q_ld(K)
+    dQ, dS = P.to_device(P.q_tile(q, ldq)), P.to_device(sc)
+    ws = P.Workspace(P.q8a_workspace_bytes(mode, M, N, K))
+    single = P.fvb_gemm_q8a(mode, q, sc, w, alpha=0.8, beta=beta, C0=C0)
+    for rep in range(2):
+        dC = P.to_device(C0)
+        P.fvb_gemm_q8a_next_dev(mode, M, N, K, 0.8, dQ.ptr, ldq, dS.ptr, w, beta, dC.ptr, N, ws.ptr, ws.nbytes, nxt)
+        assert _bits_equal(dC.download((M, N), np.float32), single), f"call {rep}"
+
+
 # ── several weights against the same quantised rows in one launch ─────────────────────────────────────────────────
 
 @pytest.mark.parametrize("mode", ["int8w", "int8"])
