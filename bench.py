@@ -93,6 +93,42 @@ def time_graph(graph, stream, steps, warmup):
     return e0.elapsed_ms(e1) / steps, wall
 
 
+STEPS_PER_REPLAY = 10   # short chains: steps captured per graph (a window's graph holds all its linears)
+
+
+class StepGraphs:
+    """One step's launches (`body`) captured `per` times into one graph, and `steps % per` times into a second, so
+    that timing exactly `steps` steps replays whole graphs. Launching a graph costs about 6.5 us of submission on
+    its own (four-kernel FFN step: 30.0 us at one step per replay, 23.5 us at ten, MI355X); a caller that runs a
+    window's linears from one graph pays it once per window, not once per linear pair."""
+
+    def __init__(self, stream, body, per, steps):
+        self.stream, self.per, self.rest = stream, max(1, per), steps % max(1, per)
+        self.full = self._capture(body, self.per)
+        self.part = self._capture(body, self.rest) if self.rest else None
+
+    def _capture(self, body, n):
+        with P.Graph(self.stream) as g:
+            for _ in range(n):
+                body()
+        return g
+
+    def time(self, steps, warmup):
+        for _ in range(-(-warmup // self.per)):
+            self.full.launch()
+        self.stream.sync()
+        e0, e1 = P.Event(), P.Event()
+        e0.record(self.stream.ptr)
+        t0 = time.perf_counter()
+        for _ in range(steps // self.per):
+            self.full.launch()
+        if self.rest:
+            self.part.launch()
+        e1.record(self.stream.ptr)
+        e1.sync()
+        return e0.elapsed_ms(e1) / steps, time.perf_counter() - t0
+
+
 def time_launches(launch, stream, reps):
     """Average duration (ms) of one kernel launched `reps` times on `stream` behind a stream hold, between two HIP
     events: the hold keeps the GPU busy while the host queues the launches, so they run back to back and the
@@ -188,10 +224,11 @@ def sweep_spec(M=375):
     return spec
 
 
-def measure_chain(spec, stream, steps, warmup, kreps):
-    """Capture the chain into one graph on one stream and time its replays; then, when kreps > 0, time each kernel
-    on its own. (A parallel graph branch for the positional projections, whose input is the positional table
-    rather than an earlier linear's output, measured slower on MI355X than the single chain.)"""
+def measure_chain(spec, stream, steps, warmup, kreps, per=1):
+    """Capture the chain into a graph on one stream (`per` steps per graph) and time exactly `steps` steps; then,
+    when kreps > 0, time each kernel on its own. (A parallel graph branch for the positional projections, whose
+    input is the positional table rather than an earlier linear's output, measured slower on MI355X than the
+    single chain.)"""
     linears, inputs, ws, keep = build_chain(spec, None)
     pos = [i for i, sp in enumerate(spec) if sp[4] == "pos"]
     if pos:
@@ -199,7 +236,7 @@ def measure_chain(spec, stream, steps, warmup, kreps):
         pq = P.DeviceBuffer(P.q_bytes(P0.M, P0.K))
         ps = P.DeviceBuffer(4 * P0.M)
         keep["pos_q"] = (pq, ps)
-    with P.Graph(stream) as graph:
+    def body():
         if pos:   # the positional rows quantised once, every block's projection in one launch
             P.quant_rows_dev(P0.M, P0.K, inputs[pos[0]][0], inputs[pos[0]][1], pq.ptr, P.q_ld(P0.K), ps.ptr,
                              stream.ptr)
@@ -209,7 +246,7 @@ def measure_chain(spec, stream, steps, warmup, kreps):
         order = [i for i in range(len(linears)) if i not in pos]
         for x, i in enumerate(order):   # each GEMM reads the next one's records ahead (the last, the first's)
             run_linear(linears[i], *inputs[i], ws, stream, next_w=linears[order[(x + 1) % len(order)]].w)
-    ms, wall = time_graph(graph, stream, steps, warmup)
+    ms, wall = StepGraphs(stream, body, per, steps).time(steps, warmup)
     if kreps > 0:
         qt, gt = kernel_times(linears, inputs, ws, stream, kreps)
     else:
@@ -325,7 +362,8 @@ def main():
     results = {}
 
     def run(name, spec, steps, warmup, kreps):
-        lins, ms, wall, qt, gt = measure_chain(spec, stream, steps, warmup, kreps)
+        per = STEPS_PER_REPLAY if len(spec) <= 4 else 1   # a window's chain is one graph already
+        lins, ms, wall, qt, gt = measure_chain(spec, stream, steps, warmup, kreps, per)
         r = summarize(lins, ms, qt, gt)
         r["wall_s"] = round(wall, 3)
         results[name] = (lins, r)
@@ -391,7 +429,8 @@ def main():
                                 "m6000": "FFN pair M=6000: 1024->4096 then 4096->1024, int8w",
                                 "m38": "FFN pair M=38: 1024->4096 then 4096->1024, int8w",
                                 "sweep": "216 encoder linears of one 30 s window (M=375, pos M=749), int8w"}[main_wl],
-                   "M": lins[0].M, "gemm_ops_per_step": ops, "graph": True},
+                   "M": lins[0].M, "gemm_ops_per_step": ops,
+                   "graph": {"steps_per_replay": STEPS_PER_REPLAY if len(lins) <= 4 else 1}},
         "pct_int8_peak": round(r["pct_int8_peak"], 3),
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -428,11 +467,12 @@ def exact_config(stream):
         if chain:
             os.environ["P2H_EXACT_CHAIN"] = "1"
         try:
-            with P.Graph(stream) as g:
-                P.fvb_gemm_dev("exact", M, N, K, 1.0, dA.ptr, K, w, 0.0, dC.ptr, N, None, 0, stream.ptr)
+            sg = StepGraphs(stream, lambda: P.fvb_gemm_dev("exact", M, N, K, 1.0, dA.ptr, K, w, 0.0, dC.ptr, N, None,
+                                                           0, stream.ptr), STEPS_PER_REPLAY, reps)
         finally:
             os.environ.pop("P2H_EXACT_CHAIN", None)
-        ms, _ = time_graph(g, stream, reps, 3)
+        ms, _ = sg.time(reps, 3)
+        del sg
         tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
         out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2), "pct_fp32_peak": round(100 * tf / PEAK_FP32_TFLOPS, 2)}
     return out
@@ -496,10 +536,10 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=Tru
     )
     ms = None
     if graph:
-        with P.Graph(stream) as gr:
+        def body():
             for fn in steps_fns:
                 fn()
-        ms, _ = time_graph(gr, stream, steps, warmup)
+        ms, _ = StepGraphs(stream, body, STEPS_PER_REPLAY, steps).time(steps, warmup)
     kt = [round(time_launches(fn, stream, reps), 5) for fn in steps_fns] if reps > 0 else None
     ops = gemm_ops(M, FF, D) + gemm_ops(M, D, FF)
     return {"ms_per_step": round(ms, 6) if ms else None, "tops": round(ops / (ms * 1e-3) / 1e12, 2) if ms else None,
@@ -579,9 +619,7 @@ def block_config(stream, T=375, steps=500, warmup=50):
         ln(3); gemm(lin["ff2_l1"], ldD, 1.0, 0.0, lin["ff2_l1"].out.ptr)
         silu(lin["ff2_l1"]); gemm(lin["ff2_l2"], ldF, 0.5, 1.0, x.ptr)
 
-    with P.Graph(stream) as gr:
-        block()
-    ms, _ = time_graph(gr, stream, steps, warmup)
+    ms, _ = StepGraphs(stream, block, STEPS_PER_REPLAY, steps).time(steps, warmup)
     ops = sum(gemm_ops(T, l.N, l.K) for l in lin.values())
     return {"ms_per_block": round(ms, 6), "ms_per_30s_window_24_blocks": round(24 * ms, 4),
             "tops": round(ops / (ms * 1e-3) / 1e12, 2), "kernels_per_block": 16,
@@ -603,10 +641,10 @@ def attention_config(stream, H=8, T=375, Dh=128, graph=True, reps=200):
     flops = sum(2.0 * H * M * N * K for M, N, K, *_ in calls)
     res = {"what": f"{H} heads, T={T}, Dh={Dh}: 3 batched fp32 products per block"}
     if graph:
-        with P.Graph(stream) as gr:
+        def body():
             for fn in fns:
                 fn()
-        ms, _ = time_graph(gr, stream, 200, 10)
+        ms, _ = StepGraphs(stream, body, STEPS_PER_REPLAY, 200).time(200, 10)
         res.update({"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
                     "pct_fp32_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 2)})
     res["products_ms_back_to_back"] = [round(time_launches(fn, stream, reps), 5) for fn in fns]
