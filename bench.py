@@ -78,21 +78,6 @@ def run_linear(lin, dA, lda, ws, stream, alpha=None, next_w=None):
                             lin.N, ws.ws.ptr, ws.ws.nbytes, next_w, stream.ptr)
 
 
-def time_graph(graph, stream, steps, warmup):
-    for _ in range(warmup):
-        graph.launch()
-    stream.sync()
-    e0, e1 = P.Event(), P.Event()
-    e0.record(stream.ptr)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        graph.launch()
-    e1.record(stream.ptr)
-    e1.sync()
-    wall = time.perf_counter() - t0
-    return e0.elapsed_ms(e1) / steps, wall
-
-
 STEPS_PER_REPLAY = 10   # short chains: steps captured per graph (a window's graph holds all its linears)
 
 
