@@ -10,6 +10,11 @@
  *  in host memory. Five-value and int8-table weights are uploaded once and cached on the device, keyed on their
  *  plane pointers and shape plus a content fingerprint (lo, hi and the first and last bytes of each plane);
  *  p2_gpu_weight_cache_clear() drops the cache (for callers that unmap and remap weights at the same address).
+ *  Contract of the cache: a weight is immutable while its address is in use – the reference's weights are a read-only
+ *  mmap (weights.c:551) – since a change in the middle of a plane at the same address is not seen. A caller that
+ *  changes weights in place sets P2_GPU_WEIGHT_CACHE=0 (read once): every call then uploads its weight and frees the
+ *  copy when it returns. Calls from many threads may share weights, and clearing the cache while they run is safe:
+ *  a copy in use is freed by the last call using it.
  *
  *  Nothing falls back to the CPU: if the GPU library cannot start, the first call prints the reason and aborts.
  */

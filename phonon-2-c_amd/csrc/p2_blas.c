@@ -133,18 +133,33 @@ static void *dgrow(void **p, size_t *cap, size_t need, const char *who)
 
 /* ── the device weight cache ───────────────────────────────────────────────────────────────────────────────── */
 
+/* One device copy per host weight, keyed on its plane pointers, shape and a content fingerprint. A call holds a
+ * reference for as long as its kernels may read the copy: an entry that is dropped (p2_gpu_weight_cache_clear, or new
+ * contents at the same address) while a call holds it is only unlinked, and the last holder frees it. */
 typedef struct Entry {
     const void *a, *b, *c, *d;   /* signs, flags, lo, hi  /  q8, scales */
     int K, N, ld, kind;
     uint64_t fp;
     P2hWeight *w;                /* five-value */
     void *dq8; float *dsc;       /* int8 table: [K][N] int8, [N] scales */
+    int refs;                    /* calls using the copy now */
+    int dead;                    /* unlinked from the cache: freed when refs drops to 0 */
     struct Entry *next;
 } Entry;
 
 #define CACHE_BUCKETS 1024
 static Entry *cache[CACHE_BUCKETS];
 static pthread_mutex_t cache_mu = PTHREAD_MUTEX_INITIALIZER;
+
+/* P2_GPU_WEIGHT_CACHE=0: every call uploads its weight and frees the copy afterwards (for callers that change
+ * weights in place, which the fingerprint does not fully cover) */
+static int cache_on = 1;
+static pthread_once_t cache_env_once = PTHREAD_ONCE_INIT;
+static void cache_env_init(void)
+{
+    const char *v = getenv("P2_GPU_WEIGHT_CACHE");
+    cache_on = !(v && v[0] == '0' && v[1] == 0);
+}
 
 static uint64_t fnv(uint64_t h, const void *p, size_t n)
 {
@@ -173,7 +188,7 @@ static size_t bucket(const void *a, int K, int N)
     return (size_t)(x % CACHE_BUCKETS);
 }
 
-static void entry_release(Entry *e)
+static void entry_free(Entry *e)
 {
     p2h_weight_free(e->w);
     p2h_free(e->dq8);
@@ -181,69 +196,95 @@ static void entry_release(Entry *e)
     free(e);
 }
 
-static const P2hWeight *fv_weight(const FiveValueB *B, int K, int N)
+/* cache_mu held: take e out of the cache; free it now if no call holds it, else its last holder does */
+static void entry_drop_locked(Entry *e)
 {
+    e->dead = 1;
+    if (e->refs == 0) entry_free(e);
+}
+
+/* a call is done with e (its kernels have finished) */
+static void entry_put(Entry *e)
+{
+    pthread_mutex_lock(&cache_mu);
+    if (--e->refs == 0 && e->dead) entry_free(e);
+    pthread_mutex_unlock(&cache_mu);
+}
+
+/* cache_mu held: the live entry for this key with this fingerprint, taken (refs + 1); a stale entry at the same key
+ * is dropped; NULL when there is none */
+static Entry *entry_find_locked(size_t h, int kind, const void *a, const void *b, const void *c, const void *d, int K,
+                                int N, int ld, uint64_t fp)
+{
+    for (Entry **pe = &cache[h]; *pe; pe = &(*pe)->next) {
+        Entry *e = *pe;
+        if (e->kind == kind && e->a == a && e->b == b && e->c == c && e->d == d && e->K == K && e->N == N &&
+            e->ld == ld) {
+            if (e->fp == fp) {
+                e->refs++;
+                return e;
+            }
+            *pe = e->next;   /* same addresses, new contents: drop the stale copy */
+            entry_drop_locked(e);
+            return NULL;
+        }
+    }
+    return NULL;
+}
+
+/* cache_mu held: a new entry holding one reference, in the cache unless caching is off */
+static Entry *entry_new_locked(size_t h, int kind, const void *a, const void *b, const void *c, const void *d, int K,
+                               int N, int ld, uint64_t fp, const char *who)
+{
+    Entry *e = (Entry *)calloc(1, sizeof *e);
+    if (!e) die(who, "out of memory");
+    e->a = a; e->b = b; e->c = c; e->d = d;
+    e->K = K; e->N = N; e->ld = ld; e->kind = kind; e->fp = fp;
+    e->refs = 1;
+    if (cache_on) {
+        e->next = cache[h];
+        cache[h] = e;
+    } else {
+        e->dead = 1;
+    }
+    return e;
+}
+
+static Entry *fv_weight(const FiveValueB *B, int K, int N)
+{
+    pthread_once(&cache_env_once, cache_env_init);
     size_t kn = (size_t)K * N;
     uint64_t fp = fingerprint(B->signs, kn / 4 ? kn / 4 : 1, B->flags, kn / 8 ? kn / 8 : 1, B->lo, B->hi,
                               (size_t)N * sizeof(float));
     size_t h = bucket(B->signs, K, N);
     pthread_mutex_lock(&cache_mu);
-    Entry **pe = &cache[h];
-    for (; *pe; pe = &(*pe)->next) {
-        Entry *e = *pe;
-        if (e->kind == 0 && e->a == B->signs && e->b == B->flags && e->c == B->lo && e->d == B->hi && e->K == K &&
-            e->N == N) {
-            if (e->fp == fp) {
-                pthread_mutex_unlock(&cache_mu);
-                return e->w;
-            }
-            *pe = e->next;   /* same addresses, new contents: drop the stale copy */
-            entry_release(e);
-            break;
-        }
+    Entry *e = cache_on ? entry_find_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp) : NULL;
+    if (!e) {
+        e = entry_new_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp, "p2_sgemm_fvb");
+        e->w = p2h_fv_weight_upload(B->signs, B->flags, B->lo, B->hi, K, N);
+        if (!e->w) die("p2_sgemm_fvb: weight upload", p2h_last_error());
     }
-    Entry *e = (Entry *)calloc(1, sizeof *e);
-    if (!e) die("p2_sgemm_fvb", "out of memory");
-    e->w = p2h_fv_weight_upload(B->signs, B->flags, B->lo, B->hi, K, N);
-    if (!e->w) die("p2_sgemm_fvb: weight upload", p2h_last_error());
-    e->a = B->signs; e->b = B->flags; e->c = B->lo; e->d = B->hi;
-    e->K = K; e->N = N; e->kind = 0; e->fp = fp;
-    e->next = cache[h];
-    cache[h] = e;
     pthread_mutex_unlock(&cache_mu);
-    return e->w;
+    return e;
 }
 
-static const Entry *q8_weight(const signed char *B, const float *scales, int ldb, int K, int N, void *stream)
+static Entry *q8_weight(const signed char *B, const float *scales, int ldb, int K, int N, void *stream)
 {
+    pthread_once(&cache_env_once, cache_env_init);
     size_t rows_bytes = K > 0 ? (size_t)(K - 1) * ldb + N : 1;
     uint64_t fp = fingerprint(B, rows_bytes, NULL, 0, scales, NULL, (size_t)N * sizeof(float));
     size_t h = bucket(B, K, N);
     pthread_mutex_lock(&cache_mu);
-    Entry **pe = &cache[h];
-    for (; *pe; pe = &(*pe)->next) {
-        Entry *e = *pe;
-        if (e->kind == 1 && e->a == B && e->c == scales && e->K == K && e->N == N && e->ld == ldb) {
-            if (e->fp == fp) {
-                pthread_mutex_unlock(&cache_mu);
-                return e;
-            }
-            *pe = e->next;
-            entry_release(e);
-            break;
-        }
+    Entry *e = cache_on ? entry_find_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp) : NULL;
+    if (!e) {
+        e = entry_new_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp, "p2_sgemm_q8b");
+        e->dq8 = p2h_malloc((size_t)K * N + 16);
+        e->dsc = (float *)p2h_malloc((size_t)N * sizeof(float));
+        if (!e->dq8 || !e->dsc) die("p2_sgemm_q8b: weight upload", p2h_last_error());
+        check(p2h_memcpy2d_h2d(e->dq8, (size_t)N, B, (size_t)ldb, (size_t)N, (size_t)K, stream), "p2_sgemm_q8b");
+        check(p2h_memcpy_h2d(e->dsc, scales, (size_t)N * sizeof(float), stream), "p2_sgemm_q8b");
+        check(p2h_stream_sync(stream), "p2_sgemm_q8b");
     }
-    Entry *e = (Entry *)calloc(1, sizeof *e);
-    if (!e) die("p2_sgemm_q8b", "out of memory");
-    e->dq8 = p2h_malloc((size_t)K * N + 16);
-    e->dsc = (float *)p2h_malloc((size_t)N * sizeof(float));
-    if (!e->dq8 || !e->dsc) die("p2_sgemm_q8b: weight upload", p2h_last_error());
-    check(p2h_memcpy2d_h2d(e->dq8, (size_t)N, B, (size_t)ldb, (size_t)N, (size_t)K, stream), "p2_sgemm_q8b");
-    check(p2h_memcpy_h2d(e->dsc, scales, (size_t)N * sizeof(float), stream), "p2_sgemm_q8b");
-    check(p2h_stream_sync(stream), "p2_sgemm_q8b");
-    e->a = B; e->c = scales; e->K = K; e->N = N; e->ld = ldb; e->kind = 1; e->fp = fp;
-    e->next = cache[h];
-    cache[h] = e;
     pthread_mutex_unlock(&cache_mu);
     return e;
 }
@@ -255,7 +296,7 @@ void p2_gpu_weight_cache_clear(void)
         Entry *e = cache[i];
         while (e) {
             Entry *n = e->next;
-            entry_release(e);
+            entry_drop_locked(e);
             e = n;
         }
         cache[i] = NULL;
@@ -310,6 +351,13 @@ static void scale_only(Ctx *c, float *C, int M, int N, int ldc, float beta, cons
     finish_c(c, C, dC, M, N, ldc, who);
 }
 
+/* The int8 routes with K == 0: beta outside {0, 1} pre-scales C and no K block runs, so C is otherwise left as it
+ * is – with beta == 0 too (blas.c:1436 and 1339, sgemm_i8_worker's block loop is empty). */
+static void int8_empty_k(Ctx *c, float *C, int M, int N, int ldc, float beta, const char *who)
+{
+    if (beta != 0.0f && beta != 1.0f) scale_only(c, C, M, N, ldc, beta, who);
+}
+
 /* ── the five-value GEMMs ──────────────────────────────────────────────────────────────────────────────────── */
 
 void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, const FiveValueB *B, float beta,
@@ -320,14 +368,16 @@ void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, con
     Ctx *c = ctx();
     if (M <= 0 || N <= 0) return;
     if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
-    const P2hWeight *w = fv_weight(B, K, N);
     int mode = current_mode();
+    if (mode != P2H_EXACT && K == 0) { int8_empty_k(c, C, M, N, ldc, beta, who); return; }
+    Entry *e = fv_weight(B, K, N);
     float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
     void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, mode, M, N, K, &wsb, who) : NULL;
-    check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, w, beta, dC, N, ws, wsb, c->stream), who);
+    check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, e->w, beta, dC, N, ws, wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
+    entry_put(e);
 }
 
 int p2_quant_prepare(QuantA *qa, int M, int K)
@@ -371,32 +421,36 @@ void p2_sgemm_fvb_q8a(int M, int N, int K, float alpha, const QuantA *A, const F
     if (K % 4 != 0) die(who, "K is not a multiple of 4 (p2_quant_prepare refuses such K)");
     /* the reference reads the codes plane in int8w mode and the two planes otherwise (blas.c:1408) */
     int mode = current_mode() == P2H_INT8W ? P2H_INT8W : P2H_INT8;
-    const P2hWeight *w = fv_weight(B, K, N);
+    if (K == 0) { int8_empty_k(c, C, M, N, ldc, beta, who); return; }
+    Entry *e = fv_weight(B, K, N);
     float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
     void *ws = workspace(c, mode, M, N, K, &wsb, who);
-    check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, w, beta, dC, N, ws, wsb, c->stream), who);
+    check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, e->w, beta, dC, N, ws, wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
+    entry_put(e);
 }
 
 signed char *p2_fv_pack_codes(const FiveValueB *b, int K, int N)
 {
     if (K % 4 != 0 || N % 16 != 0 || K <= 0 || N <= 0) return NULL;   /* blas.c:1393 */
     Ctx *c = ctx();
-    const P2hWeight *w = fv_weight(b, K, N);
+    Entry *e = fv_weight(b, K, N);
     size_t bytes = (size_t)K * N;
     signed char *host = (signed char *)malloc(bytes);
     void *d = p2h_malloc(bytes);
     if (!host || !d) {
         free(host);
         p2h_free(d);
+        entry_put(e);
         return NULL;
     }
-    int rc = p2h_fv_pack_codes(w, (signed char *)d, c->stream);
+    int rc = p2h_fv_pack_codes(e->w, (signed char *)d, c->stream);
     if (rc == 0) rc = p2h_memcpy_d2h(host, d, bytes, c->stream);
     if (rc == 0) rc = p2h_stream_sync(c->stream);
     p2h_free(d);
+    entry_put(e);
     if (rc != 0) {
         free(host);
         return NULL;
@@ -414,8 +468,9 @@ void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, con
     Ctx *c = ctx();
     if (M <= 0 || N <= 0) return;
     if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
-    const Entry *e = q8_weight(B, scales, ldb, K, N, c->stream);
     int mode = current_mode();
+    if (mode != P2H_EXACT && K == 0) { int8_empty_k(c, C, M, N, ldc, beta, who); return; }
+    Entry *e = q8_weight(B, scales, ldb, K, N, c->stream);
     float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
@@ -423,6 +478,7 @@ void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, con
     check(p2h_q8b_gemm(mode, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws, wsb,
                        c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
+    entry_put(e);
 }
 
 void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const signed char *B, const float *scales,
@@ -434,7 +490,8 @@ void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const s
     if (M <= 0 || N <= 0) return;
     if (alpha == 0.0f) { scale_only(c, C, M, N, ldc, beta, who); return; }
     if (K % 4 != 0) die(who, "K is not a multiple of 4 (p2_quant_prepare refuses such K)");
-    const Entry *e = q8_weight(B, scales, ldb, K, N, c->stream);
+    if (K == 0) { int8_empty_k(c, C, M, N, ldc, beta, who); return; }
+    Entry *e = q8_weight(B, scales, ldb, K, N, c->stream);
     float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
@@ -442,6 +499,7 @@ void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const s
     check(p2h_q8b_gemm(P2H_INT8W, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws,
                        wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
+    entry_put(e);
 }
 
 /* ── fp32 GEMM ─────────────────────────────────────────────────────────────────────────────────────────────── */

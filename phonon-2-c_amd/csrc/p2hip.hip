@@ -989,15 +989,20 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
         if (!aligned(dC[q], 16)) g.c_vec4 = 0;
     }
     g.units = w[0]->units;
-    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n), (unsigned)groups), block(256);
+    /* the kernel of the plan's tile: the grid and g.tiles_n/tiles_m were sized for exactly that tile */
+    const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n), (unsigned)groups);
     if (wide)
         hipLaunchKernelGGL((p2k::gemm_fv_grouped<FvW6, false>), grid, dim3(FvW6::NT), 0, s, g, ga);
-    else if (mode == P2H_INT8)
-        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8>), grid, block, 0, s, g, ga);
+    else if (mode == P2H_INT8)   /* make_plan gives the two-plane mode 32 x 32 tiles only */
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8>), grid, dim3(SmS::NT), 0, s, g, ga);
+    else if (p.cfg == FV_SS)
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8W>), grid, dim3(SmS::NT), 0, s, g, ga);
     else if (p.cfg == FV_SW)
-        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmW, p2k::MODE_INT8W>), grid, block, 0, s, g, ga);
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmW, p2k::MODE_INT8W>), grid, dim3(SmW::NT), 0, s, g, ga);
+    else if (p.cfg == FV_SD)
+        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmD, p2k::MODE_INT8W>), grid, dim3(SmD::NT), 0, s, g, ga);
     else
-        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8W>), grid, block, 0, s, g, ga);
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_grouped: no grouped kernel for tile %d", p.cfg);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }

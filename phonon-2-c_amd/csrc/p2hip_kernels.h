@@ -1661,7 +1661,7 @@ struct GroupArgs {
 };
 
 template <class G, int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_fvs_grouped(GemmArgs g, GroupArgs ga)
+__global__ __launch_bounds__(G::NT, G::NT > 256 ? 1 : 2) void gemm_fvs_grouped(GemmArgs g, GroupArgs ga)
 {
     GemmArgs h = g;
     const int q = blockIdx.y;

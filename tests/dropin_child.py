@@ -135,6 +135,71 @@ def main():
     L.p2_sgemm(111, 111, 33, 40, 70, 1.0, A.ctypes.data, 70, B.ctypes.data, 40, 1.0, out.ctypes.data, 40)
     expect(np.allclose(out, A.astype(np.float64) @ B + 1.0, rtol=1e-4, atol=1e-4), "p2_sgemm")
 
+    # K == 0 (blas.c:1436, 1488-1496): the int8 routes pre-scale C for beta outside {0, 1} and run no K block, so C
+    # keeps its values otherwise (beta 0 included); the exact route scales C by beta (0 stores zeros)
+    M, N = 7, 32
+    z8, lo0, hi0 = np.zeros(16, np.uint8), np.full(N, 0.01, np.float32), np.full(N, 0.03, np.float32)
+    b0 = FiveValueB(z8.ctypes.data, z8.ctypes.data, lo0.ctypes.data, hi0.ctypes.data, None)
+    C0 = P.gen_activations(seed, 71, M, N)
+    A0 = np.zeros((M, 4), np.float32)
+    for beta in (0.0, 1.0, 0.5):
+        out = C0.copy()
+        L.p2_sgemm_fvb(M, N, 0, 1.0, A0.ctypes.data, 4, C.byref(b0), beta, out.ctypes.data, N)
+        if mode_env == O.EXACT:
+            want = (C0 * np.float32(beta)).astype(np.float32) if beta != 0.0 else np.zeros_like(C0)
+        else:
+            want = C0 if beta in (0.0, 1.0) else (C0 * np.float32(beta)).astype(np.float32)
+        expect(np.array_equal(out.view(np.uint32), want.view(np.uint32)), f"p2_sgemm_fvb K=0 beta={beta}")
+
+    # many threads on shared weights while the cache is cleared under them (phonon2.h:277-280: concurrent
+    # transcriptions share one engine's weights): every result must still equal the oracle's
+    import threading
+    L.p2_gpu_weight_cache_clear.argtypes = []
+    L.p2_gpu_weight_cache_clear.restype = None
+    shared = []
+    for t in range(3):
+        M, K, N = (64, 1024, 256) if t < 2 else (16, 4096, 128)
+        signs, flags, lo, hi = P.gen_fv_weight(seed, 300 + t, K, N)
+        A = P.gen_activations(seed, 310 + t, M, K)
+        ref = O.sgemm_fvb(mode_env, A, signs, flags, lo, hi, N)
+        shared.append((M, K, N, signs, flags, lo, hi, A, ref,
+                       FiveValueB(signs.ctypes.data, flags.ctypes.data, lo.ctypes.data, hi.ctypes.data, None)))
+    bad = []
+    stop = threading.Event()
+
+    def worker(tid):
+        for it in range(12):
+            M, K, N, signs, flags, lo, hi, A, ref, fb = shared[(tid + it) % len(shared)]
+            out = np.zeros((M, N), np.float32)
+            if it % 2 == 0 or mode_env == O.EXACT:
+                L.p2_sgemm_fvb(M, N, K, 1.0, A.ctypes.data, K, C.byref(fb), 0.0, out.ctypes.data, N)
+            else:
+                qa = QuantA()
+                if L.p2_quant_prepare(C.byref(qa), M, K) != 0:
+                    bad.append(f"thread {tid} prepare")
+                    continue
+                for m in range(M):
+                    L.p2_quant_row(C.byref(qa), m, A[m].ctypes.data)
+                L.p2_sgemm_fvb_q8a(M, N, K, 1.0, C.byref(qa), C.byref(fb), 0.0, out.ctypes.data, N)
+            if not same(out, ref, K):
+                bad.append(f"thread {tid} call {it}")
+
+    def clearer():
+        while not stop.is_set():
+            L.p2_gpu_weight_cache_clear()
+            stop.wait(0.002)
+
+    cl = threading.Thread(target=clearer)
+    cl.start()
+    ths = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    stop.set()
+    cl.join()
+    expect(not bad, "concurrent calls: " + ", ".join(bad[:5]))
+
     if failures:
         print(f"mode {mode_name}: FAILED: " + "; ".join(failures))
         return 1

@@ -314,10 +314,12 @@ def test_q8a_next_matches_q8a(mode, M, K, N, Kn, Nn, beta):
 @pytest.mark.parametrize("mode", ["int8w", "int8"])
 @pytest.mark.parametrize("M,K,N,groups,beta", [(749, 1024, 1024, 24, 0.0), (375, 1024, 4096, 3, 1.0),
                                                (38, 4096, 1024, 5, 0.5), (2000, 1024, 256, 2, 0.0),
-                                               (600, 1024, 272, 20, 0.5)])
+                                               (600, 1024, 272, 20, 0.5), (375, 4096, 1024, 3, 0.0),
+                                               (375, 4096, 1024, 2, 1.0)])
 def test_grouped_q8a(mode, M, K, N, groups, beta):
     """Each group's output equals its own p2h_fvb_gemm_q8a call bit for bit (2000 rows: the per-weight path; int8w at
-    749 × 24 · 1024 and 600 × 20 · 272: the large-M kernel's tiles, ragged in both dimensions for the latter)."""
+    749 × 24 · 1024 and 600 × 20 · 272: the large-M kernel's tiles, ragged in both dimensions for the latter; int8w at
+    375 × 4096 → 1024: the eight-wave 32 × 64 small-M tile, whose grid has half as many column tiles as 32 × 32)."""
     A = P.gen_activations(SEED, 1500 + M, M, K)
     q, sc = O.quant_rows(A)
     ws = [P.FvWeight(*_weight(K, N, 1600 + i), K, N) for i in range(groups)]
