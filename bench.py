@@ -138,24 +138,6 @@ def time_launches(launch, stream, reps):
     raise RuntimeError(f"host queued {reps} launches more slowly than a {hold_us} us hold")
 
 
-def kernel_times(linears, inputs, ws, stream, reps):
-    """Duration (ms) of each linear's quantise and GEMM kernels, each timed on its own by time_launches (the GEMM
-    as the chain calls it, reading the next linear's records ahead)."""
-    q = np.zeros(len(linears))
-    t = np.zeros(len(linears))
-    for i, (lin, (dA, lda)) in enumerate(zip(linears, inputs)):
-        ldq = P.q_ld(lin.K)
-        nxt = linears[(i + 1) % len(linears)].w
-        q[i] = time_launches(lambda: P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr),
-                             stream, reps)
-        t[i] = time_launches(lambda: P.fvb_gemm_q8a_next_dev("int8w", lin.M, lin.N, lin.K, lin.alpha, ws.q.ptr, ldq,
-                                                             ws.s.ptr, lin.w, 0.0, lin.out.ptr, lin.N, ws.ws.ptr,
-                                                             ws.ws.nbytes, nxt, stream.ptr),
-                             stream, reps)
-    stream.sync()
-    return q, t
-
-
 def kernel_name(plan):
     return "gemm_fvs" if "waves" in plan else "gemm_fv"
 
@@ -209,34 +191,82 @@ def sweep_spec(M=375):
     return spec
 
 
+class Chain:
+    """A chain of five-value linears on one stream, as an encoder window runs them: each linear quantises its input
+    rows and runs the q8a GEMM, reading the records of the chain's next weight ahead; the positional projections
+    (spec input 'pos'), whose rows are the same for every block (encoder.c:500), are one quantisation and one grouped
+    launch at the start. body() queues one pass; it can be captured into a graph. Every linear writes its own output
+    buffer (beta 0) from inputs no linear overwrites, so passes are idempotent."""
+
+    def __init__(self, spec):
+        self.spec = spec
+        self.linears, self.inputs, self.ws, self.keep = build_chain(spec, None)
+        self.pos = [i for i, sp in enumerate(spec) if sp[4] == "pos"]
+        if self.pos:
+            P0 = self.linears[self.pos[0]]
+            self.pq = P.DeviceBuffer(P.q_bytes(P0.M, P0.K))
+            self.ps = P.DeviceBuffer(4 * P0.M)
+        self.order = [i for i in range(len(self.linears)) if i not in self.pos]
+
+    def pos_launch(self, stream):
+        P0 = self.linears[self.pos[0]]
+        P.fvb_gemm_q8a_grouped_dev("int8w", P0.M, P0.N, P0.K, 1.0, self.pq.ptr, P.q_ld(P0.K), self.ps.ptr,
+                                   [self.linears[i].w for i in self.pos], 0.0,
+                                   [self.linears[i].out.ptr for i in self.pos], P0.N, stream.ptr)
+
+    def pos_quant(self, stream):
+        P0 = self.linears[self.pos[0]]
+        dA, lda = self.inputs[self.pos[0]]
+        P.quant_rows_dev(P0.M, P0.K, dA, lda, self.pq.ptr, P.q_ld(P0.K), self.ps.ptr, stream.ptr)
+
+    def next_w(self, x):
+        return self.linears[self.order[(x + 1) % len(self.order)]].w
+
+    def body(self, stream):
+        if self.pos:   # the positional rows quantised once, every block's projection in one launch (alpha 1)
+            self.pos_quant(stream)
+            self.pos_launch(stream)
+        for x, i in enumerate(self.order):   # each GEMM reads the next one's records ahead (the last, the first's)
+            run_linear(self.linears[i], *self.inputs[i], self.ws, stream, next_w=self.next_w(x))
+
+    def kernel_times(self, stream, reps):
+        """Duration (ms) of each kernel of the chain on its own (time_launches): per linear its quantisation and its
+        GEMM as the chain calls it (the positional linears: the one grouped launch, and its quantisation, shared)."""
+        n = len(self.linears)
+        q, t = np.full(n, np.nan), np.full(n, np.nan)
+        ws = self.ws
+        for x, i in enumerate(self.order):
+            lin, (dA, lda), nxt = self.linears[i], self.inputs[i], self.next_w(x)
+            ldq = P.q_ld(lin.K)
+            q[i] = time_launches(lambda: P.quant_rows_dev(lin.M, lin.K, dA, lda, ws.q.ptr, ldq, ws.s.ptr, stream.ptr),
+                                 stream, reps)
+            t[i] = time_launches(lambda: P.fvb_gemm_q8a_next_dev("int8w", lin.M, lin.N, lin.K, lin.alpha, ws.q.ptr,
+                                                                 ldq, ws.s.ptr, lin.w, 0.0, lin.out.ptr, lin.N,
+                                                                 ws.ws.ptr, ws.ws.nbytes, nxt, stream.ptr),
+                                 stream, reps)
+        grouped = None
+        if self.pos:
+            gq = time_launches(lambda: self.pos_quant(stream), stream, reps)
+            grouped = time_launches(lambda: self.pos_launch(stream), stream, reps)
+            for i in self.pos:
+                q[i], t[i] = gq / len(self.pos), grouped / len(self.pos)
+        stream.sync()
+        return q, t, grouped
+
+
 def measure_chain(spec, stream, steps, warmup, kreps, per=1):
     """Capture the chain into a graph on one stream (`per` steps per graph) and time exactly `steps` steps; then,
     when kreps > 0, time each kernel on its own. (A parallel graph branch for the positional projections, whose
     input is the positional table rather than an earlier linear's output, measured slower on MI355X than the
     single chain.)"""
-    linears, inputs, ws, keep = build_chain(spec, None)
-    pos = [i for i, sp in enumerate(spec) if sp[4] == "pos"]
-    if pos:
-        P0 = linears[pos[0]]
-        pq = P.DeviceBuffer(P.q_bytes(P0.M, P0.K))
-        ps = P.DeviceBuffer(4 * P0.M)
-        keep["pos_q"] = (pq, ps)
-    def body():
-        if pos:   # the positional rows quantised once, every block's projection in one launch
-            P.quant_rows_dev(P0.M, P0.K, inputs[pos[0]][0], inputs[pos[0]][1], pq.ptr, P.q_ld(P0.K), ps.ptr,
-                             stream.ptr)
-            P.fvb_gemm_q8a_grouped_dev("int8w", P0.M, P0.N, P0.K, 1.0, pq.ptr, P.q_ld(P0.K), ps.ptr,   # alpha 1: encoder.c:500
-                                       [linears[i].w for i in pos], 0.0, [linears[i].out.ptr for i in pos], P0.N,
-                                       stream.ptr)
-        order = [i for i in range(len(linears)) if i not in pos]
-        for x, i in enumerate(order):   # each GEMM reads the next one's records ahead (the last, the first's)
-            run_linear(linears[i], *inputs[i], ws, stream, next_w=linears[order[(x + 1) % len(order)]].w)
-    ms, wall = StepGraphs(stream, body, per, steps).time(steps, warmup)
+    ch = Chain(spec)
+    ms, wall = StepGraphs(stream, lambda: ch.body(stream), per, steps).time(steps, warmup)
+    grouped = None
     if kreps > 0:
-        qt, gt = kernel_times(linears, inputs, ws, stream, kreps)
+        qt, gt, grouped = ch.kernel_times(stream, kreps)
     else:
-        qt, gt = np.full(len(linears), np.nan), np.full(len(linears), np.nan)
-    return linears, ms, wall, qt, gt
+        qt, gt = np.full(len(ch.linears), np.nan), np.full(len(ch.linears), np.nan)
+    return ch.linears, ms, wall, qt, gt, grouped
 
 
 def summarize(linears, ms, qt, gt):
@@ -348,8 +378,10 @@ def main():
 
     def run(name, spec, steps, warmup, kreps):
         per = STEPS_PER_REPLAY if len(spec) <= 4 else 1   # a window's chain is one graph already
-        lins, ms, wall, qt, gt = measure_chain(spec, stream, steps, warmup, kreps, per)
+        lins, ms, wall, qt, gt, grouped = measure_chain(spec, stream, steps, warmup, kreps, per)
         r = summarize(lins, ms, qt, gt)
+        if grouped is not None:
+            r["grouped_pos_ms"] = round(float(grouped), 5)
         r["wall_s"] = round(wall, 3)
         results[name] = (lins, r)
         print(f"# {name}: {ms * 1e3:.2f} us/step, {r['tops']:.1f} TOPS", file=sys.stderr, flush=True)
@@ -543,7 +575,7 @@ def m38_rotated_config(stream, pairs=40, steps=50, warmup=5):
     spec = []
     for r in range(pairs):
         spec += [(2000 + 2 * r, 1024, 4096, M, "x" if r == 0 else 2 * r - 1), (2001 + 2 * r, 4096, 1024, M, 2 * r)]
-    linears, ms, wall, qt, gt = measure_chain(spec, stream, steps, warmup, 0)
+    linears, ms, wall, qt, gt, _ = measure_chain(spec, stream, steps, warmup, 0)
     per_pair = ms / pairs
     planes = sum(l.K * l.N * 3 / 8 + 8 * l.N for l in linears) / pairs
     records = sum(l.K * l.N / 2 + 8 * l.N for l in linears) / pairs

@@ -358,6 +358,25 @@ def test_full_size_sampled_rows(M, K, N):
     assert _bits_equal(got2, (got * np.float32(4.0)).astype(np.float32))
 
 
+@pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024)])
+def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
+    """The exact route at the batched long-audio shapes (16 windows stacked, 12k+ workgroups on the fp32 matrix
+    cores): sampled rows (first and last included) within 1e-4 of the oracle's exact route, the fmaf-chain route
+    (P2H_EXACT_CHAIN=1) bit-exact on the same rows, and over every row the power-of-two property (rows scaled by 4
+    give outputs scaled by exactly 4: every product and partial sum scales exactly)."""
+    signs, flags, lo, hi = _weight(K, N, 740 + K + N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 840 + K, M, K)
+    got = P.fvb_gemm("exact", A, w)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M + K).choice(M, 40, replace=False)]))
+    ref = O.sgemm_fvb("exact", A[rows], signs, flags, lo, hi, N)
+    _assert_exact(got[rows], ref)
+    chain = _chain(monkeypatch, lambda: P.fvb_gemm("exact", A, w))
+    _assert_fp32(chain[rows], ref)
+    got4 = P.fvb_gemm("exact", A * np.float32(4.0), w)
+    assert _bits_equal(got4, (got * np.float32(4.0)).astype(np.float32))
+
+
 # ── every tile configuration and K split (the planner's choices forced through its tuning variables) ─────────────
 
 _TILE_CASES = {}
