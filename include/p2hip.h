@@ -183,6 +183,19 @@ int    p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA,
                     float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream);
 size_t p2h_fvb_workspace_bytes(int mode, int M, int N, int K);
 
+/* No counterpart in the reference: p2h_fvb_gemm for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). It takes no workspace argument and allocates nothing:
+ * its quantised rows and split partials live in a device array of P2H_NOALLOC_SCRATCH_BYTES that the library holds
+ * on each GPU it runs on until the process ends. Shapes whose p2h_fvb_workspace_bytes exceeds that size are refused
+ * with P2H_E_WORKSPACE (M = 6000 at K = 4096 fits: 24.6 MB). `stream` must be the caller's own (non-NULL). Calls on
+ * one GPU share its array: calls that overlap in time on one GPU (other streams, other threads) race and must be
+ * ordered by the caller. Nothing in the array needs to start at zero (every byte a kernel reads was written earlier
+ * in the same call). Results are those of p2h_fvb_gemm. */
+#define P2H_NOALLOC_SCRATCH_BYTES (32u << 20)
+int    p2h_fvb_gemm_noalloc(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
+                            float beta, float *dC, int ldc, void *stream);
+size_t p2h_noalloc_scratch_bytes(void);
+
 /* The raw int32 accumulators sum_k q[m][k]·B[k][n] over all K of the int8 kernel (blas.c:1256-1282): for
  * P2H_INT8W B is the codes plane into dAcc; for P2H_INT8 the S plane into dAcc and the T plane into dAcc2. */
 int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ldq, const P2hWeight *w,

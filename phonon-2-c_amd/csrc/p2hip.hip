@@ -20,6 +20,15 @@ namespace {
 thread_local char t_err[512];
 thread_local hipStream_t t_stream = nullptr;
 
+/* The allocation-free entry's workspace: one array per device, held until the process ends. Host code never passes
+ * `scratch` itself to a kernel (its host-side name is not a device address): it passes the device address that
+ * hipGetSymbolAddress gives for the current device, kept in g_scratch_ptr. */
+constexpr size_t kScratchBytes = (size_t)P2H_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
 std::once_flag g_init_once;
 int g_init_rc = P2H_E_DEVICE;
 char g_init_err[512];
@@ -70,7 +79,27 @@ void do_init()
         snprintf(g_init_err, sizeof g_init_err, "p2h_init: hipSetDevice: %s", hipGetErrorString(e));
         return;
     }
+    /* device 0's scratch address, with device 0 current (another device's is taken on its first no-alloc call) */
+    void *sp = nullptr;
+    if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_ptr[0] = sp;
     g_init_rc = P2H_OK;
+}
+
+/* The device address of the current device's scratch array (taken once per device, with that device current). */
+int scratch_of_current_device(void **out)
+{
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(P2H_E_DEVICE, "scratch: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(P2H_E_DEVICE, "scratch: hipGetSymbolAddress gave NULL on device %d", dev);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return P2H_OK;
 }
 
 int ensure_init()
@@ -1146,6 +1175,29 @@ int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
     g.rec = w->rec4; g.units = w->units;
     if (env_int("P2H_EXACT_CHAIN", 0) != 0 || K == 0) return launch_exact(p2k::EXB_FV, g, s);
     return launch_xf(g, s);
+}
+
+size_t p2h_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int p2h_fvb_gemm_noalloc(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
+                         float beta, float *dC, int ldc, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (!stream)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_noalloc: needs the caller's stream (this library's per-thread stream "
+                               "is created on first use)");
+    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_noalloc: unknown mode %d", mode);
+    const size_t need = p2h_fvb_workspace_bytes(mode, M, N, K);   /* 0 on the exact route */
+    if (need > kScratchBytes)
+        return fail(P2H_E_WORKSPACE,
+                    "p2h_fvb_gemm_noalloc: %d x %d x %d needs %zu bytes of workspace, above the %zu-byte scratch "
+                    "array; use p2h_fvb_gemm with a workspace",
+                    M, K, N, need, kScratchBytes);
+    void *ws = nullptr;
+    if (need > 0)
+        if (int rc = scratch_of_current_device(&ws)) return rc;
+    return p2h_fvb_gemm(mode, M, N, K, alpha, dA, lda, w, beta, dC, ldc, ws, need > 0 ? kScratchBytes : 0, stream);
 }
 
 int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, int ldq, const float *dScales,
