@@ -358,6 +358,37 @@ def test_full_size_sampled_rows(M, K, N):
     assert _bits_equal(got2, (got * np.float32(4.0)).astype(np.float32))
 
 
+def _i8w_fold_all_rows(q, sc, signs, flags, lo, hi, K, N, alpha):
+    """int8w outputs for one 1024-row block, all rows: exact int32 sums (float64 products of the oracle's codes and
+    the quantised rows, exact below 2^53) folded as the reference folds them, in float32 operations:
+    f = (float)acc · (hi · (1/127)), C = f · (a_scale · alpha) (blas.c:1316-1328, 1355-1366)."""
+    codes = O.codes_i8w(signs, flags, lo, hi, K, N)
+    acc = (q.astype(np.float64) @ codes.astype(np.float64)).astype(np.float32)
+    c1 = np.asarray(hi, np.float32) * (np.float32(1.0) / np.float32(127.0))
+    asc = np.asarray(sc, np.float32) * np.float32(alpha)
+    return (acc * c1[None, :]) * asc[:, None]
+
+
+@pytest.mark.parametrize("M,K,N", [(8000, 1024, 1040), (4099, 900, 2064), (1100, 1024, 4096)])
+def test_large_m_every_output(M, K, N):
+    """The large-M kernel over whole matrices: every output bit-exact against the fold of exact int32 sums, itself
+    checked against the oracle on sampled rows; ragged M and N (partial row and column tiles), K below 1024 (a
+    zero-padded unit); C wider than N (ldc = N + 16) and filled with NaN beforehand: beta 0 never reads C, every
+    output is written and nothing past column N is; two calls in a row give the same bits."""
+    signs, flags, lo, hi = _weight(K, N, 960 + K + N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 961 + M, M, K)
+    q, sc = O.quant_rows(A)
+    ref = _i8w_fold_all_rows(q, sc, signs, flags, lo, hi, K, N, 0.7)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 24, replace=False)]))
+    assert _bits_equal(ref[rows], O.gemm_i8_run("int8w", q[rows], sc[rows], signs, flags, lo, hi, N, alpha=0.7))
+    C0 = np.full((M, N + 16), np.nan, np.float32)
+    for _ in range(2):   # twice: nothing carries over between calls
+        got = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=0.7, C0=C0)
+        _assert_fp32(got[:, :N], ref)
+        assert np.isnan(got[:, N:]).all()
+
+
 @pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024)])
 def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
     """The exact route at the batched long-audio shapes (16 windows stacked, 12k+ workgroups on the fp32 matrix
