@@ -224,6 +224,65 @@ int p2h_sgemm_batched(int transA, int transB, int M, int N, int K, float alpha, 
                       long long strideA, const float *dB, int ldb, long long strideB, float beta, float *dC, int ldc,
                       long long strideC, int batch, void *stream);
 
+/* ── the conformer block between its linears (device pointers, asynchronous) ────────────────────────────────────
+ * The model's fixed widths: D = 1024 channels, 8 heads of 128 (phonon2.h:73-78); T frames, L = 2T − 1 positions.
+ *   p2h_gather_heads       QKV [T][3D] (q | k | v) → Q_u = q + bias_u, Q_v = q + bias_v, V as [8][T][128] and K
+ *                          transposed as [8][128][T] (gather_heads, encoder.c:366-404)
+ *   p2h_transpose_pos      P [L][D] → [8][128][L] (transpose_pos, encoder.c:406-423)
+ *   p2h_combine_softmax    AC [8·T][T] in place: softmax((AC + relative shift of BD [8·T][L]) / sqrt(128)) per row
+ *                          (combine_softmax, encoder.c:425-450, p2_softmax's AVX2 route, tensor_ops.c:354-413: the
+ *                          exponential of p2_exp_avx2, eight running sums, the tail T mod 8 with expf)
+ *   p2h_glu_channel_major  pw1 [T][2D] → gated [D][T] = first half / (1 + e^−second half) (glu_to_channel_major,
+ *                          encoder.c:543-555; expf)
+ *   p2h_depthwise_conv_silu  dw [D][T] = SiLU(depthwise convolution of gated [D][T] with w [D][9], b [D], padding 4)
+ *                          (p2_depthwise_conv1d then p2_swish, tensor_ops.c:559-648, 437-491; encoder.c:597-598)
+ *   p2h_silu               x · sigmoid(x) in place on n floats (p2_swish, tensor_ops.c:437-491)
+ *   p2h_add_residual       X [T][D] += alpha · Y (add_residual, encoder.c:252-275)
+ *   p2h_layer_norm_rows    Y = LayerNorm(X) per row, eps 1e-5, X == Y allowed (p2_layer_norm_rows(_inplace),
+ *                          tensor_ops.c:204-332), the same arithmetic as p2h_layer_norm_quant_rows
+ *   p2h_concat_heads_rows  heads [8][T][128] → rows [T][D] fp32 (concat_heads, encoder.c:452-466)
+ *   p2h_channel_major_rows channel-major [D][T] → rows [T][D] fp32 (channel_major_to_rows, encoder.c:557-571)
+ * Transcendentals use expf where the reference calls libm (GLU, softmax and SiLU tails) and the reference's AVX2
+ * polynomial where it does (softmax and SiLU bodies); every quotient and square root is correctly rounded. */
+int p2h_gather_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, float *dQu, float *dQv,
+                     float *dKt, float *dVh, void *stream);
+int p2h_transpose_pos(int L, const float *dP, float *dPt, void *stream);
+int p2h_combine_softmax(int T, float *dAC, const float *dBD, void *stream);
+int p2h_glu_channel_major(int T, const float *dPW1, float *dGated, void *stream);
+int p2h_depthwise_conv_silu(int T, const float *dGated, const float *dW, const float *dB, float *dOut, void *stream);
+int p2h_silu(size_t n, float *dX, void *stream);
+int p2h_add_residual(int T, float *dX, const float *dY, float alpha, void *stream);
+int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta, float *dY,
+                        int ldy, void *stream);
+int p2h_concat_heads_rows(int T, const float *dAttnH, float *dY, void *stream);
+int p2h_channel_major_rows(int T, const float *dDW, float *dY, void *stream);
+
+/* One FastConformer block on the device (conformer_block, encoder.c:617-625): feed-forward ½, relative-position
+ * self-attention, convolution module, feed-forward ½, final LayerNorm, on X [T][1024] in place. The five-value
+ * linears run in `mode` (P2H_INT8W / P2H_INT8: LayerNorm, SiLU, head concatenation and the channel-major transpose
+ * quantise their rows as they make them and the residuals are the GEMMs' beta-1 epilogues, as the reference's int8
+ * path does; P2H_EXACT: fp32 rows, the fp32-input GEMM and separate residual adds, as its fp32 path does). PE is
+ * the window's positional table [2T − 1][1024] (rel_pos_encoding, encoder.c:79-96), shared by every block. The
+ * workspace is p2h_conformer_block_workspace_bytes(mode, T) bytes, 256-byte aligned. Norm vectors [1024], bias_u /
+ * bias_v [8·128], dw_w [1024·9] and dw_b [1024] are device pointers. */
+typedef struct P2hBlock {
+    const float *norm_ff1_w, *norm_ff1_b;
+    const P2hWeight *ff1_l1, *ff1_l2;            /* [1024, 4096], [4096, 1024] */
+    const float *norm_sa_w, *norm_sa_b;
+    const P2hWeight *qkv, *pos, *out;            /* [1024, 3072], [1024, 1024], [1024, 1024] */
+    const float *bias_u, *bias_v;
+    const float *norm_conv_w, *norm_conv_b;
+    const P2hWeight *pw1, *pw2;                  /* [1024, 2048], [1024, 1024] */
+    const float *dw_w, *dw_b;
+    const float *norm_ff2_w, *norm_ff2_b;
+    const P2hWeight *ff2_l1, *ff2_l2;
+    const float *norm_out_w, *norm_out_b;
+} P2hBlock;
+
+size_t p2h_conformer_block_workspace_bytes(int mode, int T);
+int    p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, float *dX, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

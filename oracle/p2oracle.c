@@ -229,6 +229,88 @@ void p2o_swish_row(float *x, int len)
     for (int i = body; i < len; i++) x[i] *= 1.0f / (1.0f + expf(x[i] < -87.0f ? 87.0f : -x[i]));
 }
 
+/* p2_softmax, AVX2 route (tensor_ops.c:354-413): the maximum (order-free); over the elements below the last
+ * multiple of eight, e = exp(x − max) summed into eight running lane sums in order (element j into lane j mod 8),
+ * the lanes met as p2_hsum_avx2 pairs them (tensor_ops.c:182-190); the tail with expf added after them in order;
+ * then every element times 1/sum. */
+static void softmax_row(float *x, int len)
+{
+    const int body = len / 8 * 8;
+    float mx = x[0];
+    for (int i = 1; i < len; i++)
+        if (x[i] > mx) mx = x[i];
+    float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < body; i++) {
+        x[i] = exp_avx2_lane(x[i] - mx);
+        lane[i & 7] += x[i];
+    }
+    float sum = ((lane[0] + lane[4]) + (lane[2] + lane[6])) + ((lane[1] + lane[5]) + (lane[3] + lane[7]));
+    for (int i = body; i < len; i++) {
+        x[i] = expf(x[i] - mx);
+        sum += x[i];
+    }
+    const float inv = 1.0f / sum;
+    for (int i = 0; i < len; i++) x[i] *= inv;
+}
+
+/* combine_softmax (encoder.c:425-450): row r of the [H·T, T] scores, query i = r mod T, reads its bd row from
+ * position T − 1 − i (the relative shift); a = (ac + bd) · scale, then the softmax of the row. */
+void p2o_combine_softmax(float *ac, const float *bd, int H, int T, float scale)
+{
+    const int L = 2 * T - 1;
+    for (int r = 0; r < H * T; r++) {
+        const int i = r % T;
+        float *a = ac + (size_t)r * T;
+        const float *b = bd + (size_t)r * L + (T - 1 - i);
+        for (int j = 0; j < T; j++) a[j] = (a[j] + b[j]) * scale;
+        softmax_row(a, T);
+    }
+}
+
+/* glu_to_channel_major (encoder.c:543-555): gated[d][t] = pw1[t][d] / (1 + p2_expneg(pw1[t][D + d])), p2_expneg
+ * clamping the exponent's argument at 87 (phonon2.h:38-41). */
+void p2o_glu_channel_major(const float *pw1, float *gated, int T, int D)
+{
+    for (int t = 0; t < T; t++) {
+        const float *row = pw1 + (size_t)t * 2 * D;
+        for (int d = 0; d < D; d++) {
+            const float g = row[D + d];
+            gated[(size_t)d * T + t] = row[d] / (1.0f + expf(g < -87.0f ? 87.0f : -g));
+        }
+    }
+}
+
+/* depthwise_conv1d_channel (tensor_ops.c:559-627): padding (K − 1)/2, per output the bias then one fmaf per tap
+ * inside the sequence in order of the tap, as the source's AVX2 body (tensor_ops.c:592-598) computes each of its
+ * eight lanes. The source's scalar edges (t < pad, the last (T − 2·pad) mod 8 interior outputs, t ≥ T − pad) write
+ * the same chain; an -ffast-math build may reassociate those, so there the reference's values can differ from these
+ * in the last bits. */
+void p2o_dwconv(const float *x, const float *w, const float *b, float *out, int D, int T, int K)
+{
+    const int pad = (K - 1) / 2;
+    for (int d = 0; d < D; d++) {
+        const float *xr = x + (size_t)d * T;
+        float *orow = out + (size_t)d * T;
+        for (int t = 0; t < T; t++) {
+            float v = b[d];
+            for (int k = 0; k < K; k++) {
+                const int s = t - pad + k;
+                if (s >= 0 && s < T) v = fmaf(xr[s], w[(size_t)d * K + k], v);
+            }
+            orow[t] = v;
+        }
+    }
+}
+
+/* the convolution module's depthwise step and activation (encoder.c:596-597): p2o_dwconv, then p2_swish
+ * (tensor_ops.c:481-491) on the channel-major result, whose length D·T is a multiple of 16 at D = 1024, so every
+ * element takes the eight-wide body. */
+void p2o_dwconv_silu(const float *x, const float *w, const float *b, float *out, int D, int T, int K)
+{
+    p2o_dwconv(x, w, b, out, D, T, K);
+    p2o_swish_row(out, D * T);
+}
+
 /* LayerNorm then quantise each row (p2_layer_norm_quant_rows, tensor_ops.c:329-350) */
 void p2o_ln_quant_rows(const float *X, int M, int D, int ldx, const float *gamma, const float *beta, int8_t *q,
                        float *scales)

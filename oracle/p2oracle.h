@@ -78,6 +78,16 @@ void p2o_silu_quant_rows(const float *H, int M, int K, int ldh, int8_t *q, float
 void p2o_concat_heads_quant_rows(const float *attn_h, int H, int T, int Dh, int8_t *q, float *scales);
 void p2o_channel_major_quant_rows(const float *dw, int D, int T, int8_t *q, float *scales);
 
+/* The conformer block between its linears, in the reference's order of operations, each operation rounded once:
+ *   p2o_combine_softmax  scores (encoder.c:425-450) with p2_softmax's AVX2 route (tensor_ops.c:354-413)
+ *   p2o_glu_channel_major  encoder.c:543-555 (expf, IEEE quotient)
+ *   p2o_dwconv           p2_depthwise_conv1d (tensor_ops.c:559-648) as an fmaf chain per output
+ *   p2o_dwconv_silu      p2o_dwconv, then p2_swish's AVX2 body (tensor_ops.c:437-463) over the channel-major result */
+void p2o_combine_softmax(float *ac, const float *bd, int H, int T, float scale);
+void p2o_glu_channel_major(const float *pw1, float *gated, int T, int D);
+void p2o_dwconv(const float *x, const float *w, const float *b, float *out, int D, int T, int K);
+void p2o_dwconv_silu(const float *x, const float *w, const float *b, float *out, int D, int T, int K);
+
 /* The mode latch's decision for given P2_GEMM / P2_EXACT strings (NULL = unset), without the CPU-feature clause
  * (blas.c:1032-1047). */
 int p2o_mode_from_env(const char *p2_gemm, const char *p2_exact);

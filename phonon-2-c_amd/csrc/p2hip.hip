@@ -579,12 +579,17 @@ static int produce(const char *name, int kind, p2k::ProdArgs a, bool vec, hipStr
     if (a.M < 0 || a.K < 0 || (a.M > 0 && a.K == 0) || a.K > P2H_PROD_KMAX)
         return fail(P2H_E_ARG, "%s: %d rows of %d columns (columns 1..%d)", name, a.M, a.K, P2H_PROD_KMAX);
     if (a.M == 0) return P2H_OK;
-    if (!a.X || !a.Q || !a.scales) return fail(P2H_E_ARG, "%s: null pointer", name);
-    if (a.ldq < p2h_q_ld(a.K) || a.ldq % P2H_Q_KALIGN != 0 || a.ldq > P2H_PROD_KMAX || !aligned(a.Q, 16))
-        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d, <= %d and a multiple of %d, Q 16-byte aligned", name,
-                    a.ldq, p2h_q_ld(a.K), P2H_PROD_KMAX, P2H_Q_KALIGN);
+    if (a.Y) {   /* fp32 rows: the row length picks the kernel's chunks as a quantised row's pitch would */
+        if (!a.X || a.ldy < a.K) return fail(P2H_E_ARG, "%s: null input or ldy < %d", name, a.K);
+        a.ldq = p2h_q_ld(a.K);
+    } else {
+        if (!a.X || !a.Q || !a.scales) return fail(P2H_E_ARG, "%s: null pointer", name);
+        if (a.ldq < p2h_q_ld(a.K) || a.ldq % P2H_Q_KALIGN != 0 || a.ldq > P2H_PROD_KMAX || !aligned(a.Q, 16))
+            return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d, <= %d and a multiple of %d, Q 16-byte aligned", name,
+                        a.ldq, p2h_q_ld(a.K), P2H_PROD_KMAX, P2H_Q_KALIGN);
+    }
     a.Mp = (int)align_up((size_t)a.M, 16);
-    if (kind == p2k::PROD_CMAJOR && a.K <= 1024 && a.ldq <= 1024) {   /* 16 rows per workgroup through LDS */
+    if (kind == p2k::PROD_CMAJOR && !a.Y && a.K <= 1024 && a.ldq <= 1024) {   /* 16 rows per workgroup via LDS */
         hipLaunchKernelGGL(p2k::cmajor_tile, dim3((unsigned)align_up((size_t)(a.Mp / 16), 16)), dim3(1024), 0, s, a);
         HIPCHK(hipGetLastError());
         return P2H_OK;
@@ -670,6 +675,133 @@ int p2h_channel_major_quant_rows(int D, int T, const float *dDW, signed char *dQ
     p2k::ProdArgs a{};
     a.M = T; a.K = D; a.X = dDW; a.T = T; a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
     return produce("p2h_channel_major_quant_rows", p2k::PROD_CMAJOR, a, false, stream_of(stream));
+}
+
+int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta, float *dY,
+                        int ldy, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (M > 0 && (ldx < D || !dGamma || !dBeta || !dY))
+        return fail(P2H_E_ARG, "p2h_layer_norm_rows: ldx = %d < D = %d or a null pointer", ldx, D);
+    if (M > 0 && dX != dY && ((const char *)dY < (const char *)(dX + (size_t)M * ldx) &&
+                              (const char *)dX < (const char *)(dY + (size_t)M * ldy)))
+        return fail(P2H_E_ARG, "p2h_layer_norm_rows: X and Y overlap without being the same rows");
+    if (M > 0 && dX == dY && ldx != ldy) return fail(P2H_E_ARG, "p2h_layer_norm_rows: in place needs ldy == ldx");
+    p2k::ProdArgs a{};
+    a.M = M; a.K = D; a.X = dX; a.ldx = ldx; a.gamma = dGamma; a.beta = dBeta; a.Y = dY; a.ldy = ldy;
+    return produce("p2h_layer_norm_rows", p2k::PROD_LN, a,
+                   D % 4 == 0 && ldx % 4 == 0 && aligned(dX, 16) && aligned(dGamma, 16) && aligned(dBeta, 16),
+                   stream_of(stream));
+}
+
+int p2h_concat_heads_rows(int T, const float *dAttnH, float *dY, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    p2k::ProdArgs a{};
+    a.M = T; a.K = p2k::kD; a.X = dAttnH; a.T = T; a.Dh = p2k::kDh; a.Y = dY; a.ldy = p2k::kD;
+    return produce("p2h_concat_heads_rows", p2k::PROD_HEADS, a, aligned(dAttnH, 16), stream_of(stream));
+}
+
+int p2h_channel_major_rows(int T, const float *dDW, float *dY, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    p2k::ProdArgs a{};
+    a.M = T; a.K = p2k::kD; a.X = dDW; a.T = T; a.Y = dY; a.ldy = p2k::kD;
+    return produce("p2h_channel_major_rows", p2k::PROD_CMAJOR, a, false, stream_of(stream));
+}
+
+/* ── the conformer block between its linears ─────────────────────────────────────────────────────────────────── */
+
+static unsigned blocks_of(size_t n) { return (unsigned)((n + 255) / 256); }
+
+int p2h_gather_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, float *dQu, float *dQv,
+                     float *dKt, float *dVh, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_gather_heads: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dQKV || !dBiasU || !dBiasV || !dQu || !dQv || !dKt || !dVh)
+        return fail(P2H_E_ARG, "p2h_gather_heads: null pointer");
+    hipStream_t s = stream_of(stream);
+    hipLaunchKernelGGL(p2k::gather_qv, dim3(blocks_of((size_t)T * p2k::kD)), dim3(256), 0, s, T, dQKV, dBiasU,
+                       dBiasV, dQu, dQv, dVh);
+    hipLaunchKernelGGL(p2k::head_transpose, dim3((unsigned)((T + 31) / 32), p2k::kH), dim3(256), 0, s, T,
+                       dQKV + p2k::kD, 3 * p2k::kD, dKt);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_transpose_pos(int L, const float *dP, float *dPt, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (L < 0) return fail(P2H_E_ARG, "p2h_transpose_pos: L = %d", L);
+    if (L == 0) return P2H_OK;
+    if (!dP || !dPt) return fail(P2H_E_ARG, "p2h_transpose_pos: null pointer");
+    hipLaunchKernelGGL(p2k::head_transpose, dim3((unsigned)((L + 31) / 32), p2k::kH), dim3(256), 0, stream_of(stream),
+                       L, dP, p2k::kD, dPt);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_combine_softmax(int T, float *dAC, const float *dBD, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_combine_softmax: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dAC || !dBD) return fail(P2H_E_ARG, "p2h_combine_softmax: null pointer");
+    const int rows = p2k::kH * T;
+    const float scale = 1.0f / sqrtf((float)p2k::kDh);   /* encoder.c:521; correctly rounded, as GCC folds it */
+    hipLaunchKernelGGL(p2k::combine_softmax_rows, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, stream_of(stream),
+                       rows, T, scale, dAC, dBD);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_glu_channel_major(int T, const float *dPW1, float *dGated, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_glu_channel_major: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dPW1 || !dGated) return fail(P2H_E_ARG, "p2h_glu_channel_major: null pointer");
+    hipLaunchKernelGGL(p2k::glu_channel_major, dim3((unsigned)((T + 31) / 32), p2k::kD / 64), dim3(256), 0,
+                       stream_of(stream), T, dPW1, dGated);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_depthwise_conv_silu(int T, const float *dGated, const float *dW, const float *dB, float *dOut, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_depthwise_conv_silu: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dGated || !dW || !dB || !dOut) return fail(P2H_E_ARG, "p2h_depthwise_conv_silu: null pointer");
+    if (dGated == dOut) return fail(P2H_E_ARG, "p2h_depthwise_conv_silu: in place is not supported");
+    hipLaunchKernelGGL(p2k::dwconv_silu, dim3((unsigned)((T + 255) / 256), p2k::kD), dim3(256), 0, stream_of(stream),
+                       T, dGated, dW, dB, dOut);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_silu(size_t n, float *dX, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (n == 0) return P2H_OK;
+    if (!dX) return fail(P2H_E_ARG, "p2h_silu: null pointer");
+    hipLaunchKernelGGL(p2k::silu_flat, dim3(blocks_of(n)), dim3(256), 0, stream_of(stream), n, dX);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_add_residual(int T, float *dX, const float *dY, float alpha, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_add_residual: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dX || !dY) return fail(P2H_E_ARG, "p2h_add_residual: null pointer");
+    const size_t n = (size_t)T * p2k::kD;
+    hipLaunchKernelGGL(p2k::axpy_rows, dim3(blocks_of(n)), dim3(256), 0, stream_of(stream), n, alpha, dY, dX);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
 }
 
 /* ── GEMMs ──────────────────────────────────────────────────────────────────────────────────────────────────── */
@@ -1336,6 +1468,176 @@ int p2h_sgemm(int transA, int transB, int M, int N, int K, float alpha, const fl
               const float *dB, int ldb, float beta, float *dC, int ldc, void *stream)
 {
     return p2h_sgemm_batched(transA, transB, M, N, K, alpha, dA, lda, 0, dB, ldb, 0, beta, dC, ldc, 0, 1, stream);
+}
+
+/* ── one conformer block on the device ───────────────────────────────────────────────────────────────────────── */
+
+namespace {
+
+/* The block's buffers in the caller's workspace, 256-byte aligned sections. With base == nullptr only the size. */
+struct BlockWs {
+    signed char *q; float *sc;                   /* quantised rows [T][≤ 4096] and their scales (int8 modes) */
+    float *h, *qkv, *qu, *qv, *kt, *vh, *p, *pt, *ac, *bd, *attn_h, *gated, *dw;
+    float *ln, *out, *attn;                      /* exact mode: fp32 rows */
+    void *gws; size_t gws_bytes;                 /* the GEMMs' own workspace */
+    size_t total;
+};
+
+size_t gemm_ws_bytes(int mode, int T)
+{
+    const int D = p2k::kD, FF = 4 * p2k::kD, L = 2 * T - 1;
+    const int shapes[6][2] = {{D, FF}, {FF, D}, {D, 3 * D}, {D, D}, {D, 2 * D}, {D, D}};
+    size_t need = p2h_fvb_workspace_bytes(mode, L, D, D);   /* the positional rows go through the fp32-input GEMM */
+    for (auto &sh : shapes) {
+        need = std::max(need, mode == P2H_EXACT ? p2h_fvb_workspace_bytes(mode, T, sh[1], sh[0])
+                                                : p2h_fvb_q8a_workspace_bytes(mode, T, sh[1], sh[0]));
+    }
+    return need;
+}
+
+BlockWs block_ws(int mode, int T, char *base)
+{
+    BlockWs w{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> char * {
+        char *p = base ? base + off : nullptr;
+        off += align_up(bytes, 256);
+        return p;
+    };
+    const size_t D = p2k::kD, Tz = (size_t)T, L = 2 * Tz - 1;
+    if (mode != P2H_EXACT) {
+        w.q = (signed char *)take(p2h_q_bytes(T, 4 * p2k::kD));
+        w.sc = (float *)take(4 * Tz);
+    } else {
+        w.ln = (float *)take(4 * Tz * D);
+        w.out = (float *)take(4 * Tz * D);
+        w.attn = (float *)take(4 * Tz * D);
+    }
+    w.h = (float *)take(4 * Tz * 4 * D);
+    w.qkv = (float *)take(4 * Tz * 3 * D);
+    w.qu = (float *)take(4 * Tz * D);
+    w.qv = (float *)take(4 * Tz * D);
+    w.kt = (float *)take(4 * Tz * D);
+    w.vh = (float *)take(4 * Tz * D);
+    w.p = (float *)take(4 * L * D);
+    w.pt = (float *)take(4 * L * D);
+    w.ac = (float *)take(4 * p2k::kH * Tz * Tz);
+    w.bd = (float *)take(4 * p2k::kH * Tz * L);
+    w.attn_h = (float *)take(4 * Tz * D);
+    w.gated = (float *)take(4 * D * Tz);
+    w.dw = (float *)take(4 * D * Tz);
+    w.gws_bytes = gemm_ws_bytes(mode, T);
+    w.gws = w.gws_bytes ? take(w.gws_bytes) : nullptr;
+    w.total = off;
+    return w;
+}
+
+int check_block_weight(const P2hWeight *w, int K, int N, const char *name)
+{
+    if (!w || w->K != K || w->N != N)
+        return fail(P2H_E_ARG, "p2h_conformer_block: %s must be a [%d, %d] five-value weight", name, K, N);
+    return P2H_OK;
+}
+
+}  // namespace
+
+size_t p2h_conformer_block_workspace_bytes(int mode, int T)
+{
+    if (ensure_init() || T <= 0 || (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)) return 0;
+    return block_ws(mode, T, nullptr).total;
+}
+
+int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, float *dX, void *workspace,
+                        size_t workspace_bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
+        return fail(P2H_E_ARG, "p2h_conformer_block: unknown mode %d", mode);
+    if (T <= 0 || !blk || !dPE || !dX) return fail(P2H_E_ARG, "p2h_conformer_block: T = %d or a null pointer", T);
+    const int D = p2k::kD, FF = 4 * p2k::kD, L = 2 * T - 1, Dh = p2k::kDh, H = p2k::kH;
+    {
+        const struct { const P2hWeight *w; int K, N; const char *name; } ws_[] = {
+            {blk->ff1_l1, D, FF, "ff1_l1"}, {blk->ff1_l2, FF, D, "ff1_l2"}, {blk->qkv, D, 3 * D, "qkv"},
+            {blk->pos, D, D, "pos"},        {blk->out, D, D, "out"},         {blk->pw1, D, 2 * D, "pw1"},
+            {blk->pw2, D, D, "pw2"},        {blk->ff2_l1, D, FF, "ff2_l1"}, {blk->ff2_l2, FF, D, "ff2_l2"}};
+        for (auto &x : ws_)
+            if (int rc = check_block_weight(x.w, x.K, x.N, x.name)) return rc;
+        const float *vecs[] = {blk->norm_ff1_w, blk->norm_ff1_b, blk->norm_sa_w,   blk->norm_sa_b,   blk->bias_u,
+                               blk->bias_v,     blk->norm_conv_w, blk->norm_conv_b, blk->dw_w,        blk->dw_b,
+                               blk->norm_ff2_w, blk->norm_ff2_b, blk->norm_out_w,  blk->norm_out_b};
+        for (const float *v : vecs)
+            if (!v) return fail(P2H_E_ARG, "p2h_conformer_block: a null norm, bias or convolution vector");
+    }
+    const BlockWs need = block_ws(mode, T, nullptr);
+    if (!workspace || workspace_bytes < need.total || !aligned(workspace, 256))
+        return fail(P2H_E_WORKSPACE, "p2h_conformer_block: workspace of %zu bytes (256-byte aligned) needed",
+                    need.total);
+    const BlockWs w = block_ws(mode, T, (char *)workspace);
+    hipStream_t s = stream_of(stream);
+    const int ldD = p2h_q_ld(D), ldF = p2h_q_ld(FF);
+#define P2H_TRY(call) do { if (int rc_ = (call)) return rc_; } while (0)
+    /* a linear from produced rows: quantised (int8 modes) or fp32 (exact) */
+    auto linear = [&](const P2hWeight *wt, int K, int N, float alpha, float beta, const float *rows, float *C) {
+        if (mode == P2H_EXACT)
+            return p2h_fvb_gemm(mode, T, N, K, alpha, rows, K, wt, beta, C, N, w.gws, w.gws_bytes, s);
+        return p2h_fvb_gemm_q8a(mode, T, N, K, alpha, w.q, K > D ? ldF : ldD, w.sc, wt, beta, C, N, w.gws,
+                                w.gws_bytes, s);
+    };
+    auto layer_norm = [&](const float *g, const float *b) {   /* x → the next linear's rows */
+        if (mode == P2H_EXACT) return p2h_layer_norm_rows(T, D, dX, D, g, b, w.ln, D, s);
+        return p2h_layer_norm_quant_rows(T, D, dX, D, g, b, w.q, ldD, w.sc, s);
+    };
+    /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
+    auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2) {
+        P2H_TRY(layer_norm(g, b));
+        P2H_TRY(linear(l1, D, FF, 1.0f, 0.0f, w.ln, w.h));
+        if (mode == P2H_EXACT) {
+            P2H_TRY(p2h_silu((size_t)T * FF, w.h, s));
+            P2H_TRY(linear(l2, FF, D, 1.0f, 0.0f, w.h, w.out));
+            return p2h_add_residual(T, dX, w.out, 0.5f, s);
+        }
+        P2H_TRY(p2h_silu_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
+        return linear(l2, FF, D, 0.5f, 1.0f, nullptr, dX);
+    };
+    P2H_TRY(feed_forward(blk->norm_ff1_w, blk->norm_ff1_b, blk->ff1_l1, blk->ff1_l2));
+    /* self_attention (encoder.c:471-541) */
+    P2H_TRY(layer_norm(blk->norm_sa_w, blk->norm_sa_b));
+    P2H_TRY(linear(blk->qkv, D, 3 * D, 1.0f, 0.0f, w.ln, w.qkv));
+    P2H_TRY(p2h_gather_heads(T, w.qkv, blk->bias_u, blk->bias_v, w.qu, w.qv, w.kt, w.vh, s));
+    P2H_TRY(p2h_fvb_gemm(mode, L, D, D, 1.0f, dPE, D, blk->pos, 0.0f, w.p, D, w.gws, w.gws_bytes, s));
+    P2H_TRY(p2h_transpose_pos(L, w.p, w.pt, s));
+    P2H_TRY(p2h_sgemm_batched(0, 0, T, T, Dh, 1.0f, w.qu, Dh, (long long)T * Dh, w.kt, T, (long long)Dh * T, 0.0f,
+                              w.ac, T, (long long)T * T, H, s));
+    P2H_TRY(p2h_sgemm_batched(0, 0, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, w.pt, L, (long long)Dh * L, 0.0f,
+                              w.bd, L, (long long)T * L, H, s));
+    P2H_TRY(p2h_combine_softmax(T, w.ac, w.bd, s));
+    P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.vh, Dh, (long long)T * Dh, 0.0f,
+                              w.attn_h, Dh, (long long)T * Dh, H, s));
+    if (mode == P2H_EXACT) {
+        P2H_TRY(p2h_concat_heads_rows(T, w.attn_h, w.attn, s));
+        P2H_TRY(linear(blk->out, D, D, 1.0f, 0.0f, w.attn, w.out));
+        P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
+    } else {
+        P2H_TRY(p2h_concat_heads_quant_rows(H, T, Dh, w.attn_h, w.q, ldD, w.sc, s));
+        P2H_TRY(linear(blk->out, D, D, 1.0f, 1.0f, nullptr, dX));
+    }
+    /* conv_module (encoder.c:573-613) */
+    P2H_TRY(layer_norm(blk->norm_conv_w, blk->norm_conv_b));
+    P2H_TRY(linear(blk->pw1, D, 2 * D, 1.0f, 0.0f, w.ln, w.h));
+    P2H_TRY(p2h_glu_channel_major(T, w.h, w.gated, s));
+    P2H_TRY(p2h_depthwise_conv_silu(T, w.gated, blk->dw_w, blk->dw_b, w.dw, s));
+    if (mode == P2H_EXACT) {
+        P2H_TRY(p2h_channel_major_rows(T, w.dw, w.attn, s));
+        P2H_TRY(linear(blk->pw2, D, D, 1.0f, 0.0f, w.attn, w.out));
+        P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
+    } else {
+        P2H_TRY(p2h_channel_major_quant_rows(D, T, w.dw, w.q, ldD, w.sc, s));
+        P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, nullptr, dX));
+    }
+    P2H_TRY(feed_forward(blk->norm_ff2_w, blk->norm_ff2_b, blk->ff2_l1, blk->ff2_l2));
+    P2H_TRY(p2h_layer_norm_rows(T, D, dX, D, blk->norm_out_w, blk->norm_out_b, dX, D, s));
+#undef P2H_TRY
+    return P2H_OK;
 }
 
 }  // extern "C"

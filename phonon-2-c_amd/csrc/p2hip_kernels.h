@@ -194,6 +194,7 @@ struct ProdArgs {
     int T, Dh;
     const float *gamma, *beta;                /* LN */
     int8_t *Q; int ldq; float *scales;
+    float *Y; int ldy;                        /* when set: the made rows as fp32 [M][ldy] instead of quantised rows */
 };
 
 /* e^x as the reference's AVX2 exp (tensor_ops.c:154-175) in IEEE operations: clamp to ±87, k = rint(x·log2e),
@@ -271,6 +272,7 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
     if (m >= a.Mp) return;
     const int K = a.K, kst = a.ldq / 64, k16 = K / 16 * 16;
     if (m >= a.M) {
+        if (a.Y) return;
         for (int k0 = 16 * lr; k0 < a.ldq; k0 += 16 * STRIDE)
             *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
         return;
@@ -398,6 +400,17 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
                 x[c][e] = (16 * (lane + 64 * c) + e < K) ? y : 0.0f;
             }
     }
+    if (a.Y) {   /* fp32 rows (the exact route's LayerNorm, SiLU, head concatenation and transpose) */
+        float *yr = a.Y + (size_t)m * a.ldy;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int k0 = 16 * (lr + STRIDE * c);
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                if (k0 + e < K) yr[k0 + e] = x[c][e];
+        }
+        return;
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; c++)
@@ -469,6 +482,158 @@ __global__ __launch_bounds__(1024) void cmajor_tile(ProdArgs a)
     const float inv = 1.0f / scale;
     if (k0 < a.ldq) *reinterpret_cast<uint4 *>(a.Q + q_index(m, k0, kst)) = quant16(x, k0, K, k16, scale, inv);
     if (lane == 0 && m < a.M) a.scales[m] = scale;
+}
+
+/* ── the conformer block between its linears (encoder.c:252-613): attention and convolution internals ────── */
+
+constexpr int kD = 1024, kH = 8, kDh = 128, kConvK = 9;   /* P2_D_MODEL, P2_N_HEADS, P2_HEAD_DIM, P2_CONV_KERNEL */
+
+/* The head gather of encoder.c:366-404 without its transpose: Q_u = Q + bias_u, Q_v = Q + bias_v and V as [H, T, Dh]
+ * from the fused rows QKV [T, 3D] (q | k | v). One thread per element, consecutive threads along d. */
+__global__ __launch_bounds__(256) void gather_qv(int T, const float *__restrict__ qkv, const float *__restrict__ bu,
+                                                 const float *__restrict__ bv, float *__restrict__ qu,
+                                                 float *__restrict__ qv, float *__restrict__ vh)
+{
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)T * kD) return;
+    const int t = (int)(idx / kD), c = (int)(idx % kD), h = c / kDh, d = c % kDh;
+    const float *row = qkv + (size_t)t * 3 * kD;
+    const float q = row[c];
+    const size_t o = ((size_t)h * T + t) * kDh + d;
+    qu[o] = __fadd_rn(q, bu[c]);
+    qv[o] = __fadd_rn(q, bv[c]);
+    vh[o] = row[2 * kD + c];
+}
+
+/* Per head transposed: dst[h][d][r] = src[r·ld + h·Dh + d] for r < rows (the keys of gather_heads, encoder.c:397-398,
+ * and transpose_pos, encoder.c:406-423). A 32-row × 128-column tile of one head through LDS: reads along d, writes
+ * along r. */
+__global__ __launch_bounds__(256) void head_transpose(int rows, const float *__restrict__ src, int ld,
+                                                      float *__restrict__ dst)
+{
+    __shared__ float tile[kDh][33];
+    const int r0 = blockIdx.x * 32, h = blockIdx.y, tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int idx = tid + 256 * i, rl = idx / kDh, d = idx % kDh;
+        if (r0 + rl < rows) tile[d][rl] = src[(size_t)(r0 + rl) * ld + h * kDh + d];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int idx = tid + 256 * i, d = idx / 32, rl = idx % 32;
+        if (r0 + rl < rows) dst[((size_t)h * kDh + d) * rows + r0 + rl] = tile[d][rl];
+    }
+}
+
+/* combine_softmax (encoder.c:425-450) with p2_softmax's AVX2 route (tensor_ops.c:354-413) in IEEE operations, eight
+ * threads per row of the [H·T, T] scores: thread q takes the row's elements j ≡ q (mod 8). a[j] = (ac[j] + bd[j +
+ * T − 1 − i]) · scale (the relative shift: row i of a head reads a window of its bd row); the maximum; for j below
+ * the last multiple of eight, e = exp_p2(a − max) added to running sum q in order of j (the eight vector lanes),
+ * the sums meeting as p2_hsum_avx2 does; the tail elements take expf and are added in order after them; then every
+ * element times 1/sum. */
+__global__ __launch_bounds__(256) void combine_softmax_rows(int rows, int T, float scale, float *__restrict__ ac,
+                                                            const float *__restrict__ bd)
+{
+    const int r = blockIdx.x * 32 + (threadIdx.x >> 3), q = threadIdx.x & 7;
+    const bool live = r < rows;
+    const int i = live ? r % T : 0, L = 2 * T - 1, body = T / 8 * 8;
+    float *a = ac + (size_t)(live ? r : 0) * T;
+    const float *b = bd + (size_t)(live ? r : 0) * L + (T - 1 - i);
+    float mx = -INFINITY;
+    if (live)
+        for (int j = q; j < T; j += 8) {
+            const float v = __fmul_rn(__fadd_rn(a[j], b[j]), scale);
+            a[j] = v;
+            mx = fmaxf(mx, v);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 8));
+    float lane_sum = 0.0f, tail = 0.0f;
+    if (live) {
+        for (int j = q; j < body; j += 8) {
+            const float e = exp_p2(__fsub_rn(a[j], mx));
+            a[j] = e;
+            lane_sum = __fadd_rn(lane_sum, e);
+        }
+        if (body + q < T) {
+            tail = expf(__fsub_rn(a[body + q], mx));
+            a[body + q] = tail;
+        }
+    }
+    /* p2_hsum_avx2: lanes q and q + 4, then q and q + 2, then 0 and 1 */
+    float s = __fadd_rn(lane_sum, __shfl_down(lane_sum, 4, 8));
+    s = __fadd_rn(s, __shfl_down(s, 2, 8));
+    s = __fadd_rn(s, __shfl_down(s, 1, 8));
+    s = __shfl(s, 0, 8);
+    for (int k = 0; k < T - body; k++) s = __fadd_rn(s, __shfl(tail, k, 8));
+    const float inv = __fdiv_rn(1.0f, s);
+    if (live)
+        for (int j = q; j < T; j += 8) a[j] = __fmul_rn(a[j], inv);
+}
+
+/* glu_to_channel_major (encoder.c:543-555): gated[d][t] = pw1[t][d] / (1 + expf(−pw1[t][D + d])), the exponent's
+ * argument clamped at 87 (p2_expneg, phonon2.h:38-41). A 32-frame × 64-channel tile through LDS: reads along d,
+ * writes along t. */
+__global__ __launch_bounds__(256) void glu_channel_major(int T, const float *__restrict__ pw1,
+                                                         float *__restrict__ gated)
+{
+    __shared__ float tile[64][33];
+    const int t0 = blockIdx.x * 32, d0 = blockIdx.y * 64, tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int idx = tid + 256 * i, tl = idx / 64, dl = idx % 64;
+        if (t0 + tl < T) {
+            const float *row = pw1 + (size_t)(t0 + tl) * 2 * kD;
+            const float g = row[kD + d0 + dl];
+            tile[dl][tl] = __fdiv_rn(row[d0 + dl], __fadd_rn(1.0f, expf(g < -87.0f ? 87.0f : -g)));
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int idx = tid + 256 * i, dl = idx / 32, tl = idx % 32;
+        if (t0 + tl < T) gated[(size_t)(d0 + dl) * T + t0 + tl] = tile[dl][tl];
+    }
+}
+
+/* p2_depthwise_conv1d (tensor_ops.c:559-648; kernel 9, padding 4, the BatchNorm folded into w and b) then p2_swish
+ * over the result (tensor_ops.c:437-491): per channel d and frame t, v = b[d], then v = fmaf(x[t − 4 + k], w[d][k],
+ * v) for the taps inside the sequence in order of k (the AVX2 route's fmadd chain; its scalar edges contract the
+ * same way), out = v · (1 / (1 + e^−v)) as silu_p2. Channel-major [D][T] in and out, one thread per frame. */
+__global__ __launch_bounds__(256) void dwconv_silu(int T, const float *__restrict__ x, const float *__restrict__ w,
+                                                   const float *__restrict__ bias, float *__restrict__ out)
+{
+    const int d = blockIdx.y, t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= T) return;
+    const float *xr = x + (size_t)d * T;
+    float v = bias[d];
+#pragma unroll
+    for (int k = 0; k < kConvK; k++) {
+        const int src = t - kConvK / 2 + k;
+        if (src >= 0 && src < T) v = __builtin_fmaf(xr[src], w[d * kConvK + k], v);
+    }
+    out[(size_t)d * T + t] = silu_p2(v);
+}
+
+/* p2_swish on a flat array in place (tensor_ops.c:437-491): elements below the last multiple of eight as silu_p2,
+ * the tail as x · p2_sigmoid(x) (expf clamped at 87, phonon2.h:38-46). */
+__global__ __launch_bounds__(256) void silu_flat(size_t n, float *__restrict__ x)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    if (i < n / 8 * 8) x[i] = silu_p2(v);
+    else x[i] = __fmul_rn(v, __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(v < -87.0f ? 87.0f : -v))));
+}
+
+/* add_residual (encoder.c:252-275): x += alpha · y as the AVX2 route's fmadd(y, alpha, x). */
+__global__ __launch_bounds__(256) void axpy_rows(size_t n, float alpha, const float *__restrict__ y,
+                                                 float *__restrict__ x)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = __builtin_fmaf(y[i], alpha, x[i]);
 }
 
 /* ── the int8 GEMM ─────────────────────────────────────────────────────────────────────────────────────────── */

@@ -85,6 +85,18 @@ _HIP_SIG = {
     "p2h_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
     "p2h_sgemm_batched": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, C.c_longlong, _vp, _i, C.c_longlong, _f, _vp, _i,
                                C.c_longlong, _i, _vp]),
+    "p2h_gather_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_transpose_pos": (_i, [_i, _vp, _vp, _vp]),
+    "p2h_combine_softmax": (_i, [_i, _vp, _vp, _vp]),
+    "p2h_glu_channel_major": (_i, [_i, _vp, _vp, _vp]),
+    "p2h_depthwise_conv_silu": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_silu": (_i, [_sz, _vp, _vp]),
+    "p2h_add_residual": (_i, [_i, _vp, _vp, _f, _vp]),
+    "p2h_layer_norm_rows": (_i, [_i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp]),
+    "p2h_concat_heads_rows": (_i, [_i, _vp, _vp, _vp]),
+    "p2h_channel_major_rows": (_i, [_i, _vp, _vp, _vp]),
+    "p2h_conformer_block_workspace_bytes": (_sz, [_i, _i]),
+    "p2h_conformer_block": (_i, [_i, _vp, _i, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _hip = None
@@ -561,6 +573,148 @@ def sgemm_batched(A, B, transA=False, transB=False, alpha=1.0, beta=0.0, C0=None
     return dC.download(C0.shape, np.float32)
 
 
+# ── the conformer block between its linears (model widths D = 1024, 8 heads of 128) ─────────────────────────────
+
+D_MODEL, N_HEADS, HEAD_DIM, CONV_K = 1024, 8, 128, 9
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def gather_heads(qkv, bias_u, bias_v):
+    """p2h_gather_heads on host arrays: QKV [T, 3072] → (Q_u, Q_v, V_h [8, T, 128], K_t [8, 128, T])."""
+    qkv = _f32(qkv)
+    T = qkv.shape[0]
+    dq, du, dv = to_device(qkv), to_device(_f32(bias_u)), to_device(_f32(bias_v))
+    outs = [DeviceBuffer(T * D_MODEL * 4) for _ in range(4)]
+    _ok(hip().p2h_gather_heads(T, dq.ptr, du.ptr, dv.ptr, outs[0].ptr, outs[1].ptr, outs[2].ptr, outs[3].ptr, None),
+        "p2h_gather_heads")
+    qu, qv, vh = (outs[i].download((N_HEADS, T, HEAD_DIM), np.float32) for i in (0, 1, 3))
+    return qu, qv, outs[2].download((N_HEADS, HEAD_DIM, T), np.float32), vh
+
+
+def transpose_pos(P):
+    P = _f32(P)
+    L = P.shape[0]
+    dP, dPt = to_device(P), DeviceBuffer(P.nbytes)
+    _ok(hip().p2h_transpose_pos(L, dP.ptr, dPt.ptr, None), "p2h_transpose_pos")
+    return dPt.download((N_HEADS, HEAD_DIM, L), np.float32)
+
+
+def combine_softmax(ac, bd):
+    """ac [8·T, T], bd [8·T, 2T−1] → softmax((ac + shift(bd)) / sqrt(128)) per row."""
+    ac = _f32(ac)
+    T = ac.shape[1]
+    dA, dB = to_device(ac), to_device(_f32(bd))
+    _ok(hip().p2h_combine_softmax(T, dA.ptr, dB.ptr, None), "p2h_combine_softmax")
+    return dA.download(ac.shape, np.float32)
+
+
+def glu_channel_major(pw1):
+    pw1 = _f32(pw1)
+    T = pw1.shape[0]
+    dP, dG = to_device(pw1), DeviceBuffer(T * D_MODEL * 4)
+    _ok(hip().p2h_glu_channel_major(T, dP.ptr, dG.ptr, None), "p2h_glu_channel_major")
+    return dG.download((D_MODEL, T), np.float32)
+
+
+def depthwise_conv_silu(gated, w, b):
+    gated = _f32(gated)
+    T = gated.shape[1]
+    dX, dW, dB, dO = to_device(gated), to_device(_f32(w)), to_device(_f32(b)), DeviceBuffer(gated.nbytes)
+    _ok(hip().p2h_depthwise_conv_silu(T, dX.ptr, dW.ptr, dB.ptr, dO.ptr, None), "p2h_depthwise_conv_silu")
+    return dO.download(gated.shape, np.float32)
+
+
+def silu(x):
+    x = _f32(x)
+    d = to_device(x)
+    _ok(hip().p2h_silu(x.size, d.ptr, None), "p2h_silu")
+    return d.download(x.shape, np.float32)
+
+
+def add_residual(X, Y, alpha):
+    X = _f32(X)
+    dX, dY = to_device(X), to_device(_f32(Y))
+    _ok(hip().p2h_add_residual(X.shape[0], dX.ptr, dY.ptr, alpha, None), "p2h_add_residual")
+    return dX.download(X.shape, np.float32)
+
+
+def layer_norm_rows(X, gamma, beta, in_place=False):
+    X = _f32(X)
+    M, D = X.shape
+    dX, dg, db = to_device(X), to_device(_f32(gamma)), to_device(_f32(beta))
+    dY = dX if in_place else DeviceBuffer(X.nbytes)
+    _ok(hip().p2h_layer_norm_rows(M, D, dX.ptr, D, dg.ptr, db.ptr, dY.ptr, D, None), "p2h_layer_norm_rows")
+    return dY.download(X.shape, np.float32)
+
+
+def concat_heads_rows(attn_h):
+    attn_h = _f32(attn_h)
+    T = attn_h.shape[1]
+    dA, dY = to_device(attn_h), DeviceBuffer(T * D_MODEL * 4)
+    _ok(hip().p2h_concat_heads_rows(T, dA.ptr, dY.ptr, None), "p2h_concat_heads_rows")
+    return dY.download((T, D_MODEL), np.float32)
+
+
+def channel_major_rows(dw):
+    dw = _f32(dw)
+    T = dw.shape[1]
+    dA, dY = to_device(dw), DeviceBuffer(T * D_MODEL * 4)
+    _ok(hip().p2h_channel_major_rows(T, dA.ptr, dY.ptr, None), "p2h_channel_major_rows")
+    return dY.download((T, D_MODEL), np.float32)
+
+
+BLOCK_FIELDS = ("norm_ff1_w", "norm_ff1_b", "ff1_l1", "ff1_l2", "norm_sa_w", "norm_sa_b", "qkv", "pos", "out",
+                "bias_u", "bias_v", "norm_conv_w", "norm_conv_b", "pw1", "pw2", "dw_w", "dw_b", "norm_ff2_w",
+                "norm_ff2_b", "ff2_l1", "ff2_l2", "norm_out_w", "norm_out_b")
+BLOCK_LINEARS = {"ff1_l1": (1024, 4096), "ff1_l2": (4096, 1024), "qkv": (1024, 3072), "pos": (1024, 1024),
+                 "out": (1024, 1024), "pw1": (1024, 2048), "pw2": (1024, 1024), "ff2_l1": (1024, 4096),
+                 "ff2_l2": (4096, 1024)}
+
+
+class _P2hBlock(C.Structure):
+    _fields_ = [(f, C.c_void_p) for f in BLOCK_FIELDS]
+
+
+class Block:
+    """One conformer block's weights on the device (P2hBlock): `params` maps each vector name to a float32 array and
+    each linear name to (signs, flags, lo, hi)."""
+
+    def __init__(self, params):
+        self._keep = {}
+        vals = {}
+        for f in BLOCK_FIELDS:
+            if f in BLOCK_LINEARS:
+                K, N = BLOCK_LINEARS[f]
+                w = FvWeight(*params[f], K, N)
+                self._keep[f] = w
+                vals[f] = w.ptr
+            else:
+                d = to_device(_f32(params[f]))
+                self._keep[f] = d
+                vals[f] = d.ptr
+        self.c = _P2hBlock(**vals)
+
+    def run_dev(self, mode, T, dPE, dX, ws, stream=None):
+        _ok(hip().p2h_conformer_block(MODES.get(mode, mode), C.byref(self.c), T, dPE, dX, ws.ptr, ws.nbytes, stream),
+            "p2h_conformer_block")
+
+    def run(self, mode, x, pe):
+        """x [T, 1024] through the block; pe [2T−1, 1024]."""
+        x = _f32(x)
+        T = x.shape[0]
+        dX, dPE = to_device(x), to_device(_f32(pe))
+        ws = Workspace(block_workspace_bytes(mode, T))
+        self.run_dev(mode, T, dPE.ptr, dX.ptr, ws)
+        return dX.download(x.shape, np.float32)
+
+
+def block_workspace_bytes(mode, T):
+    return hip().p2h_conformer_block_workspace_bytes(MODES.get(mode, mode), T)
+
+
 # ── the generator ───────────────────────────────────────────────────────────────────────────────────────────────
 
 def gen():
@@ -601,3 +755,21 @@ def gen_i8_weight(seed, tensor_id, K, N):
     sc = np.empty(N, np.float32)
     gen().p2g_i8_weight(seed, tensor_id, K, N, q8.ctypes.data, sc.ctypes.data)
     return q8, sc
+
+
+def block_params(seed, tid0):
+    """Seeded synthetic weights of one conformer block in the shapes of P2hBlock: the nine five-value linears from
+    the generator (tensor ids tid0 .. tid0 + 8), norms gamma ~ U(0.5, 1.5) and beta ~ U(−0.2, 0.2), bias_u / bias_v
+    ~ N(0, 0.1²), depthwise kernel ~ N(0, 0.3²) and bias ~ N(0, 0.1²)."""
+    rng = np.random.default_rng(seed * 1000 + tid0)
+    p = {}
+    for i, (name, (K, N)) in enumerate(BLOCK_LINEARS.items()):
+        p[name] = gen_fv_weight(seed, tid0 + i, K, N)
+    for name in ("norm_ff1", "norm_sa", "norm_conv", "norm_ff2", "norm_out"):
+        p[name + "_w"] = rng.uniform(0.5, 1.5, D_MODEL).astype(np.float32)
+        p[name + "_b"] = rng.uniform(-0.2, 0.2, D_MODEL).astype(np.float32)
+    p["bias_u"] = (rng.standard_normal(D_MODEL) * 0.1).astype(np.float32)
+    p["bias_v"] = (rng.standard_normal(D_MODEL) * 0.1).astype(np.float32)
+    p["dw_w"] = (rng.standard_normal(D_MODEL * CONV_K) * 0.3).astype(np.float32)
+    p["dw_b"] = (rng.standard_normal(D_MODEL) * 0.1).astype(np.float32)
+    return p

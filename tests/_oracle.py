@@ -52,6 +52,10 @@ def lib():
             "p2o_silu_quant_rows": [_f32p, _i, _i, _i, _i8p, _f32p],
             "p2o_concat_heads_quant_rows": [_f32p, _i, _i, _i, _i8p, _f32p],
             "p2o_channel_major_quant_rows": [_f32p, _i, _i, _i8p, _f32p],
+            "p2o_combine_softmax": [_f32p, _f32p, _i, _i, _f],
+            "p2o_glu_channel_major": [_f32p, _f32p, _i, _i],
+            "p2o_dwconv": [_f32p, _f32p, _f32p, _f32p, _i, _i, _i],
+            "p2o_dwconv_silu": [_f32p, _f32p, _f32p, _f32p, _i, _i, _i],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -306,3 +310,120 @@ def ref_swish_rows(X):
         ref().p2_swish(row.ctypes.data, row.size)
         out[m] = row
     return out
+
+
+# ── the conformer block between its linears ─────────────────────────────────────────────────────────────────────
+
+SCORE_SCALE = np.float32(1.0) / np.sqrt(np.float32(128.0), dtype=np.float32)   # 1/sqrtf(128), encoder.c:521
+
+
+def combine_softmax(ac, bd, H=8):
+    ac = _c(ac, np.float32).copy()
+    T = ac.shape[1]
+    lib().p2o_combine_softmax(ac, _c(bd, np.float32), H, T, float(SCORE_SCALE))
+    return ac
+
+
+def glu_channel_major(pw1, D=1024):
+    pw1 = _c(pw1, np.float32)
+    T = pw1.shape[0]
+    out = np.zeros((D, T), np.float32)
+    lib().p2o_glu_channel_major(pw1, out, T, D)
+    return out
+
+
+def dwconv(x, w, b, K=9):
+    x = _c(x, np.float32)
+    D, T = x.shape
+    out = np.zeros((D, T), np.float32)
+    lib().p2o_dwconv(x, _c(w, np.float32), _c(b, np.float32), out, D, T, K)
+    return out
+
+
+def dwconv_silu(x, w, b, K=9):
+    x = _c(x, np.float32)
+    D, T = x.shape
+    out = np.zeros((D, T), np.float32)
+    lib().p2o_dwconv_silu(x, _c(w, np.float32), _c(b, np.float32), out, D, T, K)
+    return out
+
+
+REFBLOCK_SO = os.path.join(ROOT, "oracle", "_ref", "libp2refblock.so")
+REFBLOCK_ORACLE_SO = os.path.join(ROOT, "oracle", "_ref", "libp2refblock_oracle.so")
+
+
+class RefFv(C.Structure):
+    _fields_ = [("signs", C.c_void_p), ("flags", C.c_void_p), ("lo", C.c_void_p), ("hi", C.c_void_p),
+                ("K", C.c_int), ("N", C.c_int)]
+
+
+_BLOCK_ORDER = [("norm_ff1_w", 0), ("norm_ff1_b", 0), ("ff1_l1", 1), ("ff1_l2", 1), ("norm_sa_w", 0),
+                ("norm_sa_b", 0), ("qkv", 1), ("pos", 1), ("out", 1), ("bias_u", 0), ("bias_v", 0),
+                ("norm_conv_w", 0), ("norm_conv_b", 0), ("pw1", 1), ("pw2", 1), ("dw_w", 0), ("dw_b", 0),
+                ("norm_ff2_w", 0), ("norm_ff2_b", 0), ("ff2_l1", 1), ("ff2_l2", 1), ("norm_out_w", 0),
+                ("norm_out_b", 0)]
+
+
+class RefBlock(C.Structure):
+    _fields_ = [(n, RefFv if fv else C.c_void_p) for n, fv in _BLOCK_ORDER]
+
+
+_refblock = {}
+
+
+def refblock(oracle_gemms=False):
+    """The reference's own conformer block (oracle/_ref/libp2refblock*.so, built from its encoder.c by
+    oracle/ref_block.c): with its blas.c (x86: the fp32 path) or with the oracle's quantised GEMMs (the int8 path in
+    the mode P2_GEMM names when the first GEMM runs; int8w when unset)."""
+    key = bool(oracle_gemms)
+    if key not in _refblock:
+        L = C.CDLL(REFBLOCK_ORACLE_SO if key else REFBLOCK_SO)
+        vp = C.c_void_p
+        L.refblock_run.argtypes = [C.POINTER(RefBlock), vp, vp, _i]
+        L.refblock_run.restype = _i
+        L.refblock_pos_encoding.argtypes = [_i, vp]
+        L.refblock_gather_heads.argtypes = [vp, vp, vp, vp, vp, vp, vp, _i]
+        L.refblock_transpose_pos.argtypes = [vp, vp, _i]
+        L.refblock_combine_softmax.argtypes = [vp, vp, _i]
+        L.refblock_concat_heads.argtypes = [vp, vp, _i]
+        L.refblock_glu.argtypes = [vp, vp, _i]
+        L.refblock_cm_to_rows.argtypes = [vp, vp, _i]
+        L.refblock_add_residual.argtypes = [vp, vp, _i, _f]
+        L.p2_depthwise_conv1d.argtypes = [vp, vp, vp, vp, _i, _i, _i]
+        L.p2_swish.argtypes = [vp, _i]
+        L.p2_layer_norm_rows_inplace.argtypes = [vp, vp, vp, _i, _i]
+        _refblock[key] = L
+    return _refblock[key]
+
+
+def refblock_available():
+    return os.path.exists(REFBLOCK_SO) and os.path.exists(REFBLOCK_ORACLE_SO)
+
+
+def ref_pos_encoding(T):
+    out = np.zeros((2 * T - 1, 1024), np.float32)
+    refblock().refblock_pos_encoding(T, out.ctypes.data)
+    return out
+
+
+def ref_block_run(params, x, pe, oracle_gemms=False):
+    """x [T, 1024] through the reference's conformer_block (encoder.c:617-625); params as for p2gemm.Block."""
+    x = _c(x, np.float32).copy()
+    T = x.shape[0]
+    keep, vals = [], {}
+    for n, fv in _BLOCK_ORDER:
+        if fv:
+            s, f, lo, hi = (_c(a, t) for a, t in zip(params[n], (np.uint8, np.uint8, np.float32, np.float32)))
+            keep += [s, f, lo, hi]
+            vals[n] = RefFv(s.ctypes.data, f.ctypes.data, lo.ctypes.data, hi.ctypes.data, hi.size and
+                            (s.size * 4 // hi.size), hi.size)
+        else:
+            a = _c(params[n], np.float32)
+            keep.append(a)
+            vals[n] = a.ctypes.data
+    blk = RefBlock(**vals)
+    pe = _c(pe, np.float32)
+    rc = refblock(oracle_gemms).refblock_run(C.byref(blk), pe.ctypes.data, x.ctypes.data, T)
+    if rc != 0:
+        raise RuntimeError("refblock_run failed")
+    return x

@@ -1,0 +1,189 @@
+"""The conformer block on the GPU (encoder.c:252-625): its pieces between the linears through the C ABI against the
+oracle, and one whole block (p2h_conformer_block) against the reference engine's own conformer_block built from its
+sources (oracle/_ref/libp2refblock*.so), on the seeded synthetic block of p2gemm.block_params.
+
+Pieces. Index moves (head gather, transposes, concatenation), the residual fmadd, the depthwise convolution with its
+SiLU, and the LayerNorm rows are bit-exact with the oracle: every operation is rounded once in the source's order on
+both sides. The softmax and the GLU call expf (the softmax for its last T mod 8 elements, the GLU everywhere); the
+device's expf and the host's libm may differ in the last place, so those are held to 4 ulp, and rows of the softmax
+without a tail (T % 8 == 0) are bit-exact.
+
+Whole block. int8w and int8: the reference block runs with the oracle's GEMMs (the reference's x86 blas.c has only
+the exact route, blas.c:1043-1045), which the device's GEMMs equal bit for bit on the same quantised rows. Between
+them the block's fp32 pieces may differ in the last bits (the reference's -ffast-math build divides through
+approximate reciprocals, reassociates the convolution's scalar edges, and its heads' fp32 GEMMs sum in another
+order), and a last-bit difference moves a quantisation code where a value sits on a rounding boundary; the final
+LayerNorm scales the output to unit variance. The bound: per frame, the relative L2 difference of the 1024 outputs
+is at most 2e-3 (a code moved by one in a few of a row's 1024 to 4096 inputs per linear), and over the block at most
+1e-3. exact: the reference block with the reference's own blas.c; no quantisation, so the bound is 2e-5 per frame.
+"""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import _oracle as O
+import p2gemm as P
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261202
+HERE = os.path.dirname(os.path.abspath(__file__))
+CHILD = os.path.join(HERE, "refblock_child.py")
+H, Dh, D = 8, 128, 1024
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    name = P.init()
+    assert name.startswith("gfx950"), name
+    return name
+
+
+def _ulps(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    spacing = np.spacing(np.abs(b)).astype(np.float64)
+    return np.abs(a.astype(np.float64) - b.astype(np.float64)) / np.maximum(spacing, np.finfo(np.float32).tiny)
+
+
+@pytest.mark.parametrize("T", [375, 17, 1])
+def test_gather_and_transposes(T):
+    print(f"gather/transpose T={T}", flush=True)
+    rng = np.random.default_rng(SEED + T)
+    qkv = rng.standard_normal((T, 3 * D)).astype(np.float32)
+    bu, bv = (rng.standard_normal(D) * 0.1).astype(np.float32), (rng.standard_normal(D) * 0.1).astype(np.float32)
+    qu, qv, kt, vh = P.gather_heads(qkv, bu, bv)
+    q, k, v = (qkv[:, i * D:(i + 1) * D].reshape(T, H, Dh) for i in range(3))
+    assert np.array_equal(qu, (q + bu.reshape(H, Dh)).transpose(1, 0, 2))
+    assert np.array_equal(qv, (q + bv.reshape(H, Dh)).transpose(1, 0, 2))
+    assert np.array_equal(kt, k.transpose(1, 2, 0))
+    assert np.array_equal(vh, v.transpose(1, 0, 2))
+    L = 2 * T - 1
+    Pm = rng.standard_normal((L, D)).astype(np.float32)
+    assert np.array_equal(P.transpose_pos(Pm), Pm.reshape(L, H, Dh).transpose(1, 2, 0))
+    attn_h = rng.standard_normal((H, T, Dh)).astype(np.float32)
+    assert np.array_equal(P.concat_heads_rows(attn_h), attn_h.transpose(1, 0, 2).reshape(T, D))
+    dw = rng.standard_normal((D, T)).astype(np.float32)
+    assert np.array_equal(P.channel_major_rows(dw), dw.T)
+
+
+@pytest.mark.parametrize("T", [376, 375, 9, 5, 1])
+def test_combine_softmax(T):
+    print(f"combine_softmax T={T}", flush=True)
+    rng = np.random.default_rng(SEED + 7 * T)
+    ac = (rng.standard_normal((H * T, T)) * 3).astype(np.float32)
+    bd = (rng.standard_normal((H * T, 2 * T - 1)) * 3).astype(np.float32)
+    ac[0, :] = -200.0   # a row far below zero: exp of (a − max) still sums from 1
+    got, ref = P.combine_softmax(ac, bd), O.combine_softmax(ac, bd)
+    if T % 8 == 0:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    else:
+        assert _ulps(got, ref).max() <= 4
+
+
+@pytest.mark.parametrize("T", [375, 7])
+def test_glu_channel_major(T):
+    print(f"glu T={T}", flush=True)
+    rng = np.random.default_rng(SEED + 11 * T)
+    pw1 = (rng.standard_normal((T, 2 * D)) * 2).astype(np.float32)
+    pw1[0, D:D + 4] = [-100.0, 100.0, -87.5, 88.0]
+    assert _ulps(P.glu_channel_major(pw1), O.glu_channel_major(pw1)).max() <= 4
+
+
+@pytest.mark.parametrize("T", [375, 300, 9, 4, 1])
+def test_depthwise_conv_silu(T):
+    print(f"depthwise_conv_silu T={T}", flush=True)
+    rng = np.random.default_rng(SEED + 13 * T)
+    x = rng.standard_normal((D, T)).astype(np.float32)
+    w = (rng.standard_normal((D, 9)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    got = P.depthwise_conv_silu(x, w, b)
+    assert np.array_equal(got.view(np.uint32), O.dwconv_silu(x, w, b).view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [375 * 4096, 1001])
+def test_silu_flat(n):
+    """The eight-wide body bit-exact; the tail (n mod 8 elements, expf) within 4 ulp."""
+    print(f"silu n={n}", flush=True)
+    rng = np.random.default_rng(SEED + n)
+    x = (rng.standard_normal(n) * 4).astype(np.float32)
+    x[:6] = [0.0, 100.0, -100.0, 87.0, -87.5, 30.0]
+    x[-3:] = [-100.0, 0.5, -2.0]
+    got = P.silu(x)
+    ref = x.copy()
+    O.lib().p2o_swish_row(ref, n)
+    body = n // 8 * 8
+    assert np.array_equal(got[:body].view(np.uint32), ref[:body].view(np.uint32))
+    assert _ulps(got[body:], ref[body:]).max() <= 4
+
+
+def test_add_residual():
+    rng = np.random.default_rng(SEED + 5)
+    X, Y = (rng.standard_normal((37, D)).astype(np.float32) for _ in range(2))
+    ref = (Y.astype(np.float64) * 0.5 + X.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(P.add_residual(X, Y, 0.5), ref)
+
+
+@pytest.mark.parametrize("M", [375, 6000, 3])
+def test_layer_norm_rows(M):
+    print(f"layer_norm_rows M={M}", flush=True)
+    rng = np.random.default_rng(SEED + M)
+    X = (rng.standard_normal((M, D)) * 1.7 + 0.3).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    b = rng.uniform(-0.2, 0.2, D).astype(np.float32)
+    ref = O.layer_norm_rows(X, g, b)
+    assert np.array_equal(P.layer_norm_rows(X, g, b).view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(P.layer_norm_rows(X, g, b, in_place=True).view(np.uint32), ref.view(np.uint32))
+
+
+# ── the whole block ───────────────────────────────────────────────────────────────────────────────────────────
+
+_BLOCK = {}
+
+
+def _device_block(seed):
+    if seed not in _BLOCK:
+        _BLOCK.clear()
+        sys.path.insert(0, HERE)
+        _BLOCK[seed] = P.Block(P.block_params(seed, 100))
+    return _BLOCK[seed]
+
+
+def _reference_block(mode, seed, T, tmp_path):
+    """The reference's conformer_block in a child process: the GEMM mode is latched once per process."""
+    out = tmp_path / f"ref_{mode}_{seed}_{T}.npy"
+    env = dict(os.environ)
+    env["P2_GEMM"] = mode
+    env.pop("P2_EXACT", None)
+    gemms = "reference" if mode == "exact" else "oracle"
+    r = subprocess.run([sys.executable, CHILD, str(seed), str(T), str(out), gemms], env=env, capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    return np.load(out)
+
+
+@pytest.mark.skipif(not O.refblock_available(), reason="reference block library not built")
+@pytest.mark.parametrize("mode,T", [("int8w", 375), ("int8", 375), ("exact", 375), ("int8w", 40), ("exact", 9)])
+def test_block_against_reference(mode, T, tmp_path):
+    print(f"conformer block mode={mode} T={T}", flush=True)
+    sys.path.insert(0, HERE)
+    import refblock_child as RC
+    ref = _reference_block(mode, SEED, T, tmp_path)
+    x, pe = RC.block_input(SEED, T)
+    got = _device_block(SEED).run(mode, x, pe)
+    assert np.isfinite(got).all()
+    diff = (got - ref).astype(np.float64)
+    row_rel = np.linalg.norm(diff, axis=1) / np.linalg.norm(ref.astype(np.float64), axis=1)
+    total_rel = np.linalg.norm(diff) / np.linalg.norm(ref.astype(np.float64))
+    print(f"  per-frame rel max {row_rel.max():.3g}, block rel {total_rel:.3g}, max |d| {np.abs(diff).max():.3g}",
+          flush=True)
+    if mode == "exact":
+        assert row_rel.max() <= 2e-5
+    else:
+        assert row_rel.max() <= 2e-3 and total_rel <= 1e-3
+    # the same block in another mode is far outside these bounds: the comparison sees the GEMM route
+    if mode == "int8w" and T == 375:
+        other = _device_block(SEED).run("exact", x, pe)
+        assert np.linalg.norm(other - ref) / np.linalg.norm(ref) > 3e-3
