@@ -6,7 +6,9 @@
  *  points over those functions with plain pointers:
  *
  *    refblock_run              conformer_block (encoder.c:617-625) on x [T, 1024] in place, with the positional
- *                              rows pe [2T−1, 1024]; five-value weights as their sign/flag planes and lo/hi
+ *                              rows pe [2T−1, 1024]; five-value weights as their sign/flag planes and lo/hi; or
+ *                              one of its five steps (stage 0..4: feed_forward, self_attention, conv_module,
+ *                              feed_forward, the final LayerNorm)
  *    refblock_pos_encoding     rel_pos_encoding (encoder.c:79-96), into a caller buffer
  *    refblock_gather_heads     gather_heads (encoder.c:366-404)
  *    refblock_transpose_pos    transpose_pos (encoder.c:406-423)
@@ -56,26 +58,39 @@ static Weight fv_weight_of(RefFv w)
     return x;
 }
 
-int refblock_run(const RefBlock *b, const float *pe, float *x, int T)
+static void block_of(const RefBlock *b, ConformerBlock *blk)
+{
+    memset(blk, 0, sizeof *blk);
+    blk->norm_ff1_w = b->norm_ff1_w; blk->norm_ff1_b = b->norm_ff1_b;
+    blk->ff1.linear1_w = fv_weight_of(b->ff1_l1); blk->ff1.linear2_w = fv_weight_of(b->ff1_l2);
+    blk->norm_sa_w = b->norm_sa_w; blk->norm_sa_b = b->norm_sa_b;
+    blk->mha.qkv_w = fv_weight_of(b->qkv); blk->mha.pos_w = fv_weight_of(b->pos); blk->mha.out_w = fv_weight_of(b->out);
+    blk->mha.bias_u = b->bias_u; blk->mha.bias_v = b->bias_v;
+    blk->norm_conv_w = b->norm_conv_w; blk->norm_conv_b = b->norm_conv_b;
+    blk->conv.pw1_w = fv_weight_of(b->pw1); blk->conv.pw2_w = fv_weight_of(b->pw2);
+    blk->conv.dw_w = b->dw_w; blk->conv.dw_b = b->dw_b;
+    blk->norm_ff2_w = b->norm_ff2_w; blk->norm_ff2_b = b->norm_ff2_b;
+    blk->ff2.linear1_w = fv_weight_of(b->ff2_l1); blk->ff2.linear2_w = fv_weight_of(b->ff2_l2);
+    blk->norm_out_w = b->norm_out_w; blk->norm_out_b = b->norm_out_b;
+}
+
+/* stage < 0: the whole block; 0..4: one of its five steps (encoder.c:619-623) on x */
+int refblock_run(const RefBlock *b, const float *pe, float *x, int T, int stage)
 {
     ConformerBlock blk;
-    memset(&blk, 0, sizeof blk);
-    blk.norm_ff1_w = b->norm_ff1_w; blk.norm_ff1_b = b->norm_ff1_b;
-    blk.ff1.linear1_w = fv_weight_of(b->ff1_l1); blk.ff1.linear2_w = fv_weight_of(b->ff1_l2);
-    blk.norm_sa_w = b->norm_sa_w; blk.norm_sa_b = b->norm_sa_b;
-    blk.mha.qkv_w = fv_weight_of(b->qkv); blk.mha.pos_w = fv_weight_of(b->pos); blk.mha.out_w = fv_weight_of(b->out);
-    blk.mha.bias_u = b->bias_u; blk.mha.bias_v = b->bias_v;
-    blk.norm_conv_w = b->norm_conv_w; blk.norm_conv_b = b->norm_conv_b;
-    blk.conv.pw1_w = fv_weight_of(b->pw1); blk.conv.pw2_w = fv_weight_of(b->pw2);
-    blk.conv.dw_w = b->dw_w; blk.conv.dw_b = b->dw_b;
-    blk.norm_ff2_w = b->norm_ff2_w; blk.norm_ff2_b = b->norm_ff2_b;
-    blk.ff2.linear1_w = fv_weight_of(b->ff2_l1); blk.ff2.linear2_w = fv_weight_of(b->ff2_l2);
-    blk.norm_out_w = b->norm_out_w; blk.norm_out_b = b->norm_out_b;
+    block_of(b, &blk);
     CfmWS ws;
     ws.cap = conformer_ws_peak(T);
     ws.buf = (float *)malloc(ws.cap * sizeof(float));
     if (!ws.buf) return -1;
-    conformer_block(&blk, pe, x, T, &ws);
+    switch (stage) {
+    case 0: feed_forward(blk.norm_ff1_w, blk.norm_ff1_b, &blk.ff1, x, T, &ws); break;
+    case 1: self_attention(blk.norm_sa_w, blk.norm_sa_b, &blk.mha, pe, x, T, &ws); break;
+    case 2: conv_module(blk.norm_conv_w, blk.norm_conv_b, &blk.conv, x, T, &ws); break;
+    case 3: feed_forward(blk.norm_ff2_w, blk.norm_ff2_b, &blk.ff2, x, T, &ws); break;
+    case 4: p2_layer_norm_rows_inplace(x, blk.norm_out_w, blk.norm_out_b, T, P2_D_MODEL); break;
+    default: conformer_block(&blk, pe, x, T, &ws); break;
+    }
     free(ws.buf);
     return 0;
 }

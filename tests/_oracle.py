@@ -379,7 +379,7 @@ def refblock(oracle_gemms=False):
     if key not in _refblock:
         L = C.CDLL(REFBLOCK_ORACLE_SO if key else REFBLOCK_SO)
         vp = C.c_void_p
-        L.refblock_run.argtypes = [C.POINTER(RefBlock), vp, vp, _i]
+        L.refblock_run.argtypes = [C.POINTER(RefBlock), vp, vp, _i, _i]
         L.refblock_run.restype = _i
         L.refblock_pos_encoding.argtypes = [_i, vp]
         L.refblock_gather_heads.argtypes = [vp, vp, vp, vp, vp, vp, vp, _i]
@@ -406,8 +406,9 @@ def ref_pos_encoding(T):
     return out
 
 
-def ref_block_run(params, x, pe, oracle_gemms=False):
-    """x [T, 1024] through the reference's conformer_block (encoder.c:617-625); params as for p2gemm.Block."""
+def ref_block_run(params, x, pe, oracle_gemms=False, stage=-1):
+    """x [T, 1024] through the reference's conformer_block (encoder.c:617-625), or one of its five steps (stage 0..4,
+    encoder.c:619-623); params as for p2gemm.Block."""
     x = _c(x, np.float32).copy()
     T = x.shape[0]
     keep, vals = [], {}
@@ -423,7 +424,7 @@ def ref_block_run(params, x, pe, oracle_gemms=False):
             vals[n] = a.ctypes.data
     blk = RefBlock(**vals)
     pe = _c(pe, np.float32)
-    rc = refblock(oracle_gemms).refblock_run(C.byref(blk), pe.ctypes.data, x.ctypes.data, T)
+    rc = refblock(oracle_gemms).refblock_run(C.byref(blk), pe.ctypes.data, x.ctypes.data, T, stage)
     if rc != 0:
         raise RuntimeError("refblock_run failed")
     return x

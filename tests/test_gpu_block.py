@@ -11,11 +11,18 @@ without a tail (T % 8 == 0) are bit-exact.
 Whole block. int8w and int8: the reference block runs with the oracle's GEMMs (the reference's x86 blas.c has only
 the exact route, blas.c:1043-1045), which the device's GEMMs equal bit for bit on the same quantised rows. Between
 them the block's fp32 pieces may differ in the last bits (the reference's -ffast-math build divides through
-approximate reciprocals, reassociates the convolution's scalar edges, and its heads' fp32 GEMMs sum in another
-order), and a last-bit difference moves a quantisation code where a value sits on a rounding boundary; the final
-LayerNorm scales the output to unit variance. The bound: per frame, the relative L2 difference of the 1024 outputs
-is at most 2e-3 (a code moved by one in a few of a row's 1024 to 4096 inputs per linear), and over the block at most
-1e-3. exact: the reference block with the reference's own blas.c; no quantisation, so the bound is 2e-5 per frame.
+approximate reciprocals and reassociates the convolution's scalar edges; its heads' fp32 GEMMs sum in another
+order than the matrix cores), and a last-bit difference moves a quantisation code wherever a value sits on a
+rounding boundary; the steps after it carry the moved code on. The reference block itself, run on its input with
+every element moved one ulp, moves by 3.3e-3 (relative L2) at T = 375 on this block; the int8 and int8w blocks
+differ by 6e-3. So the whole quantised block is held to 1e-2 over the block and 2e-2 per frame, which catches
+wiring mistakes but not last-bit ones, and each step is also tested alone (test_block_step_against_reference):
+the other three steps' residual linears get all-zero weights, so both sides compute LayerNorm(x + step(x)) from the
+same x and a moved code stays a local effect. There the step's contribution agrees with the reference's to fp32
+rounding on most frames (median per frame at most 1e-4 of its size; measured 3e-7 to 2e-5), and on the frames where
+a code moved (one code of a 1024-element row is about 1e-3 of the row) within 1e-2.
+exact: the reference block with the reference's own blas.c, no quantisation: at most 2e-5 per frame, which holds
+every piece of the attention and convolution modules to fp32 rounding.
 """
 import os
 import subprocess
@@ -116,7 +123,7 @@ def test_silu_flat(n):
     O.lib().p2o_swish_row(ref, n)
     body = n // 8 * 8
     assert np.array_equal(got[:body].view(np.uint32), ref[:body].view(np.uint32))
-    assert _ulps(got[body:], ref[body:]).max() <= 4
+    assert body == n or _ulps(got[body:], ref[body:]).max() <= 4
 
 
 def test_add_residual():
@@ -151,21 +158,28 @@ def _device_block(seed):
     return _BLOCK[seed]
 
 
-def _reference_block(mode, seed, T, tmp_path):
-    """The reference's conformer_block in a child process: the GEMM mode is latched once per process."""
-    out = tmp_path / f"ref_{mode}_{seed}_{T}.npy"
+def _reference_block(mode, seed, T, tmp_path, stage=None):
+    """The reference's conformer_block in a child process (the GEMM mode is latched once per process)."""
+    out = tmp_path / f"ref_{mode}_{seed}_{T}_{stage}.npy"
     env = dict(os.environ)
     env["P2_GEMM"] = mode
     env.pop("P2_EXACT", None)
     gemms = "reference" if mode == "exact" else "oracle"
-    r = subprocess.run([sys.executable, CHILD, str(seed), str(T), str(out), gemms], env=env, capture_output=True,
-                       text=True, timeout=300)
+    args = [sys.executable, CHILD, str(seed), str(T), str(out), gemms] + ([] if stage is None else [str(stage)])
+    r = subprocess.run(args, env=env, capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     return np.load(out)
 
 
+def _distance(a, ref):
+    d = (a - ref).astype(np.float64)
+    r64 = ref.astype(np.float64)
+    return np.linalg.norm(d, axis=1) / np.linalg.norm(r64, axis=1), np.linalg.norm(d) / np.linalg.norm(r64)
+
+
 @pytest.mark.skipif(not O.refblock_available(), reason="reference block library not built")
-@pytest.mark.parametrize("mode,T", [("int8w", 375), ("int8", 375), ("exact", 375), ("int8w", 40), ("exact", 9)])
+@pytest.mark.parametrize("mode,T", [("int8w", 375), ("int8", 375), ("exact", 375), ("int8w", 40), ("exact", 9),
+                                    ("int8", 1)])
 def test_block_against_reference(mode, T, tmp_path):
     print(f"conformer block mode={mode} T={T}", flush=True)
     sys.path.insert(0, HERE)
@@ -174,16 +188,34 @@ def test_block_against_reference(mode, T, tmp_path):
     x, pe = RC.block_input(SEED, T)
     got = _device_block(SEED).run(mode, x, pe)
     assert np.isfinite(got).all()
-    diff = (got - ref).astype(np.float64)
-    row_rel = np.linalg.norm(diff, axis=1) / np.linalg.norm(ref.astype(np.float64), axis=1)
-    total_rel = np.linalg.norm(diff) / np.linalg.norm(ref.astype(np.float64))
-    print(f"  per-frame rel max {row_rel.max():.3g}, block rel {total_rel:.3g}, max |d| {np.abs(diff).max():.3g}",
-          flush=True)
+    row_rel, total_rel = _distance(got, ref)
+    print(f"  per-frame max {row_rel.max():.3g}, block {total_rel:.3g}", flush=True)
     if mode == "exact":
         assert row_rel.max() <= 2e-5
     else:
-        assert row_rel.max() <= 2e-3 and total_rel <= 1e-3
-    # the same block in another mode is far outside these bounds: the comparison sees the GEMM route
-    if mode == "int8w" and T == 375:
-        other = _device_block(SEED).run("exact", x, pe)
-        assert np.linalg.norm(other - ref) / np.linalg.norm(ref) > 3e-3
+        assert row_rel.max() <= 2e-2 and total_rel <= 1e-2
+
+
+@pytest.mark.skipif(not O.refblock_available(), reason="reference block library not built")
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+@pytest.mark.parametrize("stage", [0, 1, 2, 3])
+def test_block_step_against_reference(mode, stage, tmp_path):
+    """One step of the block alone (the others' residual linears zero): the device's step contribution
+    LayerNorm⁻¹-free form — the block output minus LayerNorm(x) — against the reference's, per frame."""
+    print(f"conformer block step {stage} mode={mode} T=375", flush=True)
+    sys.path.insert(0, HERE)
+    import refblock_child as RC
+    T = 375
+    ref = _reference_block(mode, SEED, T, tmp_path, stage)
+    x, pe = RC.block_input(SEED, T)
+    params = RC.isolated_params(P.block_params(SEED, RC.BLOCK_TID0), stage)
+    got = P.Block(params).run(mode, x, pe)
+    base = O.layer_norm_rows(x, params["norm_out_w"], params["norm_out_b"])   # the block with the step removed
+    contrib = (ref - base).astype(np.float64)
+    d = (got - ref).astype(np.float64)
+    rel = np.linalg.norm(d, axis=1) / np.linalg.norm(contrib, axis=1)
+    print(f"  step contribution / output {np.linalg.norm(contrib) / np.linalg.norm(ref):.3g}; device vs reference "
+          f"per frame max {rel.max():.3g} median {np.median(rel):.3g} of the contribution", flush=True)
+    print(f"  percentiles 90 / 99: {np.percentile(rel, 90):.3g} / {np.percentile(rel, 99):.3g}", flush=True)
+    assert np.linalg.norm(contrib) > 1e-2 * np.linalg.norm(ref)   # the step does contribute
+    assert np.median(rel) <= 1e-4 and rel.max() <= 1e-2
