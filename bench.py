@@ -544,6 +544,7 @@ def main():
         extra["producers"] = producer_config(stream)
         extra["ffn_module375"] = ffn_module_config(stream)
         extra["block375"] = block_config(stream)
+        extra["conformer_block375"] = conformer_block_config(stream)
         extra["m38_rotated"] = m38_rotated_config(stream)
     sweep_ms = results["sweep"][1]["ms_per_step"] if "sweep" in results else None
 
@@ -777,6 +778,28 @@ def block_config(stream, T=375, steps=500, warmup=50):
     return {"ms_per_block": round(ms, 6), "ms_per_30s_window_24_blocks": round(24 * ms, 4),
             "tops": round(ops / (ms * 1e-3) / 1e12, 2), "kernels_per_block": 16,
             "what": f"T={T}: 8 producers + 8 five-value GEMMs (int8w), residuals in the epilogues"}
+
+
+def conformer_block_config(stream, T=375, steps=200, warmup=20):
+    """One whole conformer block on the device (p2h_conformer_block: encoder.c:617-625, every step between the
+    linears included — attention scores, relative shift and softmax, GLU, depthwise convolution and SiLU, the
+    LayerNorms, the positional projection of its 2T − 1 rows) on a seeded synthetic block, replayed from one graph;
+    x is carried from replay to replay (the final LayerNorm keeps it bounded). Per mode: ms per block and per 30 s
+    window of 24 blocks."""
+    params = P.block_params(SEED, 100)
+    blk = P.Block(params)
+    D = P.D_MODEL
+    x = P.to_device(P.gen_activations(SEED, 20_000 + T, T, D))
+    pe = P.to_device(P.gen_activations(SEED, 20_001 + T, 2 * T - 1, D))
+    res = {"what": f"T={T}: one device conformer block (9 five-value linears + attention + convolution module)"}
+    for mode in ("int8w", "exact"):
+        ws = P.Workspace(P.block_workspace_bytes(mode, T))
+        body = lambda m=mode, w=ws: blk.run_dev(m, T, pe.ptr, x.ptr, w, stream.ptr)
+        body()   # anything a first call prepares is made before the capture
+        stream.sync()
+        ms, _ = StepGraphs(stream, body, 1, steps).time(steps, warmup)
+        res[mode] = {"ms_per_block": round(ms, 5), "ms_per_30s_window_24_blocks": round(24 * ms, 4)}
+    return res
 
 
 def attention_config(stream, H=8, T=375, Dh=128, graph=True, reps=200):
