@@ -261,3 +261,73 @@ def test_alpha_zero_and_k_not_multiple_of_4():
     a = O.sgemm_fvb("int8w", A, signs, flags, lo, hi, 16)
     b = O.sgemm_fvb("exact", A, signs, flags, lo, hi, 16)
     assert np.array_equal(a, b)
+
+
+# ── the int8-table route (p2_sgemm_q8b, blas.c:1448-1460) ──────────────────────────────────────────────────────
+
+def _q8b_table(rng, K, N, ldb):
+    """An int8 table [K, ldb] whose first N columns are the weight codes; the columns beyond N hold values that
+    must never be read (a stride mistake picks them up)."""
+    B = rng.integers(-127, 128, (K, ldb)).astype(np.int8)
+    B[:, N:] = 127
+    scales = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    return B, scales
+
+
+def _q8b_run(M, N, K, alpha, q, sc, B, scales, beta_zero=True, C0=None):
+    C = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32).copy()
+    O.lib().p2o_gemm_q8b_run(M, N, K, alpha, np.ascontiguousarray(q, np.int8), np.ascontiguousarray(sc, np.float32),
+                             np.ascontiguousarray(B, np.int8), B.shape[1], np.ascontiguousarray(scales, np.float32),
+                             1 if beta_zero else 0, C, N)
+    return C
+
+
+@pytest.mark.parametrize("K,ldb", [(1024, 48), (2052, 40), (100, 32)])
+def test_q8b_run_float64_evaluation_strided_table(K, ldb):
+    """p2o_gemm_q8b_run against an int64 product folded in float64: C = alpha·a_scale[m]·scales[n]·Σ_k q·B, over a
+    table whose row stride ldb exceeds N (K > 1024 spans two of the per-1024-row blocks; K = 100 is one partial)."""
+    rng = _rng(40 + K)
+    M, N = 7, 32
+    B, scales = _q8b_table(rng, K, N, ldb)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    q, sc = O.quant_rows(A)
+    alpha = 0.625
+    C = _q8b_run(M, N, K, alpha, q, sc, B, scales)
+    acc = q.astype(np.int64) @ B[:, :N].astype(np.int64)
+    ref = acc.astype(np.float64) * scales.astype(np.float64)[None, :] * (sc.astype(np.float64) * alpha)[:, None]
+    assert np.allclose(C, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+    # the same product against a table packed to exactly N columns
+    assert np.array_equal(C, _q8b_run(M, N, K, alpha, q, sc, np.ascontiguousarray(B[:, :N]), scales))
+    # and beta = 1 adds onto C, block by block
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    acc_c = _q8b_run(M, N, K, alpha, q, sc, B, scales, beta_zero=False, C0=C0)
+    assert np.allclose(acc_c, C0 + ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8", "exact"])
+def test_sgemm_q8b_float64_evaluation(mode):
+    """p2o_sgemm_q8b (the public entry) with a strided table: the int8 modes quantise A and run the table route
+    (float64 of the quantised product); exact expands B·scales and runs the fp32 chain (float64 of A·W)."""
+    rng = _rng(50)
+    M, K, N, ldb = 6, 1536, 24, 40
+    B, scales = _q8b_table(rng, K, N, ldb)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    alpha = 1.5
+    C = O.sgemm_q8b(mode, A, B, scales, N, alpha=alpha)
+    if mode == "exact":
+        W = B[:, :N].astype(np.float32) * scales[None, :]
+        ref = alpha * (A.astype(np.float64) @ W.astype(np.float64))
+        assert np.allclose(C, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+    else:
+        q, sc = O.quant_rows(A)
+        acc = (q.astype(np.int64) @ B[:, :N].astype(np.int64)).astype(np.float64)
+        ref = acc * scales.astype(np.float64)[None, :] * (sc.astype(np.float64) * alpha)[:, None]
+        assert np.allclose(C, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+        # quantisation error bound against the fp32 product: ≤ (scale/2)·Σ|w| per output
+        W = np.abs(B[:, :N].astype(np.float64) * scales[None, :])
+        exact = alpha * (A.astype(np.float64) @ (B[:, :N].astype(np.float64) * scales[None, :]))
+        assert (np.abs(C - exact) <= alpha * (sc[:, None] / 2) * W.sum(axis=0)[None, :] + 1e-5).all()
+    # beta = 0.5 scales C first
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    Cb = O.sgemm_q8b(mode, A, B, scales, N, alpha=alpha, beta=0.5, C0=C0)
+    assert np.allclose(Cb, C + np.float32(0.5) * C0, rtol=1e-5, atol=1e-5)
