@@ -289,11 +289,51 @@ def summarize(linears, ms, qt, gt):
 
 
 def host_cores():
-    """Host cores this process may use (the GPU box's share), for the reference's thread pool."""
+    """Host cores this process may use, at most 16 (one GPU's share of its host), for the reference's thread pool."""
     try:
-        return len(os.sched_getaffinity(0))
+        n = len(os.sched_getaffinity(0))
     except AttributeError:
-        return os.cpu_count() or 1
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def engine_window(seconds=30.0, timeout=300):
+    """The reference engine's encoder on one 30 s window (encdump: its log-mel, p2_encoder, encoder.c:725-751) on a
+    synthetic model in its weights format (tests/e2e/model.py), wall time of p2_encoder: as the reference ships it
+    on this host's cores (encdump_cpu, exact: the x86 build's only GEMM route), and the same engine with its
+    quantised GEMMs bound to this library (encdump_gpu: every linear crosses PCIe both ways, the attention and
+    convolution steps stay on the CPU), int8w and exact. The first GPU-linked run moves the weights to the device;
+    the figure is the best of the runs after it."""
+    import re
+    import subprocess
+    import tempfile
+    exes = {v: os.path.join(ROOT, "oracle", "_ref", f"encdump_{v}") for v in ("cpu", "gpu")}
+    if not all(os.path.exists(e) for e in exes.values()):
+        return None
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from e2e import model
+    cores = host_cores()
+    res = {"cores": cores, "kind": "reference", "what": f"p2_encoder wall time, {seconds:g} s of synthetic audio"}
+    with tempfile.TemporaryDirectory() as d:
+        model.write_model(os.path.join(d, "model"))
+        wav = os.path.join(d, "a.wav")
+        model.write_wav(wav, seconds, seed=5)
+        for name, exe, env_mode, repeat in (("encdump_cpu_exact_ms", exes["cpu"], {"P2_EXACT": "1"}, 2),
+                                            ("encdump_gpu_int8w_ms", exes["gpu"], {"P2_GEMM": "int8w"}, 4),
+                                            ("encdump_gpu_exact_ms", exes["gpu"], {"P2_EXACT": "1"}, 4)):
+            env = {k: v for k, v in os.environ.items() if k not in ("P2_GEMM", "P2_EXACT", "P2H_EXACT_CHAIN")}
+            env.update(env_mode, P2_THREADS=str(cores), ENCDUMP_REPEAT=str(repeat))
+            try:
+                r = subprocess.run([exe, os.path.join(d, "model"), wav, os.path.join(d, "out.f32")],
+                                   capture_output=True, text=True, timeout=timeout, env=env)
+            except subprocess.TimeoutExpired:
+                res[name] = None
+                continue
+            ms = [float(x) for x in re.findall(r"^encoder_ms ([\d.]+)", r.stderr, re.M)]
+            res[name] = round(min(ms[1:]), 2) if r.returncode == 0 and len(ms) > 1 else None
+            if name.startswith("encdump_gpu") and len(ms) > 0:
+                res[name.replace("_ms", "_first_run_ms")] = round(ms[0], 2)
+    return res
 
 
 def cpu_baseline(M, shapes, seconds=8.0):
@@ -556,6 +596,7 @@ def main():
                 "exact375_1024x1024": cpu_baseline(375, [(1024, 1024)], seconds=4.0),
                 "ffn375_pair": cpu_baseline(375, [(1024, 4096), (4096, 1024)], seconds=4.0),
                 "bench_gemm_as_shipped": bench_gemm_as_shipped(),
+                "engine_30s_window": engine_window(),
             }
 
     line = {

@@ -86,6 +86,7 @@ typedef struct {
     void *dW;  size_t capW;     /* quantisation workspace */
     float *hq; size_t capq;     /* pinned host rows of the QuantA handed out by p2_quant_prepare */
     float *hs; size_t caps;     /* its scales array (never read: the GPU quantises) */
+    void *hp;  size_t capp;     /* pinned host rows: strided operands packed or unpacked on the way */
 } Ctx;
 
 static pthread_key_t ctx_key;
@@ -97,6 +98,7 @@ static void ctx_free(void *p)
     if (!c) return;
     p2h_free(c->dA); p2h_free(c->dB); p2h_free(c->dC); p2h_free(c->dW);
     p2h_host_free(c->hq);
+    p2h_host_free(c->hp);
     free(c->hs);
     p2h_stream_destroy(c->stream);
     free(c);
@@ -129,6 +131,33 @@ static void *dgrow(void **p, size_t *cap, size_t need, const char *who)
         *cap = n;
     }
     return *p;
+}
+
+static void *hgrow(Ctx *c, size_t need, const char *who)
+{
+    if (need > c->capp || !c->hp) {
+        p2h_host_free(c->hp);
+        size_t n = need < 4096 ? 4096 : need + need / 4;
+        c->hp = p2h_host_malloc(n);
+        if (!c->hp) die(who, p2h_last_error());
+        c->capp = n;
+    }
+    return c->hp;
+}
+
+/* rows of `width` bytes at host pitch `pitch` to a packed device buffer: one linear copy when the rows are packed,
+ * else packed into pinned host memory first (a 2-D copy from the host goes row by row, milliseconds for a few
+ * hundred rows) */
+static void h2d_rows(Ctx *c, void *d, const void *h, size_t width, size_t pitch, size_t rows, const char *who)
+{
+    if (pitch == width) {
+        check(p2h_memcpy_h2d(d, h, rows * width, c->stream), who);
+        return;
+    }
+    check(p2h_stream_sync(c->stream), who);   /* a copy from the pinned rows may still be in flight */
+    char *hp = (char *)hgrow(c, rows * width, who);
+    for (size_t r = 0; r < rows; r++) memcpy(hp + r * width, (const char *)h + r * pitch, width);
+    check(p2h_memcpy_h2d(d, hp, rows * width, c->stream), who);
 }
 
 /* ── the device weight cache ───────────────────────────────────────────────────────────────────────────────── */
@@ -312,24 +341,31 @@ static float *upload_f32(Ctx *c, void **slot, size_t *cap, const float *h, int r
 {
     size_t bytes = (size_t)rows * cols * sizeof(float);
     float *d = (float *)dgrow(slot, cap, bytes ? bytes : 4, who);
-    if (bytes)
-        check(p2h_memcpy2d_h2d(d, (size_t)cols * 4, h, (size_t)ld * 4, (size_t)cols * 4, (size_t)rows, c->stream),
-              who);
+    if (bytes) h2d_rows(c, d, h, (size_t)cols * 4, (size_t)ld * 4, (size_t)rows, who);
     return d;
 }
 
 static float *stage_c(Ctx *c, const float *C, int M, int N, int ldc, int need_old, const char *who)
 {
     float *d = (float *)dgrow(&c->dC, &c->capC, (size_t)M * N * sizeof(float) + 16, who);
-    if (need_old)
-        check(p2h_memcpy2d_h2d(d, (size_t)N * 4, C, (size_t)ldc * 4, (size_t)N * 4, (size_t)M, c->stream), who);
+    if (need_old) h2d_rows(c, d, C, (size_t)N * 4, (size_t)ldc * 4, (size_t)M, who);
     return d;
 }
 
+/* the packed device result into the caller's rows (pitch ldc), through pinned host memory when they are strided */
 static void finish_c(Ctx *c, float *C, const float *dC, int M, int N, int ldc, const char *who)
 {
-    check(p2h_memcpy2d_d2h(C, (size_t)ldc * 4, dC, (size_t)N * 4, (size_t)N * 4, (size_t)M, c->stream), who);
+    const size_t width = (size_t)N * 4, rows = (size_t)M;
+    if (ldc == N) {
+        check(p2h_memcpy_d2h(C, dC, rows * width, c->stream), who);
+        check(p2h_stream_sync(c->stream), who);
+        return;
+    }
+    check(p2h_stream_sync(c->stream), who);   /* a copy from the pinned rows may still be in flight */
+    char *hp = (char *)hgrow(c, rows * width, who);
+    check(p2h_memcpy_d2h(hp, dC, rows * width, c->stream), who);
     check(p2h_stream_sync(c->stream), who);
+    for (size_t r = 0; r < rows; r++) memcpy((char *)C + r * (size_t)ldc * 4, hp + r * width, width);
 }
 
 static void *workspace(Ctx *c, int mode, int M, int N, int K, size_t *bytes, const char *who)

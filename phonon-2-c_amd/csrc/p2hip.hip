@@ -259,7 +259,11 @@ int p2h_memcpy2d_h2d(void *dst, size_t dpitch, const void *src, size_t spitch, s
 {
     if (int rc = ensure_init()) return rc;
     if (rows == 0 || row_bytes == 0) return P2H_OK;
-    HIPCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, row_bytes, rows, hipMemcpyHostToDevice, stream_of(stream)));
+    if (dpitch == row_bytes && spitch == row_bytes)   /* packed rows: one linear copy (the 2-D copy goes row by row,
+                                                         about 3 ms for 375 rows whatever their length) */
+        HIPCHK(hipMemcpyAsync(dst, src, rows * row_bytes, hipMemcpyHostToDevice, stream_of(stream)));
+    else
+        HIPCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, row_bytes, rows, hipMemcpyHostToDevice, stream_of(stream)));
     return P2H_OK;
 }
 
@@ -268,7 +272,10 @@ int p2h_memcpy2d_d2h(void *dst, size_t dpitch, const void *src, size_t spitch, s
 {
     if (int rc = ensure_init()) return rc;
     if (rows == 0 || row_bytes == 0) return P2H_OK;
-    HIPCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, row_bytes, rows, hipMemcpyDeviceToHost, stream_of(stream)));
+    if (dpitch == row_bytes && spitch == row_bytes)
+        HIPCHK(hipMemcpyAsync(dst, src, rows * row_bytes, hipMemcpyDeviceToHost, stream_of(stream)));
+    else
+        HIPCHK(hipMemcpy2DAsync(dst, dpitch, src, spitch, row_bytes, rows, hipMemcpyDeviceToHost, stream_of(stream)));
     return P2H_OK;
 }
 

@@ -7,11 +7,22 @@
  *  usage: encdump <weights_dir> <mono 16 kHz wav> <out.f32>
  *  Writes T × 640 fp32 encoder frames (phonon2.h:395, encoder.c:725-751) to out.f32 and prints "T <T>" and the
  *  token ids of p2_greedy_decode (phonon2.h:407) on stdout.
+ *  ENCDUMP_REPEAT=n (default 1) runs p2_encoder n times on the same log-mel (the last run's frames are written) and
+ *  prints the wall time of each run on stderr as "encoder_ms <ms>"; the first run of a GPU-linked build includes
+ *  moving the weights to the device.
  */
 #include "phonon2.h"
 
 #include <stdio.h>
 #include <stdlib.h>
+#include <time.h>
+
+static double now_ms(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
+}
 
 int main(int argc, char **argv)
 {
@@ -33,7 +44,15 @@ int main(int argc, char **argv)
     const P2Model *m = p2_engine_model(e);
     float *enc = NULL;
     int T = 0;
-    if (p2_encoder(m, mel, frames, &enc, &T) != 0) return 1;
+    const char *rep = getenv("ENCDUMP_REPEAT");
+    const int repeat = rep && atoi(rep) > 0 ? atoi(rep) : 1;
+    for (int r = 0; r < repeat; r++) {
+        free(enc);
+        enc = NULL;
+        const double t0 = now_ms();
+        if (p2_encoder(m, mel, frames, &enc, &T) != 0) return 1;
+        fprintf(stderr, "encoder_ms %.3f\n", now_ms() - t0);
+    }
     FILE *f = fopen(argv[3], "wb");
     if (!f || fwrite(enc, sizeof(float), (size_t)T * P2_JOINT_DIM, f) != (size_t)T * P2_JOINT_DIM) return 1;
     fclose(f);
