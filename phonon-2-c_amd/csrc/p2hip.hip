@@ -758,8 +758,16 @@ int p2h_combine_softmax(int T, float *dAC, const float *dBD, void *stream)
     if (!dAC || !dBD) return fail(P2H_E_ARG, "p2h_combine_softmax: null pointer");
     const int rows = p2k::kH * T;
     const float scale = 1.0f / sqrtf((float)p2k::kDh);   /* encoder.c:521; correctly rounded, as GCC folds it */
-    hipLaunchKernelGGL(p2k::combine_softmax_rows, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, stream_of(stream),
-                       rows, T, scale, dAC, dBD);
+    hipStream_t s = stream_of(stream);
+    const dim3 wgrid((unsigned)((rows + 3) / 4));   /* one wave per row while the row fits its registers */
+    if (T <= 64 * 6) hipLaunchKernelGGL(p2k::combine_softmax_wave<6>, wgrid, dim3(256), 0, s, rows, T, scale, dAC, dBD);
+    else if (T <= 64 * 12)
+        hipLaunchKernelGGL(p2k::combine_softmax_wave<12>, wgrid, dim3(256), 0, s, rows, T, scale, dAC, dBD);
+    else if (T <= 64 * 32)
+        hipLaunchKernelGGL(p2k::combine_softmax_wave<32>, wgrid, dim3(256), 0, s, rows, T, scale, dAC, dBD);
+    else
+        hipLaunchKernelGGL(p2k::combine_softmax_rows, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, rows, T,
+                           scale, dAC, dBD);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -1484,7 +1492,7 @@ namespace {
 /* The block's buffers in the caller's workspace, 256-byte aligned sections. With base == nullptr only the size. */
 struct BlockWs {
     signed char *q; float *sc;                   /* quantised rows [T][≤ 4096] and their scales (int8 modes) */
-    float *h, *qkv, *qu, *qv, *kt, *vh, *p, *pt, *ac, *bd, *attn_h, *gated, *dw;
+    float *h, *qkv, *qu, *qv, *p, *ac, *bd, *attn_h, *gated, *dw;
     float *ln, *out, *attn;                      /* exact mode: fp32 rows */
     void *gws; size_t gws_bytes;                 /* the GEMMs' own workspace */
     size_t total;
@@ -1524,10 +1532,7 @@ BlockWs block_ws(int mode, int T, char *base)
     w.qkv = (float *)take(4 * Tz * 3 * D);
     w.qu = (float *)take(4 * Tz * D);
     w.qv = (float *)take(4 * Tz * D);
-    w.kt = (float *)take(4 * Tz * D);
-    w.vh = (float *)take(4 * Tz * D);
     w.p = (float *)take(4 * L * D);
-    w.pt = (float *)take(4 * L * D);
     w.ac = (float *)take(4 * p2k::kH * Tz * Tz);
     w.bd = (float *)take(4 * p2k::kH * Tz * L);
     w.attn_h = (float *)take(4 * Tz * D);
@@ -1610,15 +1615,19 @@ int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, 
     /* self_attention (encoder.c:471-541) */
     P2H_TRY(layer_norm(blk->norm_sa_w, blk->norm_sa_b));
     P2H_TRY(linear(blk->qkv, D, 3 * D, 1.0f, 0.0f, w.ln, w.qkv));
-    P2H_TRY(p2h_gather_heads(T, w.qkv, blk->bias_u, blk->bias_v, w.qu, w.qv, w.kt, w.vh, s));
+    /* Q_u, Q_v as [H, T, Dh] (the bias adds of gather_heads); the products read K, V and the positional rows where
+     * they lie, head h at column offset h·Dh of its row (the transposes of gather_heads and transpose_pos are only
+     * layouts for the reference's NN kernel; the sums are the same) */
+    hipLaunchKernelGGL(p2k::gather_qv, dim3((unsigned)(((size_t)T * D + 255) / 256)), dim3(256), 0, s, T, w.qkv,
+                       blk->bias_u, blk->bias_v, w.qu, w.qv, (float *)nullptr);
+    HIPCHK(hipGetLastError());
     P2H_TRY(p2h_fvb_gemm(mode, L, D, D, 1.0f, dPE, D, blk->pos, 0.0f, w.p, D, w.gws, w.gws_bytes, s));
-    P2H_TRY(p2h_transpose_pos(L, w.p, w.pt, s));
-    P2H_TRY(p2h_sgemm_batched(0, 0, T, T, Dh, 1.0f, w.qu, Dh, (long long)T * Dh, w.kt, T, (long long)Dh * T, 0.0f,
-                              w.ac, T, (long long)T * T, H, s));
-    P2H_TRY(p2h_sgemm_batched(0, 0, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, w.pt, L, (long long)Dh * L, 0.0f,
-                              w.bd, L, (long long)T * L, H, s));
+    P2H_TRY(p2h_sgemm_batched(0, 1, T, T, Dh, 1.0f, w.qu, Dh, (long long)T * Dh, w.qkv + D, 3 * D, Dh, 0.0f, w.ac, T,
+                              (long long)T * T, H, s));
+    P2H_TRY(p2h_sgemm_batched(0, 1, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, w.p, D, Dh, 0.0f, w.bd, L,
+                              (long long)T * L, H, s));
     P2H_TRY(p2h_combine_softmax(T, w.ac, w.bd, s));
-    P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.vh, Dh, (long long)T * Dh, 0.0f,
+    P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.qkv + 2 * D, 3 * D, Dh, 0.0f,
                               w.attn_h, Dh, (long long)T * Dh, H, s));
     if (mode == P2H_EXACT) {
         P2H_TRY(p2h_concat_heads_rows(T, w.attn_h, w.attn, s));

@@ -489,7 +489,8 @@ __global__ __launch_bounds__(1024) void cmajor_tile(ProdArgs a)
 constexpr int kD = 1024, kH = 8, kDh = 128, kConvK = 9;   /* P2_D_MODEL, P2_N_HEADS, P2_HEAD_DIM, P2_CONV_KERNEL */
 
 /* The head gather of encoder.c:366-404 without its transpose: Q_u = Q + bias_u, Q_v = Q + bias_v and V as [H, T, Dh]
- * from the fused rows QKV [T, 3D] (q | k | v). One thread per element, consecutive threads along d. */
+ * from the fused rows QKV [T, 3D] (q | k | v); V is skipped when vh is null (a caller whose product reads V in
+ * place). One thread per element, consecutive threads along d. */
 __global__ __launch_bounds__(256) void gather_qv(int T, const float *__restrict__ qkv, const float *__restrict__ bu,
                                                  const float *__restrict__ bv, float *__restrict__ qu,
                                                  float *__restrict__ qv, float *__restrict__ vh)
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(256) void gather_qv(int T, const float *__restrict_
     const size_t o = ((size_t)h * T + t) * kDh + d;
     qu[o] = __fadd_rn(q, bu[c]);
     qv[o] = __fadd_rn(q, bv[c]);
-    vh[o] = row[2 * kD + c];
+    if (vh) vh[o] = row[2 * kD + c];
 }
 
 /* Per head transposed: dst[h][d][r] = src[r·ld + h·Dh + d] for r < rows (the keys of gather_heads, encoder.c:397-398,
@@ -571,6 +572,68 @@ __global__ __launch_bounds__(256) void combine_softmax_rows(int rows, int T, flo
     const float inv = __fdiv_rn(1.0f, s);
     if (live)
         for (int j = q; j < T; j += 8) a[j] = __fmul_rn(a[j], inv);
+}
+
+/* combine_softmax_rows' arithmetic with one wave per row (T <= 64·NM), four rows per workgroup. The row's scores are
+ * read and written along j by all 64 lanes (lane l holds j = l + 64m in registers); the exponentials go to LDS by
+ * chain, element j at chain j mod 8, place j / 8, so that lanes 0..7 run the eight sums of the AVX2 route's lanes
+ * in order of j over contiguous float4 reads; the tail (expf) and p2_hsum_avx2's pairing follow on lane 0. Every
+ * operation and its order are those of combine_softmax_rows: the results are the same bits. */
+template <int NM>
+__global__ __launch_bounds__(256) void combine_softmax_wave(int rows, int T, float scale, float *__restrict__ ac,
+                                                            const float *__restrict__ bd)
+{
+    constexpr int S = 8 * NM + 4;   /* chain stride (floats): 64·NM / 8 places, 16 bytes of padding */
+    __shared__ __align__(16) float chains[4][8 * S];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r = blockIdx.x * 4 + w;
+    if (r >= rows) return;
+    const int i = r % T, L = 2 * T - 1, body = T / 8 * 8;
+    float *a = ac + (size_t)r * T;
+    const float *b = bd + (size_t)r * L + (T - 1 - i);
+    float v[NM];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const int j = lane + 64 * m;
+        v[m] = j < T ? __fmul_rn(__fadd_rn(a[j], b[j]), scale) : -INFINITY;
+        mx = fmaxf(mx, v[m]);
+    }
+    mx = wave_max_dpp(mx);
+    float *ch = chains[w];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const int j = lane + 64 * m;
+        if (j < body) v[m] = exp_p2(__fsub_rn(v[m], mx));
+        else if (j < T) v[m] = expf(__fsub_rn(v[m], mx));
+        if (j < T) ch[(j & 7) * S + (j >> 3)] = v[m];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    /* lane q < 8: the running sum of chain q over places 0 .. body/8 − 1 */
+    float p = 0.0f;
+    if (lane < 8) {
+        const float *cq = ch + lane * S;
+        const int n8 = body / 8;
+        int k = 0;
+        for (; k + 4 <= n8; k += 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(cq + k);
+            p = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(p, x.x), x.y), x.z), x.w);
+        }
+        for (; k < n8; k++) p = __fadd_rn(p, cq[k]);
+    }
+    float l8[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) l8[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), q));
+    float s = __fadd_rn(__fadd_rn(__fadd_rn(l8[0], l8[4]), __fadd_rn(l8[2], l8[6])),
+                        __fadd_rn(__fadd_rn(l8[1], l8[5]), __fadd_rn(l8[3], l8[7])));
+    for (int j = body; j < T; j++) s = __fadd_rn(s, ch[(j & 7) * S + (j >> 3)]);
+    const float inv = __fdiv_rn(1.0f, s);
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const int j = lane + 64 * m;
+        if (j < T) a[j] = __fmul_rn(v[m], inv);
+    }
 }
 
 /* glu_to_channel_major (encoder.c:543-555): gated[d][t] = pw1[t][d] / (1 + expf(−pw1[t][D + d])), the exponent's

@@ -76,8 +76,10 @@ def test_gather_and_transposes(T):
     assert np.array_equal(P.channel_major_rows(dw), dw.T)
 
 
-@pytest.mark.parametrize("T", [376, 375, 9, 5, 1])
+@pytest.mark.parametrize("T", [376, 375, 9, 5, 1, 700, 1030, 2100])
 def test_combine_softmax(T):
+    """One wave per row up to T = 2048 (the row in registers, 6, 12 or 32 values per lane), eight threads per row
+    beyond; the same bits either way."""
     print(f"combine_softmax T={T}", flush=True)
     rng = np.random.default_rng(SEED + 7 * T)
     ac = (rng.standard_normal((H * T, T)) * 3).astype(np.float32)
