@@ -742,11 +742,12 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=Tru
             if kt else None}
 
 
-def m38_rotated_config(stream, pairs=40, steps=50, warmup=5):
+def m38_rotated_config(stream, pairs=188, steps=20, warmup=3):
     """The 3 s utterance's FFN pair (M = 38: 1024 -> 4096, then 4096 -> 1024, int8w) over `pairs` independently seeded
-    weight pairs chained one after another (pair r's up-projection reads pair r - 1's output), so that the weights a
-    step touches (about 10 MB of device copies per pair, 400 MB in all) exceed the 256 MB Infinity Cache and stream
-    from HBM: the weight-streaming bound of the small-M path. One graph replay runs all pairs; reported per pair,
+    weight pairs chained one after another (pair r's up-projection reads pair r - 1's output): 188 pairs hold 602 MB
+    of packed planes (the reference's format) and 1.4 GB of device copies (planes, 4-bit records, column tables), far
+    beyond the 256 MB Infinity Cache, so the weights stream from HBM: the weight-streaming bound of the small-M path.
+    One graph replay runs all pairs; reported per pair,
     with GB/s on the packed planes (K·N·3/8 + 8N, the bytes the reference's format holds) and on the 4-bit operand
     records the kernels read (K·N/2 + 8N), against 8 TB/s."""
     M = 38

@@ -126,8 +126,8 @@ struct P2hWeight {
     const float *lo, *hi;
     uint8_t *clo;
     float *c1w, *c2;
-    uint8_t *rec;     /* operand records of the int8 routes (fv_repack): [N/16][units][64 lanes][12 B] */
-    uint8_t *rec4;    /* 4-bit selector records of the large-M GEMM (fv_repack4): [N/16][units][64 lanes][16 B] */
+    uint8_t *rec4;    /* 4-bit selector records, the operand of every GEMM route (fv_repack4):
+                         [N/16][units][64 lanes][16 B] */
     int units;        /* 128-row K units: K rounded up / 128 */
     void *own;        /* the one device allocation this handle made */
     size_t own_bytes;
@@ -391,7 +391,6 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     size_t off_c1 = off; off += align_up((size_t)N * 4, 256);
     size_t off_c2 = off; off += align_up((size_t)N * 4, 256);
     const int units = (K + 127) / 128;
-    size_t off_rec = off; off += align_up((size_t)(N / 16) * units * 768 + 16, 256);
     size_t off_rec4 = off; off += align_up((size_t)(N / 16) * units * 1024 + 16, 256);
     void *base = nullptr;
     if (hipMalloc(&base, off) != hipSuccess) {
@@ -410,7 +409,6 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     w->clo = b + off_clo;
     w->c1w = (float *)(b + off_c1);
     w->c2 = (float *)(b + off_c2);
-    w->rec = b + off_rec;
     w->rec4 = b + off_rec4;
     w->units = units;
     w->own = base;
@@ -426,9 +424,6 @@ static int weight_tables(P2hWeight *w)
     HIPCHK(hipGetLastError());
     const size_t recs = (size_t)(w->N / 16) * w->units * 64;
     if (recs > 0) {
-        hipLaunchKernelGGL(p2k::fv_repack, dim3((unsigned)((recs + 255) / 256)), dim3(256), 0, s, w->K, w->N,
-                           w->units, w->signs, w->flags, (uint32_t *)w->rec);
-        HIPCHK(hipGetLastError());
         hipLaunchKernelGGL(p2k::fv_repack4, dim3((unsigned)((recs + 255) / 256)), dim3(256), 0, s, w->K, w->N,
                            w->units, w->signs, w->flags, (uint4 *)w->rec4);
         HIPCHK(hipGetLastError());
@@ -607,11 +602,18 @@ static int produce(const char *name, int kind, p2k::ProdArgs a, bool vec, hipStr
     const int cus = g_cus > 0 ? g_cus : 256;
     const bool wide = kind != p2k::PROD_LN && a.K > 1024 && (a.Mp + 3) / 4 < cus;
     const dim3 grid((unsigned)(wide ? a.Mp : (a.Mp + 3) / 4)), block(256);
+    const bool ln_regs = a.Mp <= 2048;   /* LayerNorm's sums from registers when the rows are few */
     auto launch = [&](auto kind_tag, auto nch_tag, auto vec_tag) {
         constexpr int KIND = decltype(kind_tag)::value;
         if constexpr (KIND != p2k::PROD_LN) {
             if (wide) {   /* ldq <= 4096: one chunk per lane */
                 hipLaunchKernelGGL((p2k::produce_rows<KIND, 1, decltype(vec_tag)::value, 4>), grid, block, 0, s, a);
+                return;
+            }
+        } else if constexpr (decltype(nch_tag)::value == 1) {
+            if (ln_regs) {
+                hipLaunchKernelGGL((p2k::produce_rows<KIND, 1, decltype(vec_tag)::value, 1, true>), grid, block, 0, s,
+                                   a);
                 return;
             }
         }
@@ -863,9 +865,9 @@ using FvT6 = p2k::FvGeo<2, 1, 4, 6>;  /*  32 ×  64, 6 stages in flight */
 using FvW6 = p2k::FvGeo<6, 4, 4, 2>;  /*  96 × 256, 2 stages: K <= 1024 */
 using FvWK = p2k::FvGeo<6, 2, 4, 2>;  /*  96 × 128, 2 stages: K > 1024, unsplit (504 tiles at M = 6000, N = 1024) */
 /* Small-M tiles (gemm_fvs): operands straight to registers, K split across the four waves, 4-bit records */
-using SmS = p2k::SmGeo<2, 2, true>;     /*  32 ×  32 */
-using SmW = p2k::SmGeo<3, 4, true>;     /*  48 ×  64 (int8w) */
-using SmD = p2k::SmGeo<2, 4, true, 2, 8>;    /*  32 ×  64, eight waves of four units each, all in flight: K > 1024 (int8w) */
+using SmS = p2k::SmGeo<2, 2>;         /*  32 ×  32 */
+using SmW = p2k::SmGeo<3, 4>;         /*  48 ×  64 (int8w) */
+using SmD = p2k::SmGeo<2, 4, 2, 8>;   /*  32 ×  64, eight waves of four units each, all in flight: K > 1024 (int8w) */
 enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_WK = 9,
        FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_COUNT = 13 };
 const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
@@ -875,7 +877,6 @@ const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::
 /* gemm_fvs splits K among the four waves of a workgroup: at most four K segments, so K <= 4096 */
 inline bool small_ok(int K) { return K <= 4 * p2k::kFoldRows; }
 inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW || cfg == FV_SD; }
-inline bool uses_rec4(int cfg) { return cfg == FV_W6 || cfg == FV_WK || is_small(cfg); }
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -968,10 +969,10 @@ void launch_fv_large(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G::NT);
     if (g.K > p2k::kFoldRows)
-        hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, true, false, 2, true, true>), grid, block, 0,
+        hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, true, false, 2, true>), grid, block, 0,
                            s, g);
     else
-        hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, false, false, 2, true, true>), grid, block,
+        hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, false, false, 2, true>), grid, block,
                            0, s, g);
 }
 
@@ -1093,13 +1094,11 @@ static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed
     Plan p = make_plan(mode, M, N, K, workspace != nullptr);
     if (int rc = check_split_ws("p2h_fvb_gemm_q8a", p, workspace, workspace_bytes)) return rc;
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
-    g.rec = uses_rec4(p.cfg) ? w->rec4 : w->rec;
+    g.rec = w->rec4;
     g.units = w->units; g.clo = w->clo;
-    if (next && is_small(p.cfg)) {   /* the records the next call reads if it has this M */
-        const Plan pn = make_plan(mode, M, next->N, next->K, true);
-        const bool r4 = uses_rec4(pn.cfg);
-        const size_t bytes = (size_t)(next->N / 16) * next->units * (r4 ? 1024 : 768);
-        g.warm = r4 ? next->rec4 : next->rec;
+    if (next && is_small(p.cfg)) {   /* the records the next call reads */
+        const size_t bytes = (size_t)(next->N / 16) * next->units * 1024;
+        g.warm = next->rec4;
         g.warm_lines = (int)std::min<size_t>((bytes + 127) / 128, 0x7fffffff);
     }
     if (mode == P2H_INT8W) {
@@ -1202,14 +1201,16 @@ int p2h_fvb_acc_i32(int mode, int M, int N, int K, const signed char *dQ, int ld
     p.tiles_m = (M + FvL::BM - 1) / FvL::BM;
     p.tiles_n = (N + FvL::BN - 1) / FvL::BN;
     p2k::GemmArgs g = gemm_args(M, N, K, 1.0f, 0.0f, dQ, ldq, nullptr, nullptr, 0, p, nullptr);
-    g.rec = w->rec; g.units = w->units; g.clo = w->clo;
+    g.rec = w->rec4; g.units = w->units; g.clo = w->clo;
     g.acc1 = dAcc; g.acc2 = dAcc2; g.ldacc = ldacc;
     hipStream_t s = stream_of(stream);
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(FvL::NT);
     if (mode == P2H_INT8W)
-        hipLaunchKernelGGL((p2k::gemm_fv<FvL, p2k::MODE_INT8W, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<FvL, p2k::MODE_INT8W, p2k::OUT_ACC, false, false>), grid, block, 0,
+                           s, g);
     else
-        hipLaunchKernelGGL((p2k::gemm_fv<FvL, p2k::MODE_INT8, p2k::OUT_ACC, false, false>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((p2k::gemm_fv<FvL, p2k::MODE_INT8, p2k::OUT_ACC, false, false>), grid, block, 0, s,
+                           g);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }

@@ -9,7 +9,7 @@
  *                   across the waves of a workgroup, partial sums combined and folded through LDS
  *    gemm_exact     the exact route (blas.c:838-987): fp32 panels expanded in LDS, one fmaf chain per output
  *    fv_pack_codes  the reference's pre-packed int8w code layout (blas.c:1372-1400)
- *    fv_repack / fv_repack4  the planes re-laid per matrix-core operand (3 and 4 bits per weight) at upload
+ *    fv_repack4     the planes re-laid per matrix-core operand (4 bits per weight) at upload
  *    scale_c        C = beta · C (blas.c:60-70)
  */
 #pragma once
@@ -257,9 +257,9 @@ __global__ void recip_check(uint32_t lo, uint32_t hi, unsigned long long *out)
  *                the same for fmaf(d, d, ·) with d = x − mean; inv_std = 1/sqrtf(var + 1e-5), square root and
  *                quotient correctly rounded (__builtin_sqrtf; the v_sqrt_f32 behind __fsqrt_rn is not);
  *                y = fmaf((x − mean)·inv_std, gamma, beta). The row is staged in LDS for the eight sums.
- * NCH chunks of 16 columns per lane (ldq <= 1024·WPR·NCH). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
+ * NCH chunks of 16 columns per lane (ldq <= 1024·WPR·NCH). LNR: LayerNorm's sums from registers (below). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
  * ldx % 4 == 0 (LN: gamma and beta 16-byte aligned too); HEADS with Dh % 16 == 0; X 16-byte aligned. */
-template <int KIND, int NCH, bool VEC, int WPR = 1>
+template <int KIND, int NCH, bool VEC, int WPR = 1, bool LNR = false>
 __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
 {
     static_assert(WPR == 1 || (WPR == 4 && KIND != PROD_LN), "LayerNorm keeps one wave per row");
@@ -376,14 +376,37 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
             return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
                              __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
         };
+        /* LNR (NCH = 1, K = 1024 .. 1031: every LayerNorm of the encoder, chosen when the rows are few): each chain's
+         * 128 elements read into registers once, for both sums, with one wait; the chains then run without LDS round
+         * trips between batches. 4.5 against 5.3 us at 375 rows; at 6000 rows its 237 VGPRs cost occupancy (13.0
+         * against 11.3 us), so many rows take the LDS batches. */
+        float4 cv[LNR ? 32 : 1];
+        const bool whole = LNR && n8 == 128;
+        if (LNR && whole) {   /* lanes 8.. read chain lane % 8 again (broadcast reads), their sums unused */
+#pragma unroll
+            for (int u = 0; u < (LNR ? 32 : 1); u++)
+                cv[u] = *reinterpret_cast<const float4 *>(rt + (lane & 7) * S + 4 * u);
+        }
+        auto chain_regs = [&](auto add) {
+            float p = 0.0f;
+#pragma unroll
+            for (int u = 0; u < (LNR ? 32 : 1); u++) p = add(add(add(add(p, cv[u].x), cv[u].y), cv[u].z), cv[u].w);
+            float v8[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v8[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+            return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
+                             __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+        };
+        auto add_sum = [](float p, float v) { return __fadd_rn(p, v); };
         auto at = [&](int k) { return rt[(k & 7) * S + (k >> 3)]; };
-        float sum = chain([](float p, float v) { return __fadd_rn(p, v); });
+        float sum = whole ? chain_regs(add_sum) : chain(add_sum);
         for (int k = body; k < K; k++) sum = __fadd_rn(sum, at(k));
         const float mean = __fdiv_rn(sum, (float)K);
-        float var_sum = chain([mean](float p, float v) {
+        auto add_sq = [mean](float p, float v) {
             const float d = __fsub_rn(v, mean);
             return __builtin_fmaf(d, d, p);
-        });
+        };
+        float var_sum = whole ? chain_regs(add_sq) : chain(add_sq);
         for (int k = body; k < K; k++) {
             const float d = __fsub_rn(at(k), mean);
             var_sum = __builtin_fmaf(d, d, var_sum);
@@ -714,7 +737,7 @@ struct GemmArgs {
     int kq;                                               /* K rounded up to 128: Q columns that may be read */
     int splits, split_rows;                               /* K splits; rows per split (divides 1024) */
     int32_t *part;                                        /* split partials [planes][splits][M][N] */
-    const uint8_t *rec;                                   /* five-value operand records (fv_repack) */
+    const uint8_t *rec;                                   /* five-value operand records (fv_repack4) */
     int units;                                            /* 128-row K units of the records: K rounded up / 128 */
     int kst;                                              /* 64-column steps per 16-row group of Q: ldq / 64 */
     int mg_last, ng_last;                                 /* last 16-row group of Q, last 16-column group of C */
@@ -1181,44 +1204,13 @@ void gemm_i8(GemmArgs g)
 
 /* ── the five-value GEMM on operand records ──────────────────────────────────────────────────────────────────── */
 
-/* Five-value planes → operand records. Record (column group cg, unit u) holds for each of 64 lanes three dwords:
- * lane l serves column n = 16·cg + l % 16 and rows k = 128·u + 64·s + 16·(l / 16) + 4·d + b (s = 0, 1: the two
- * 64-row steps of the unit; d, b = 0..3), with
- *   dword s: byte b, bits 2d..2d+1 = the 2-bit sign code;   dword 2: byte b, bit d + 4s = the flag.
- * Rows k >= K hold code 1 (weight 0) and flag 0. Records are stored [N/16][units][64][3 dwords], so a 16-column
- * group streams along K, and one 64-lane load brings a whole operand's codes (3 bits per weight, as the planes). */
-__global__ void fv_repack(int K, int N, int units, const uint8_t *__restrict__ signs,
-                          const uint8_t *__restrict__ flags, uint32_t *__restrict__ rec)
-{
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)(N / 16) * units * 64) return;
-    const int l = (int)(idx % 64);
-    const size_t gu = idx / 64;
-    const int u = (int)(gu % units), cg = (int)(gu / units);
-    const int n = 16 * cg + (l & 15), kq = l >> 4;
-    uint32_t w[3] = {0u, 0u, 0u};
-    for (int s = 0; s < 2; s++)
-        for (int d = 0; d < 4; d++)
-            for (int b = 0; b < 4; b++) {
-                const int k = 128 * u + 64 * s + 16 * kq + 4 * d + b;
-                uint32_t code = 1u, flag = 0u;
-                if (k < K) {
-                    code = (signs[(size_t)k * (N / 4) + (n >> 2)] >> (2 * (n & 3))) & 3u;
-                    flag = (flags[(size_t)k * (N / 8) + (n >> 3)] >> (n & 7)) & 1u;
-                }
-                w[s] |= code << (8 * b + 2 * d);
-                w[2] |= flag << (8 * b + d + 4 * s);
-            }
-    rec[3 * idx] = w[0];
-    rec[3 * idx + 1] = w[1];
-    rec[3 * idx + 2] = w[2];
-}
-
-/* Five-value planes → 4-bit selector records, the operand layout of the large-M GEMM. Record (cg, u) holds 16 bytes
- * per lane l (column n = 16·cg + l % 16, rows k = 128·u + 64·s + 16·(l / 16) + 4·d + b as in fv_repack): dword
- * 2s + d/2, byte b, nibble d % 2 is the byte-permute selector code | flag << 2 of row k. Rows k >= K hold code 1 (weight
- * 0). Half a byte per weight: one 16-byte load per lane brings a whole 128-row unit, and an operand dword decodes with
- * one mask (and one shift for odd d) before the table permute. */
+/* Five-value planes → 4-bit selector records, the weight operand of every GEMM route. Record (column group cg, unit
+ * u) holds 16 bytes per lane l, which serves column n = 16·cg + l % 16 and rows k = 128·u + 64·s + 16·(l / 16) +
+ * 4·d + b (s = 0, 1: the two 64-row steps of the unit; d, b = 0..3): dword 2s + d/2, byte b, nibble d % 2 is the
+ * byte-permute selector code | flag << 2 of row k. Rows k >= K hold code 1 (weight 0). Records are stored
+ * [N/16][units][64][16 B], so a 16-column group streams along K. Half a byte per weight: one 16-byte load per lane
+ * brings a whole 128-row unit, and an operand dword decodes with one mask (and one shift for odd d) before the
+ * table permute. */
 __global__ void fv_repack4(int K, int N, int units, const uint8_t *__restrict__ signs,
                            const uint8_t *__restrict__ flags, uint4 *__restrict__ rec)
 {
@@ -1243,16 +1235,6 @@ __global__ void fv_repack4(int K, int N, int units, const uint8_t *__restrict__ 
     rec[idx] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-/* One 16-byte weight operand (64 rows × one column per lane, as the MFMA reads it) from a lane's record: 64-row step
- * s, sign dword S, flag dword F. Selector byte = code | flag << 2, then the column's code table (i8w_lo_table). */
-template <int STEP>
-__device__ __forceinline__ uint32_t fv_sel(uint32_t S, uint32_t F, int d)
-{
-    const int sh = d + 4 * STEP - 2;   /* moves flag bit d + 4s of each byte to bit 2 */
-    const uint32_t fl = (sh >= 0 ? (F >> sh) : (F << -sh)) & 0x04040404u;
-    return ((S >> (2 * d)) & 0x03030303u) | fl;
-}
-
 template <int FM_, int FN_, int NW_, int D_>
 struct FvGeo {
     static constexpr int FM = FM_, FN = FN_, NW = NW_, D = D_;
@@ -1268,18 +1250,13 @@ struct FvGeo {
     static_assert(D >= 2 && D * STAGE <= 160 * 1024, "LDS ring");
 };
 
-/* Direct global → LDS loads (16 or 12 bytes per lane into 16-byte lane slots at lds + 16·lane). Issued from inline
+/* Direct global → LDS loads (16 bytes per lane into 16-byte lane slots at lds + 16·lane). Issued from inline
  * assembly so that the compiler adds no waits of its own for them: the GEMM waits for them explicitly (wait_vm),
  * and the compiler's waits for its own loads stay correct since the vector-memory counter retires in order. */
 __device__ __forceinline__ void dma_16(const void *src, const void *lds)
 {
     const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
-}
-__device__ __forceinline__ void dma_12(const void *src, const void *lds)
-{
-    const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx3 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
 }
 
 /* s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left open); a compiler barrier for memory operations */
@@ -1303,7 +1280,7 @@ __device__ __forceinline__ void lds_barrier()
  *  Operands stream through a ring of D LDS stages (two 64-row steps each) by direct global→LDS loads: stage t + D − 1
  *  is requested while stage t is computed, with one barrier per stage and no register staging.
  *  Folding into fp32 is as in gemm_i8: per 1024-row block in registers, or int32 partials per split for fold_splits. */
-template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC, bool REC4, bool CSHUF>
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC, bool CSHUF>
 __device__ __forceinline__ void fv_tile(const GemmArgs &g)
 {
     constexpr bool TWO = (MODE == MODE_INT8);
@@ -1338,8 +1315,7 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
 #pragma unroll
     for (int i = 0; i < FN; i++) {
         const int cg = min((n0 >> 4) + wave * FN + i, g.ng_last);
-        b_src[i] = REC4 ? g.rec + ((size_t)cg * g.units + u_begin) * 1024 + lane * 16
-                        : g.rec + ((size_t)cg * g.units + u_begin) * 768 + lane * 12;
+        b_src[i] = g.rec + ((size_t)cg * g.units + u_begin) * 1024 + lane * 16;
         if (MODE == MODE_INT8W) lo_tab[i] = i8w_lo_table(g.clo[16 * cg + (lane & 15)]);
     }
     auto issue = [&](int t) {   /* stage t → ring slot t % D */
@@ -1348,8 +1324,7 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
         for (int q = 0; q < G::A_DMA; q++) dma_16(a_src[q] + (size_t)t * 2048, slot + a_dst[q]);
 #pragma unroll
         for (int i = 0; i < FN; i++) {
-            if (REC4) dma_16(b_src[i] + (size_t)t * 1024, slot + G::A_STAGE + (wave * FN + i) * 1024);
-            else dma_12(b_src[i] + (size_t)t * 768, slot + G::A_STAGE + (wave * FN + i) * 1024);
+            dma_16(b_src[i] + (size_t)t * 1024, slot + G::A_STAGE + (wave * FN + i) * 1024);
         }
     };
     /* epilogue factors: loaded before the first DMAs (so waiting for them waits for no DMA), into LDS before the
@@ -1458,13 +1433,8 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
         uint32_t rw[FN][4];
 #pragma unroll
         for (int i = 0; i < FN; i++) {
-            if (REC4) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(sb + i * 1024);
-                rw[i][0] = v.x; rw[i][1] = v.y; rw[i][2] = v.z; rw[i][3] = v.w;
-            } else {
-                const uint32_t *p = reinterpret_cast<const uint32_t *>(sb + i * 1024);
-                rw[i][0] = p[0]; rw[i][1] = p[1]; rw[i][2] = p[2]; rw[i][3] = 0u;
-            }
+            const uint4 v = *reinterpret_cast<const uint4 *>(sb + i * 1024);
+            rw[i][0] = v.x; rw[i][1] = v.y; rw[i][2] = v.z; rw[i][3] = v.w;
         }
         v4i av[2][FM];
 #pragma unroll
@@ -1480,8 +1450,7 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
             for (int i = 0; i < FN; i++)
 #pragma unroll
                 for (int d = 0; d < 4; d++) {
-                    const uint32_t sel = REC4 ? ((rw[i][2 * S + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u)
-                                              : fv_sel<S>(rw[i][S], rw[i][2], d);
+                    const uint32_t sel = (rw[i][2 * S + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u;
                     if (MODE == MODE_INT8W) {
                         bw[S][i][d] = (int)perm(kI8wHiTable, lo_tab[i], sel);
                     } else {
@@ -1623,10 +1592,10 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
     }
 }
 
-template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC = 1, bool REC4 = false, bool CSHUF = false>
+template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC = 1, bool CSHUF = false>
 __global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
 {
-    fv_tile<G, MODE, OUT, MULTI, SPLIT, OCC, REC4, CSHUF>(g);
+    fv_tile<G, MODE, OUT, MULTI, SPLIT, OCC, CSHUF>(g);
 }
 
 /* ── the small-M five-value GEMM ─────────────────────────────────────────────────────────────────────────────── */
@@ -1636,10 +1605,9 @@ __global__ __launch_bounds__(G::NT, OCC) void gemm_fv(GemmArgs g)
  * registers – the tiled activations and the operand records are already in matrix-core order – two 128-row units
  * per load batch, the next batch in flight while the current one is decoded and multiplied. No LDS staging and no
  * barrier in the K loop. */
-template <int FM_, int FN_, bool REC4_, int CH_ = 2, int W_ = 4>
+template <int FM_, int FN_, int CH_ = 2, int W_ = 4>
 struct SmGeo {
     static constexpr int FM = FM_, FN = FN_;
-    static constexpr bool REC4 = REC4_;
     static constexpr int BM = 16 * FM, BN = 16 * FN;
     static constexpr int WAVES = W_, NT = 64 * W_;
     static constexpr int PITCH = BN + 4;     /* int32 per row of a partial tile in LDS */
@@ -1671,14 +1639,7 @@ __device__ __forceinline__ void sm_unit_mma(const v4i (&a)[2][G::FM], const uint
         for (int i = 0; i < G::FN; i++)
 #pragma unroll
             for (int d = 0; d < 4; d++) {
-                uint32_t sel;
-                if (G::REC4) {
-                    sel = (r[i][2 * s + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u;
-                } else {
-                    const int sh = d + 4 * s - 2;
-                    const uint32_t fl = (sh >= 0 ? (r[i][2] >> sh) : (r[i][2] << -sh)) & 0x04040404u;
-                    sel = ((r[i][s] >> (2 * d)) & 0x03030303u) | fl;
-                }
+                const uint32_t sel = (r[i][2 * s + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u;
                 if (MODE == MODE_INT8W) {
                     bw[i][d] = (int)perm(kI8wHiTable, lo_tab[i], sel);
                 } else {
@@ -1738,7 +1699,7 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
 #pragma unroll
     for (int i = 0; i < FN; i++) {
         const int cg = min((n0 >> 4) + i, g.ng_last);
-        b_base[i] = g.rec + (size_t)cg * units * (G::REC4 ? 1024 : 768) + lane * (G::REC4 ? 16 : 12);
+        b_base[i] = g.rec + (size_t)cg * units * 1024 + lane * 16;
         clo[i] = MODE == MODE_INT8W ? g.clo[16 * cg + (lane & 15)] : 0u;
     }
 
@@ -1769,13 +1730,8 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
                     a[buf][c][s][j] = *reinterpret_cast<const v4i *>(a_base[j] + (size_t)(2 * u + s) * 1024);
 #pragma unroll
             for (int i = 0; i < FN; i++) {
-                if (G::REC4) {
-                    const uint4 v = *reinterpret_cast<const uint4 *>(b_base[i] + (size_t)u * 1024);
-                    r[buf][c][i][0] = v.x; r[buf][c][i][1] = v.y; r[buf][c][i][2] = v.z; r[buf][c][i][3] = v.w;
-                } else {
-                    const uint3 v = *reinterpret_cast<const uint3 *>(b_base[i] + (size_t)u * 768);
-                    r[buf][c][i][0] = v.x; r[buf][c][i][1] = v.y; r[buf][c][i][2] = v.z; r[buf][c][i][3] = 0u;
-                }
+                const uint4 v = *reinterpret_cast<const uint4 *>(b_base[i] + (size_t)u * 1024);
+                r[buf][c][i][0] = v.x; r[buf][c][i][1] = v.y; r[buf][c][i][2] = v.z; r[buf][c][i][3] = v.w;
             }
         }
     };
@@ -1897,14 +1853,14 @@ __global__ __launch_bounds__(G::NT, G::NT > 256 ? 1 : 2) void gemm_fvs_grouped(G
     fvs_tile<G, MODE>(h);
 }
 
-/* The same for the large-M kernel's tiles (int8w, 4-bit records, one split; blockIdx.x is the tile as in gemm_fv). */
+/* The same for the large-M kernel's tiles (int8w, one split; blockIdx.x is the tile as in gemm_fv). */
 template <class G, bool MULTI>
 __global__ __launch_bounds__(G::NT, 2) void gemm_fv_grouped(GemmArgs g, GroupArgs ga)
 {
     GemmArgs h = g;
     const int q = blockIdx.y;
     h.rec = ga.rec[q]; h.clo = ga.clo[q]; h.c1 = ga.c1[q]; h.c2 = ga.c2[q]; h.C = ga.C[q];
-    fv_tile<G, MODE_INT8W, OUT_F32, MULTI, false, 2, true, true>(h);
+    fv_tile<G, MODE_INT8W, OUT_F32, MULTI, false, 2, true>(h);
 }
 
 /* The fold after a split GEMM: per output, the int32 partial sums of the splits inside each 1024-row block are
