@@ -478,9 +478,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--eager-extras", action="store_true",
-                    help="extra configurations without HIP graphs: the producers, the attention products, the "
-                         "feed-forward module's kernels and the sweep's kernels, each timed by back-to-back "
-                         "launches (what rocprofv3 traces)")
+                    help="extra configurations without HIP graphs: the device conformer block, the producers, the "
+                         "attention products, the feed-forward module's kernels and the sweep's kernels, each "
+                         "timed by back-to-back launches (what rocprofv3 traces)")
     ap.add_argument("--no-sweep", action="store_true",
                     help="leave the 216-linear sweep out of the extra configurations")
     ap.add_argument("--kernel-reps", type=int, default=200,
@@ -566,6 +566,7 @@ def main():
         cpu_shapes = (lins[0].M, [(l.K, l.N) for l in lins])
 
     if not args.no_extra and args.eager_extras:
+        extra["conformer_block375"] = conformer_block_config(stream, graph=False)
         extra["attention375"] = attention_config(stream, graph=False)
         extra["producers"] = producer_config(stream)
         extra["ffn_module375"] = ffn_module_config(stream, graph=False)
@@ -822,12 +823,13 @@ def block_config(stream, T=375, steps=500, warmup=50):
             "what": f"T={T}: 8 producers + 8 five-value GEMMs (int8w), residuals in the epilogues"}
 
 
-def conformer_block_config(stream, T=375, steps=200, warmup=20):
+def conformer_block_config(stream, T=375, steps=200, warmup=20, graph=True):
     """One whole conformer block on the device (p2h_conformer_block: encoder.c:617-625, every step between the
     linears included — attention scores, relative shift and softmax, GLU, depthwise convolution and SiLU, the
     LayerNorms, the positional projection of its 2T − 1 rows) on a seeded synthetic block, replayed from one graph;
     x is carried from replay to replay (the final LayerNorm keeps it bounded). Per mode: ms per block and per 30 s
-    window of 24 blocks."""
+    window of 24 blocks. graph=False launches the block's kernels directly, block after block, between two HIP
+    events (what the profiler traces)."""
     params = P.block_params(SEED, 100)
     blk = P.Block(params)
     D = P.D_MODEL
@@ -839,8 +841,20 @@ def conformer_block_config(stream, T=375, steps=200, warmup=20):
         body = lambda m=mode, w=ws: blk.run_dev(m, T, pe.ptr, x.ptr, w, stream.ptr)
         body()   # anything a first call prepares is made before the capture
         stream.sync()
-        ms, _ = StepGraphs(stream, body, 1, steps).time(steps, warmup)
+        if graph:
+            ms, _ = StepGraphs(stream, body, 1, steps).time(steps, warmup)
+        else:
+            for _ in range(warmup):
+                body()
+            e0, e1 = P.Event(), P.Event()
+            e0.record(stream.ptr)
+            for _ in range(steps):
+                body()
+            e1.record(stream.ptr)
+            e1.sync()
+            ms = e0.elapsed_ms(e1) / steps
         res[mode] = {"ms_per_block": round(ms, 5), "ms_per_30s_window_24_blocks": round(24 * ms, 4)}
+    res["launch"] = "one graph per block" if graph else "direct launches, block after block"
     return res
 
 
