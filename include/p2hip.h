@@ -257,6 +257,16 @@ int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGa
 int p2h_concat_heads_rows(int T, const float *dAttnH, float *dY, void *stream);
 int p2h_channel_major_rows(int T, const float *dDW, float *dY, void *stream);
 
+/* Relative-position self-attention of all 8 heads between the projections (encoder.c:495-523: gather_heads,
+ * transpose_pos, the two score products, combine_softmax and the product with V, heads_gemm encoder.c:279-316) in
+ * one kernel: QKV [T][3·1024] (q | k | v rows), bias_u / bias_v [1024], the projected positional rows P
+ * [2T − 1][1024] → attn_h [8][T][128]. The softmax is combine_softmax's arithmetic in its order; the score and
+ * output products are fp32 matrix-core sums (another order than the reference's packed sgemm). T <= 768, every
+ * pointer 16-byte aligned. */
+#define P2H_ATTENTION_TMAX 768
+int p2h_attention_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
+                        float *dAttnH, void *stream);
+
 /* One FastConformer block on the device (conformer_block, encoder.c:617-625): feed-forward ½, relative-position
  * self-attention, convolution module, feed-forward ½, final LayerNorm, on X [T][1024] in place. The five-value
  * linears run in `mode` (P2H_INT8W / P2H_INT8: LayerNorm, SiLU, head concatenation and the channel-major transpose

@@ -774,6 +774,25 @@ int p2h_combine_softmax(int T, float *dAC, const float *dBD, void *stream)
     return P2H_OK;
 }
 
+int p2h_attention_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
+                        float *dAttnH, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0 || T > P2H_ATTENTION_TMAX)
+        return fail(P2H_E_ARG, "p2h_attention_heads: T = %d (1 .. %d)", T, P2H_ATTENTION_TMAX);
+    if (T == 0) return P2H_OK;
+    if (!dQKV || !dBiasU || !dBiasV || !dP || !dAttnH) return fail(P2H_E_ARG, "p2h_attention_heads: null pointer");
+    if (!aligned(dQKV, 16) || !aligned(dBiasU, 16) || !aligned(dBiasV, 16) || !aligned(dP, 16) || !aligned(dAttnH, 16))
+        return fail(P2H_E_ARG, "p2h_attention_heads: operands must be 16-byte aligned");
+    const float scale = 1.0f / sqrtf((float)p2k::kDh);   /* encoder.c:521 */
+    const dim3 grid((unsigned)((T + 15) / 16), p2k::kH);
+    hipStream_t s = stream_of(stream);
+    if (T <= 64 * 6) hipLaunchKernelGGL(p2k::attention_rel<6>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH);
+    else hipLaunchKernelGGL(p2k::attention_rel<12>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
 int p2h_glu_channel_major(int T, const float *dPW1, float *dGated, void *stream)
 {
     if (int rc = ensure_init()) return rc;
@@ -1545,6 +1564,14 @@ BlockWs block_ws(int mode, int T, char *base)
     return w;
 }
 
+/* the fused attention kernel takes the block when its rows fit (T <= P2H_ATTENTION_TMAX) and the bias vectors are
+ * 16-byte aligned; P2H_ATTENTION_FUSED=0 keeps the separate products (for comparisons) */
+bool fused_attention(int T, const P2hBlock *blk)
+{
+    return T <= P2H_ATTENTION_TMAX && aligned(blk->bias_u, 16) && aligned(blk->bias_v, 16) &&
+           env_int("P2H_ATTENTION_FUSED", 1) != 0;
+}
+
 int check_block_weight(const P2hWeight *w, int K, int N, const char *name)
 {
     if (!w || w->K != K || w->N != N)
@@ -1616,20 +1643,24 @@ int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, 
     /* self_attention (encoder.c:471-541) */
     P2H_TRY(layer_norm(blk->norm_sa_w, blk->norm_sa_b));
     P2H_TRY(linear(blk->qkv, D, 3 * D, 1.0f, 0.0f, w.ln, w.qkv));
-    /* Q_u, Q_v as [H, T, Dh] (the bias adds of gather_heads); the products read K, V and the positional rows where
-     * they lie, head h at column offset h·Dh of its row (the transposes of gather_heads and transpose_pos are only
-     * layouts for the reference's NN kernel; the sums are the same) */
-    hipLaunchKernelGGL(p2k::gather_qv, dim3((unsigned)(((size_t)T * D + 255) / 256)), dim3(256), 0, s, T, w.qkv,
-                       blk->bias_u, blk->bias_v, w.qu, w.qv, (float *)nullptr);
-    HIPCHK(hipGetLastError());
     P2H_TRY(p2h_fvb_gemm(mode, L, D, D, 1.0f, dPE, D, blk->pos, 0.0f, w.p, D, w.gws, w.gws_bytes, s));
-    P2H_TRY(p2h_sgemm_batched(0, 1, T, T, Dh, 1.0f, w.qu, Dh, (long long)T * Dh, w.qkv + D, 3 * D, Dh, 0.0f, w.ac, T,
-                              (long long)T * T, H, s));
-    P2H_TRY(p2h_sgemm_batched(0, 1, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, w.p, D, Dh, 0.0f, w.bd, L,
-                              (long long)T * L, H, s));
-    P2H_TRY(p2h_combine_softmax(T, w.ac, w.bd, s));
-    P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.qkv + 2 * D, 3 * D, Dh, 0.0f,
-                              w.attn_h, Dh, (long long)T * Dh, H, s));
+    if (fused_attention(T, blk)) {   /* scores, shift, softmax and the product with V in one kernel */
+        P2H_TRY(p2h_attention_heads(T, w.qkv, blk->bias_u, blk->bias_v, w.p, w.attn_h, s));
+    } else {
+        /* Q_u, Q_v as [H, T, Dh] (the bias adds of gather_heads); the products read K, V and the positional rows
+         * where they lie, head h at column offset h·Dh of its row (the transposes of gather_heads and transpose_pos
+         * are only layouts for the reference's NN kernel; the sums are the same) */
+        hipLaunchKernelGGL(p2k::gather_qv, dim3((unsigned)(((size_t)T * D + 255) / 256)), dim3(256), 0, s, T, w.qkv,
+                           blk->bias_u, blk->bias_v, w.qu, w.qv, (float *)nullptr);
+        HIPCHK(hipGetLastError());
+        P2H_TRY(p2h_sgemm_batched(0, 1, T, T, Dh, 1.0f, w.qu, Dh, (long long)T * Dh, w.qkv + D, 3 * D, Dh, 0.0f, w.ac,
+                                  T, (long long)T * T, H, s));
+        P2H_TRY(p2h_sgemm_batched(0, 1, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, w.p, D, Dh, 0.0f, w.bd, L,
+                                  (long long)T * L, H, s));
+        P2H_TRY(p2h_combine_softmax(T, w.ac, w.bd, s));
+        P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.qkv + 2 * D, 3 * D, Dh, 0.0f,
+                                  w.attn_h, Dh, (long long)T * Dh, H, s));
+    }
     if (mode == P2H_EXACT) {
         P2H_TRY(p2h_concat_heads_rows(T, w.attn_h, w.attn, s));
         P2H_TRY(linear(blk->out, D, D, 1.0f, 0.0f, w.attn, w.out));

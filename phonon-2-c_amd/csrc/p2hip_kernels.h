@@ -659,6 +659,158 @@ __global__ __launch_bounds__(256) void combine_softmax_wave(int rows, int T, flo
     }
 }
 
+/* Relative-position self-attention of one head for 16 query rows (encoder.c:495-523 between the projections): the
+ * scores S[i][j] = (Q_u[i]·K[j] + Q_v[i]·P[j + T − 1 − i])·scale, their softmax over j as combine_softmax_rows
+ * computes it (the AVX2 route's order, the same operations), and O[i] = Σ_j softmax(S)[i][j]·V[j], written to
+ * out [8][T][128]. Q_u = Q + bias_u and Q_v = Q + bias_v are formed as the operands load (gather_heads' additions);
+ * Q, K and V are read inside QKV [T][3·1024] and the positional rows inside P [2T − 1][1024], head h at column
+ * offset 128·h. The scores live in LDS only: neither the [T, T] and [T, 2T − 1] products nor the half of the
+ * positional product that no row reads is made. Products on v_mfma_f32_16x16x4_f32 (D = A·B with A's rows and B's
+ * columns from lane % 16, the four k of a step from lane / 16): for a score tile the 16 keys or positions are A's
+ * rows and the 16 queries B's columns, and the 128-long dot products are cut into four blocks of 32 (lane group g
+ * sums k = 32g + s at step s); for O the 16 output dimensions are A's rows, the queries B's columns, j = 4s + g.
+ * Eight waves: key and position tiles round-robin over the waves, two softmax rows each, 16 output dimensions
+ * each. Grid (ceil(T / 16), 8); T <= 64·NM. */
+template <int NM>
+__global__ __launch_bounds__(512) void attention_rel(int T, float scale, const float *__restrict__ qkv,
+                                                     const float *__restrict__ bu, const float *__restrict__ bv,
+                                                     const float *__restrict__ P, float *__restrict__ out)
+{
+    constexpr int SP = 64 * NM + 4;   /* score row pitch (floats): 16 rows 4 banks apart */
+    constexpr int CS = 8 * NM + 4;    /* softmax chain stride */
+    constexpr int D3 = 3 * kD;
+    __shared__ __align__(16) float S[16 * SP];
+    __shared__ __align__(16) float chains[8][8 * CS];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, x = lane & 15;
+    const int i0 = blockIdx.x * 16, h = blockIdx.y;
+    const int Tp = (T + 15) / 16 * 16, L = 2 * T - 1;
+
+    /* this lane's query operands: row i0 + x (clamped; rows past T are computed and not stored), k = 32g .. 32g + 31 */
+    float qu[32], qv[32];
+    {
+        const int iq = min(i0 + x, T - 1);
+        const float4 *q = reinterpret_cast<const float4 *>(qkv + (size_t)iq * D3 + h * kDh + 32 * g);
+        const float4 *u = reinterpret_cast<const float4 *>(bu + h * kDh + 32 * g);
+        const float4 *v = reinterpret_cast<const float4 *>(bv + h * kDh + 32 * g);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 a = q[c], b = u[c], d = v[c];
+            qu[4 * c] = __fadd_rn(a.x, b.x); qu[4 * c + 1] = __fadd_rn(a.y, b.y);
+            qu[4 * c + 2] = __fadd_rn(a.z, b.z); qu[4 * c + 3] = __fadd_rn(a.w, b.w);
+            qv[4 * c] = __fadd_rn(a.x, d.x); qv[4 * c + 1] = __fadd_rn(a.y, d.y);
+            qv[4 * c + 2] = __fadd_rn(a.z, d.z); qv[4 * c + 3] = __fadd_rn(a.w, d.w);
+        }
+    }
+    auto dot16 = [&](const float *row, const float (&qq)[32]) __attribute__((always_inline)) {
+        float r[32];
+        const float4 *r4 = reinterpret_cast<const float4 *>(row + 32 * g);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 a = r4[c];
+            r[4 * c] = a.x; r[4 * c + 1] = a.y; r[4 * c + 2] = a.z; r[4 * c + 3] = a.w;
+        }
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 32; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(r[s], qq[s], acc, 0, 0, 0);
+        return acc;   /* lane holds D[4g + e][x]: key / position 4g + e of the tile, query x */
+    };
+
+    /* AC into S: S[x][16·kt + 4g + e] */
+    for (int kt = w; kt < Tp / 16; kt += 8) {
+        const int j = min(16 * kt + x, T - 1);
+        const v4f acc = dot16(qkv + (size_t)j * D3 + kD + h * kDh, qu);
+        *reinterpret_cast<v4f *>(&S[x * SP + 16 * kt + 4 * g]) = acc;
+    }
+    __syncthreads();
+    /* BD, shifted into S: row i reads positions j + T − 1 − i, so the 16 rows need positions lbase .. 2T − 2 − i0 */
+    const int ilast = min(i0 + 15, T - 1), lbase = T - 1 - ilast;
+    const int npt = (2 * T - 1 - i0 - lbase + 15) / 16;
+    for (int pt = w; pt < npt; pt += 8) {
+        const int lp = min(lbase + 16 * pt + x, L - 1);
+        const v4f acc = dot16(P + (size_t)lp * kD + h * kDh, qv);
+        const int i = i0 + x;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = lbase + 16 * pt + 4 * g + e - (T - 1 - i);   /* each (i, j) is one lane's, once */
+            if (i < T && j >= 0 && j < T) {
+                float *sv = &S[x * SP + j];
+                *sv = __fmul_rn(__fadd_rn(*sv, acc[e]), scale);
+            }
+        }
+    }
+    __syncthreads();
+    /* softmax of rows w and w + 8 (combine_softmax_wave's arithmetic, the scores from LDS) */
+    const int body = T / 8 * 8;
+    for (int rr = w; rr < 16; rr += 8) {
+        if (i0 + rr >= T) break;
+        float *row = S + rr * SP;
+        float v[NM];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const int j = lane + 64 * m;
+            v[m] = j < T ? row[j] : -INFINITY;
+            mx = fmaxf(mx, v[m]);
+        }
+        mx = wave_max_dpp(mx);
+        float *ch = chains[w];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   /* the previous row's chain reads are done */
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const int j = lane + 64 * m;
+            if (j < body) v[m] = exp_p2(__fsub_rn(v[m], mx));
+            else if (j < T) v[m] = expf(__fsub_rn(v[m], mx));
+            if (j < T) ch[(j & 7) * CS + (j >> 3)] = v[m];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        float p = 0.0f;
+        if (lane < 8) {
+            const float *cq = ch + lane * CS;
+            const int n8 = body / 8;
+            int k = 0;
+            for (; k + 4 <= n8; k += 4) {
+                const float4 a = *reinterpret_cast<const float4 *>(cq + k);
+                p = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(p, a.x), a.y), a.z), a.w);
+            }
+            for (; k < n8; k++) p = __fadd_rn(p, cq[k]);
+        }
+        float l8[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) l8[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), q));
+        float s = __fadd_rn(__fadd_rn(__fadd_rn(l8[0], l8[4]), __fadd_rn(l8[2], l8[6])),
+                            __fadd_rn(__fadd_rn(l8[1], l8[5]), __fadd_rn(l8[3], l8[7])));
+        for (int j = body; j < T; j++) s = __fadd_rn(s, ch[(j & 7) * CS + (j >> 3)]);
+        const float inv = __fdiv_rn(1.0f, s);
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const int j = lane + 64 * m;
+            if (j < T) row[j] = __fmul_rn(v[m], inv);
+            else if (j < Tp) row[j] = 0.0f;   /* the product with V runs over Tp keys */
+        }
+    }
+    __syncthreads();
+    /* O[i0 + x][16w + 4g + e] = Σ_j p[x][j]·V[j][16w + 4g + e]: eight steps' V values loaded ahead of their MFMAs */
+    const float *vb = qkv + 2 * kD + h * kDh + 16 * w + x;
+    const float *pr = S + x * SP + g;
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = Tp / 4;
+    for (int s0 = 0; s0 < steps; s0 += 8) {
+        float vv[8], pp[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = min(4 * (s0 + u) + g, T - 1);   /* keys past T carry p = 0 */
+            vv[u] = vb[(size_t)j * D3];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) pp[u] = s0 + u < steps ? pr[4 * (s0 + u)] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[u], pp[u], acc, 0, 0, 0);
+    }
+    if (i0 + x < T) *reinterpret_cast<v4f *>(out + ((size_t)h * T + i0 + x) * kDh + 16 * w + 4 * g) = acc;
+}
+
 /* glu_to_channel_major (encoder.c:543-555): gated[d][t] = pw1[t][d] / (1 + expf(−pw1[t][D + d])), the exponent's
  * argument clamped at 87 (p2_expneg, phonon2.h:38-41). A 32-frame × 64-channel tile through LDS: reads along d,
  * writes along t. */

@@ -92,6 +92,38 @@ def test_combine_softmax(T):
         assert _ulps(got, ref).max() <= 4
 
 
+def _attention_reference(qkv, bu, bv, pos):
+    """encoder.c:495-523 on the CPU: float64 score and output products (rounded to float32 where the reference
+    stores them), the oracle's combine_softmax (the reference's order) in between."""
+    T = qkv.shape[0]
+    q, k, v = (qkv[:, i * D:(i + 1) * D].reshape(T, H, Dh).transpose(1, 0, 2) for i in range(3))
+    qu = (q + bu.reshape(H, 1, Dh)).astype(np.float32)
+    qv = (q + bv.reshape(H, 1, Dh)).astype(np.float32)
+    Ph = pos.reshape(2 * T - 1, H, Dh).transpose(1, 0, 2)
+    ac = np.matmul(qu.astype(np.float64), k.transpose(0, 2, 1).astype(np.float64)).astype(np.float32)
+    bd = np.matmul(qv.astype(np.float64), Ph.transpose(0, 2, 1).astype(np.float64)).astype(np.float32)
+    p = O.combine_softmax(ac.reshape(H * T, T), bd.reshape(H * T, 2 * T - 1)).reshape(H, T, T)
+    return np.matmul(p.astype(np.float64), v.astype(np.float64))
+
+
+@pytest.mark.parametrize("T,gain", [(375, 1.0), (375, 3.0), (1, 1.0), (17, 1.0), (100, 2.0), (700, 1.0)])
+def test_attention_heads(T, gain):
+    """p2h_attention_heads (one kernel: scores, relative shift, softmax, product with V) against float64 products
+    around the oracle's softmax: the kernel's products are fp32 matrix-core sums, so per output row (128 values) the
+    relative L2 difference is at most 2e-5 (gain 3 makes the softmax peaked: scores up to ~±40)."""
+    print(f"attention_heads T={T} gain={gain}", flush=True)
+    rng = np.random.default_rng(SEED + 17 * T)
+    qkv = (rng.standard_normal((T, 3 * D)) * gain).astype(np.float32)
+    bu, bv = (rng.standard_normal(D) * 0.1).astype(np.float32), (rng.standard_normal(D) * 0.1).astype(np.float32)
+    pos = rng.standard_normal((2 * T - 1, D)).astype(np.float32)
+    got = P.attention_heads(qkv, bu, bv, pos)
+    ref = _attention_reference(qkv, bu, bv, pos)
+    d = np.linalg.norm(got - ref, axis=2) / np.linalg.norm(ref, axis=2)
+    print(f"  per-row relative L2: max {d.max():.3g}, median {np.median(d):.3g}", flush=True)
+    assert np.isfinite(got).all()
+    assert d.max() <= 2e-5
+
+
 @pytest.mark.parametrize("T", [375, 7])
 def test_glu_channel_major(T):
     print(f"glu T={T}", flush=True)
