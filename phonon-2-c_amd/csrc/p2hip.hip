@@ -116,6 +116,13 @@ hipStream_t stream_of(void *s)
 }
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+/* an integer from the environment (tuning and comparison switches), dflt when unset or empty */
+int env_int(const char *name, int dflt)
+{
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
@@ -785,7 +792,7 @@ int p2h_attention_heads(int T, const float *dQKV, const float *dBiasU, const flo
     if (!aligned(dQKV, 16) || !aligned(dBiasU, 16) || !aligned(dBiasV, 16) || !aligned(dP, 16) || !aligned(dAttnH, 16))
         return fail(P2H_E_ARG, "p2h_attention_heads: operands must be 16-byte aligned");
     const float scale = 1.0f / sqrtf((float)p2k::kDh);   /* encoder.c:521 */
-    const dim3 grid((unsigned)((T + 15) / 16), p2k::kH);
+    const dim3 grid((unsigned)(p2k::kH * ((T + 15) / 16)));
     hipStream_t s = stream_of(stream);
     if (T <= 64 * 6) hipLaunchKernelGGL(p2k::attention_rel<6>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH);
     else hipLaunchKernelGGL(p2k::attention_rel<12>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH);
@@ -905,12 +912,6 @@ struct Plan {
     int cfg, splits, split_rows, tiles_m, tiles_n;
     size_t part_bytes;
 };
-
-int env_int(const char *name, int dflt)
-{
-    const char *v = getenv(name);
-    return (v && *v) ? atoi(v) : dflt;
-}
 
 /* Tile and K split of a five-value call. A split is a whole number of 128-row units inside one 1024-row fold block;
  * it runs only with a workspace, for K > 1024 (its int32 partials cost splits × M × N × 4 bytes of traffic, worth

@@ -667,10 +667,12 @@ __global__ __launch_bounds__(256) void combine_softmax_wave(int rows, int T, flo
  * offset 128·h. The scores live in LDS only: neither the [T, T] and [T, 2T − 1] products nor the half of the
  * positional product that no row reads is made. Products on v_mfma_f32_16x16x4_f32 (D = A·B with A's rows and B's
  * columns from lane % 16, the four k of a step from lane / 16): for a score tile the 16 keys or positions are A's
- * rows and the 16 queries B's columns, and the 128-long dot products are cut into four blocks of 32 (lane group g
- * sums k = 32g + s at step s); for O the 16 output dimensions are A's rows, the queries B's columns, j = 4s + g.
+ * rows and the 16 queries B's columns, lane group g taking k = 16(s / 4) + 4g + s % 4 at step s (a row's 128 values
+ * arrive as 16-byte loads, the four lanes of a row reading 64 contiguous bytes per load: with k = 32g + s each load
+ * touched 64 cache lines and the loads' address processing bounded the kernel); for O the 16 output dimensions are
+ * A's rows, the queries B's columns, j = 4s + g.
  * Eight waves: key and position tiles round-robin over the waves, two softmax rows each, 16 output dimensions
- * each. Grid (ceil(T / 16), 8); T <= 64·NM. */
+ * each. Grid 8·ceil(T / 16); T <= 64·NM. */
 template <int NM>
 __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const float *__restrict__ qkv,
                                                      const float *__restrict__ bu, const float *__restrict__ bv,
@@ -678,70 +680,123 @@ __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const f
 {
     constexpr int SP = 64 * NM + 4;   /* score row pitch (floats): 16 rows 4 banks apart */
     constexpr int CS = 8 * NM + 4;    /* softmax chain stride */
-    constexpr int D3 = 3 * kD;
+    constexpr int D3 = 3 * kD, NW = 8;
     __shared__ __align__(16) float S[16 * SP];
-    __shared__ __align__(16) float chains[8][8 * CS];
+    __shared__ __align__(16) float chains[NW][8 * CS];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, x = lane & 15;
-    const int i0 = blockIdx.x * 16, h = blockIdx.y;
+    /* workgroups reach the 8 XCDs round-robin by linear id: head = id % 8 keeps each head's K, V and positional
+     * rows in one XCD's L2 (with the head as the grid's second index every XCD fetched every head) */
+    const int i0 = (int)(blockIdx.x / 8) * 16, h = (int)(blockIdx.x % 8);
     const int Tp = (T + 15) / 16 * 16, L = 2 * T - 1;
 
-    /* this lane's query operands: row i0 + x (clamped; rows past T are computed and not stored), k = 32g .. 32g + 31 */
+    /* this lane's query operands: row i0 + x (clamped; rows past T are computed and not stored), k = 16c + 4g + e
+     * for c = 0..7, e = 0..3, held as element 4c + e (step s = 4c + e sums k = 16(s / 4) + 4g + s % 4 over the four
+     * lane groups): one 16-byte load per c, and the four lanes of a row read 64 contiguous bytes at once */
     float qu[32], qv[32];
     {
         const int iq = min(i0 + x, T - 1);
-        const float4 *q = reinterpret_cast<const float4 *>(qkv + (size_t)iq * D3 + h * kDh + 32 * g);
-        const float4 *u = reinterpret_cast<const float4 *>(bu + h * kDh + 32 * g);
-        const float4 *v = reinterpret_cast<const float4 *>(bv + h * kDh + 32 * g);
+        const float4 *q = reinterpret_cast<const float4 *>(qkv + (size_t)iq * D3 + h * kDh);
+        const float4 *u = reinterpret_cast<const float4 *>(bu + h * kDh);
+        const float4 *v = reinterpret_cast<const float4 *>(bv + h * kDh);
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            const float4 a = q[c], b = u[c], d = v[c];
+            const float4 a = q[4 * c + g], b = u[4 * c + g], d = v[4 * c + g];
             qu[4 * c] = __fadd_rn(a.x, b.x); qu[4 * c + 1] = __fadd_rn(a.y, b.y);
             qu[4 * c + 2] = __fadd_rn(a.z, b.z); qu[4 * c + 3] = __fadd_rn(a.w, b.w);
             qv[4 * c] = __fadd_rn(a.x, d.x); qv[4 * c + 1] = __fadd_rn(a.y, d.y);
             qv[4 * c + 2] = __fadd_rn(a.z, d.z); qv[4 * c + 3] = __fadd_rn(a.w, d.w);
         }
     }
-    auto dot16 = [&](const float *row, const float (&qq)[32]) __attribute__((always_inline)) {
-        float r[32];
-        const float4 *r4 = reinterpret_cast<const float4 *>(row + 32 * g);
+    auto load_row = [&](const float *row, float (&r)[32]) __attribute__((always_inline)) {
+        const float4 *r4 = reinterpret_cast<const float4 *>(row);
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            const float4 a = r4[c];
+            const float4 a = r4[4 * c + g];
             r[4 * c] = a.x; r[4 * c + 1] = a.y; r[4 * c + 2] = a.z; r[4 * c + 3] = a.w;
         }
-        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    /* one 16 × 16 score tile: 32 steps on two accumulators (even and odd steps), added at the end */
+    auto dot16 = [&](const float (&r)[32], const float (&qq)[32]) __attribute__((always_inline)) {
+        v4f a0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
 #pragma unroll
-        for (int s = 0; s < 32; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(r[s], qq[s], acc, 0, 0, 0);
-        return acc;   /* lane holds D[4g + e][x]: key / position 4g + e of the tile, query x */
+        for (int s = 0; s < 32; s += 2) {
+            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(r[s], qq[s], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(r[s + 1], qq[s + 1], a1, 0, 0, 0);
+        }
+        return a0 + a1;   /* lane holds D[4g + e][x]: key / position 4g + e of the tile, query x */
+    };
+    /* tiles t = w, w + NW, … < n of one kind, in groups of MAXT: a group's rows are all requested before its first
+     * product (the loads' latency, thousands of cycles from L2, is what bounds a tile; one tile in flight at a time
+     * left the matrix cores idle most of the time) */
+    constexpr int MAXT = 4;
+    /* `between` runs once in every wave after the first group's loads are issued (the barrier before BD: its rows
+     * are on their way while the other waves finish AC) */
+    auto run_tiles = [&](int n, const float (&qq)[32], auto row_of, auto consume, auto between)
+                         __attribute__((always_inline)) {
+        float r[MAXT][32];
+        int t0 = w;
+#pragma unroll
+        for (int q = 0; q < MAXT; q++)
+            if (t0 + NW * q < n) load_row(row_of(t0 + NW * q), r[q]);
+        between();
+        while (t0 < n) {
+#pragma unroll
+            for (int q = 0; q < MAXT; q++)
+                if (t0 + NW * q < n) consume(t0 + NW * q, dot16(r[q], qq));
+            t0 += NW * MAXT;
+            if (t0 >= n) break;
+#pragma unroll
+            for (int q = 0; q < MAXT; q++)
+                if (t0 + NW * q < n) load_row(row_of(t0 + NW * q), r[q]);
+        }
     };
 
     /* AC into S: S[x][16·kt + 4g + e] */
-    for (int kt = w; kt < Tp / 16; kt += 8) {
-        const int j = min(16 * kt + x, T - 1);
-        const v4f acc = dot16(qkv + (size_t)j * D3 + kD + h * kDh, qu);
-        *reinterpret_cast<v4f *>(&S[x * SP + 16 * kt + 4 * g]) = acc;
-    }
-    __syncthreads();
+    run_tiles(Tp / 16, qu,
+              [&](int kt) { return qkv + (size_t)min(16 * kt + x, T - 1) * D3 + kD + h * kDh; },
+              [&](int kt, v4f acc) { *reinterpret_cast<v4f *>(&S[x * SP + 16 * kt + 4 * g]) = acc; }, [] {});
     /* BD, shifted into S: row i reads positions j + T − 1 − i, so the 16 rows need positions lbase .. 2T − 2 − i0 */
     const int ilast = min(i0 + 15, T - 1), lbase = T - 1 - ilast;
-    const int npt = (2 * T - 1 - i0 - lbase + 15) / 16;
-    for (int pt = w; pt < npt; pt += 8) {
-        const int lp = min(lbase + 16 * pt + x, L - 1);
-        const v4f acc = dot16(P + (size_t)lp * kD + h * kDh, qv);
-        const int i = i0 + x;
+    run_tiles((2 * T - 1 - i0 - lbase + 15) / 16, qv,
+              [&](int pt) { return P + (size_t)min(lbase + 16 * pt + x, L - 1) * kD + h * kDh; },
+              [&](int pt, v4f acc) {
+                  /* each (i, j) is one lane's, once; a lane whose (i, j) lies outside the scores updates a slot of
+                   * its own in the chain buffer instead (written again before the softmax reads it), so the four
+                   * reads and writes need no branch */
+                  const int i = i0 + x;
+                  int at[4];
+                  float sv[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int j = lbase + 16 * pt + 4 * g + e - (T - 1 - i);   /* each (i, j) is one lane's, once */
-            if (i < T && j >= 0 && j < T) {
-                float *sv = &S[x * SP + j];
-                *sv = __fmul_rn(__fadd_rn(*sv, acc[e]), scale);
-            }
-        }
-    }
+                  for (int e = 0; e < 4; e++) {
+                      const int j = lbase + 16 * pt + 4 * g + e - (T - 1 - i);
+                      at[e] = (i < T && j >= 0 && j < T) ? x * SP + j : -1;
+                      sv[e] = at[e] >= 0 ? S[at[e]] : chains[w][lane];
+                  }
+#pragma unroll
+                  for (int e = 0; e < 4; e++) {
+                      const float r = __fmul_rn(__fadd_rn(sv[e], acc[e]), scale);
+                      if (at[e] >= 0) S[at[e]] = r;
+                      else chains[w][lane] = r;
+                  }
+              },
+              [] { __syncthreads(); });
     __syncthreads();
+    /* O[i0 + x][16c + 4g + e] = Σ_j p[x][j]·V[j][16c + 4g + e], j = 4s + g, for output dimensions c = w, over
+     * all steps: chunks of CH steps, the next chunk's V loaded while the current one is multiplied, four
+     * accumulators (steps s mod 4) added at the end. V does not depend on the softmax, so the first chunk is
+     * requested before it. */
+    constexpr int CH = 24;
+    const int c = w, sb = 0, se = Tp / 4;
+    const float *vb = qkv + 2 * kD + h * kDh + 16 * c + x;
+    auto load_v = [&](int s0, float (&vv)[CH]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < CH; u++) vv[u] = vb[(size_t)min(4 * (s0 + u) + g, T - 1) * D3];   /* p = 0 past T */
+    };
+    float va[CH], vc[CH];
+    if (sb < se) load_v(sb, va);
     /* softmax of rows w and w + 8 (combine_softmax_wave's arithmetic, the scores from LDS) */
     const int body = T / 8 * 8;
-    for (int rr = w; rr < 16; rr += 8) {
+    for (int rr = w; rr < 16; rr += NW) {
         if (i0 + rr >= T) break;
         float *row = S + rr * SP;
         float v[NM];
@@ -781,7 +836,12 @@ __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const f
         for (int q = 0; q < 8; q++) l8[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), q));
         float s = __fadd_rn(__fadd_rn(__fadd_rn(l8[0], l8[4]), __fadd_rn(l8[2], l8[6])),
                             __fadd_rn(__fadd_rn(l8[1], l8[5]), __fadd_rn(l8[3], l8[7])));
-        for (int j = body; j < T; j++) s = __fadd_rn(s, ch[(j & 7) * CS + (j >> 3)]);
+        float tv[7];   /* the tail's exponentials, read at once, added in order */
+#pragma unroll
+        for (int q = 0; q < 7; q++) tv[q] = ch[q * CS + (body >> 3)];   /* element body + q: chain q, place body / 8 */
+#pragma unroll
+        for (int q = 0; q < 7; q++)
+            if (body + q < T) s = __fadd_rn(s, tv[q]);
         const float inv = __fdiv_rn(1.0f, s);
 #pragma unroll
         for (int m = 0; m < NM; m++) {
@@ -791,24 +851,34 @@ __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const f
         }
     }
     __syncthreads();
-    /* O[i0 + x][16w + 4g + e] = Σ_j p[x][j]·V[j][16w + 4g + e]: eight steps' V values loaded ahead of their MFMAs */
-    const float *vb = qkv + 2 * kD + h * kDh + 16 * w + x;
     const float *pr = S + x * SP + g;
-    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    const int steps = Tp / 4;
-    for (int s0 = 0; s0 < steps; s0 += 8) {
-        float vv[8], pp[8];
+    v4f a4[4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int j = min(4 * (s0 + u) + g, T - 1);   /* keys past T carry p = 0 */
-            vv[u] = vb[(size_t)j * D3];
+    for (int q = 0; q < 4; q++) a4[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma_chunk = [&](int s0, const float (&vv)[CH]) __attribute__((always_inline)) {
+        float pp[CH];
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const float v = pr[4 * min(s0 + u, se - 1)];   /* read unconditionally, zero past the range */
+            pp[u] = s0 + u < se ? v : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) pp[u] = s0 + u < steps ? pr[4 * (s0 + u)] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < 8; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[u], pp[u], acc, 0, 0, 0);
+        for (int u = 0; u < CH; u++) a4[u % 4] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[u], pp[u], a4[u % 4], 0, 0, 0);
+    };
+    {
+        int s0 = sb;
+        while (s0 < se) {
+            if (s0 + CH < se) load_v(s0 + CH, vc);
+            mma_chunk(s0, va);
+            s0 += CH;
+            if (s0 >= se) break;
+            if (s0 + CH < se) load_v(s0 + CH, va);
+            mma_chunk(s0, vc);
+            s0 += CH;
+        }
     }
-    if (i0 + x < T) *reinterpret_cast<v4f *>(out + ((size_t)h * T + i0 + x) * kDh + 16 * w + 4 * g) = acc;
+    const v4f acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+    if (i0 + x < T) *reinterpret_cast<v4f *>(out + ((size_t)h * T + i0 + x) * kDh + 16 * c + 4 * g) = acc;
 }
 
 /* glu_to_channel_major (encoder.c:543-555): gated[d][t] = pw1[t][d] / (1 + expf(−pw1[t][D + d])), the exponent's
