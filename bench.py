@@ -586,6 +586,7 @@ def main():
         extra["ffn_module375"] = ffn_module_config(stream)
         extra["block375"] = block_config(stream)
         extra["conformer_block375"] = conformer_block_config(stream)
+        extra["conformer_stack375"] = conformer_stack_config(stream)
         extra["m38_rotated"] = m38_rotated_config(stream)
     sweep_ms = results["sweep"][1]["ms_per_step"] if "sweep" in results else None
 
@@ -855,6 +856,29 @@ def conformer_block_config(stream, T=375, steps=200, warmup=20, graph=True):
             ms = e0.elapsed_ms(e1) / steps
         res[mode] = {"ms_per_block": round(ms, 5), "ms_per_30s_window_24_blocks": round(24 * ms, 4)}
     res["launch"] = "one graph per block" if graph else "direct launches, block after block"
+    return res
+
+
+def conformer_stack_config(stream, T=375, n_blocks=24, steps=20, warmup=3):
+    """One 30 s window's 24 conformer blocks on the device (p2h_conformer_stack: encode_blocks, encoder.c:628-644),
+    24 distinct seeded synthetic blocks (216 five-value linears, 0.53 GB of device weights), the positional rows
+    quantised once and the 24 positional projections grouped; the whole window replayed from one graph, x carried
+    from window to window. ms per 30 s window, int8w and exact."""
+    blocks = [P.Block(P.block_params(SEED, 1000 + 20 * b)) for b in range(n_blocks)]
+    stack = P.Stack(blocks)
+    D = P.D_MODEL
+    x = P.to_device(P.gen_activations(SEED, 30_000 + T, T, D))
+    pe = P.to_device(P.gen_activations(SEED, 30_001 + T, 2 * T - 1, D))
+    res = {"what": f"T={T}: {n_blocks} device conformer blocks, distinct weights, one graph per window"}
+    for mode in ("int8w", "exact"):
+        ws = P.Workspace(P.stack_workspace_bytes(mode, T, n_blocks))
+        body = lambda m=mode, w=ws: stack.run_dev(m, T, pe.ptr, x.ptr, w, stream.ptr)
+        body()
+        stream.sync()
+        ms, _ = StepGraphs(stream, body, 1, steps).time(steps, warmup)
+        res[mode] = {"ms_per_30s_window": round(ms, 4), "ms_per_block": round(ms / n_blocks, 5)}
+    res["weights_device_mb"] = round(sum(getattr(b._keep[f], "device_bytes", lambda: 0)() for b in blocks
+                                         for f in P.BLOCK_LINEARS) / 1e6, 1)
     return res
 
 

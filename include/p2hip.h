@@ -293,6 +293,16 @@ size_t p2h_conformer_block_workspace_bytes(int mode, int T);
 int    p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, float *dX, void *workspace,
                            size_t workspace_bytes, void *stream);
 
+/* The block stack of one window (encode_blocks, encoder.c:628-644): blocks[0 .. n_blocks − 1] in order on x
+ * [T][1024] in place, with the shared positional rows pe [2T − 1][1024]. The same results as p2h_conformer_block
+ * called block after block, bit for bit; in the int8 modes the positional rows are quantised once and all the
+ * blocks' positional projections run as grouped launches before the first block. The workspace is
+ * p2h_conformer_stack_workspace_bytes(mode, T, n_blocks) bytes, 256-byte aligned (one block's, plus the n
+ * projections in the int8 modes). */
+size_t p2h_conformer_stack_workspace_bytes(int mode, int T, int n_blocks);
+int    p2h_conformer_stack(int mode, const P2hBlock *blocks, int n_blocks, int T, const float *dPE, float *dX,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1588,33 +1588,32 @@ size_t p2h_conformer_block_workspace_bytes(int mode, int T)
     return block_ws(mode, T, nullptr).total;
 }
 
-int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, float *dX, void *workspace,
-                        size_t workspace_bytes, void *stream)
+namespace {
+
+/* the block's weights and vectors are present, of the shapes the reference's ConformerBlock holds */
+int check_block(const P2hBlock *blk)
 {
-    if (int rc = ensure_init()) return rc;
-    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
-        return fail(P2H_E_ARG, "p2h_conformer_block: unknown mode %d", mode);
-    if (T <= 0 || !blk || !dPE || !dX) return fail(P2H_E_ARG, "p2h_conformer_block: T = %d or a null pointer", T);
+    const int D = p2k::kD, FF = 4 * p2k::kD;
+    const struct { const P2hWeight *w; int K, N; const char *name; } lin[] = {
+        {blk->ff1_l1, D, FF, "ff1_l1"}, {blk->ff1_l2, FF, D, "ff1_l2"}, {blk->qkv, D, 3 * D, "qkv"},
+        {blk->pos, D, D, "pos"},        {blk->out, D, D, "out"},         {blk->pw1, D, 2 * D, "pw1"},
+        {blk->pw2, D, D, "pw2"},        {blk->ff2_l1, D, FF, "ff2_l1"}, {blk->ff2_l2, FF, D, "ff2_l2"}};
+    for (auto &x : lin)
+        if (int rc = check_block_weight(x.w, x.K, x.N, x.name)) return rc;
+    const float *vecs[] = {blk->norm_ff1_w, blk->norm_ff1_b, blk->norm_sa_w,   blk->norm_sa_b,   blk->bias_u,
+                           blk->bias_v,     blk->norm_conv_w, blk->norm_conv_b, blk->dw_w,        blk->dw_b,
+                           blk->norm_ff2_w, blk->norm_ff2_b, blk->norm_out_w,  blk->norm_out_b};
+    for (const float *v : vecs)
+        if (!v) return fail(P2H_E_ARG, "p2h_conformer_block: a null norm, bias or convolution vector");
+    return P2H_OK;
+}
+
+/* one block on x in place (encoder.c:617-625); dP: its positional projection [2T − 1][1024] when the caller made
+ * it, else null (made here from dPE) */
+int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const float *dP, float *dX, const BlockWs &w,
+              hipStream_t s)
+{
     const int D = p2k::kD, FF = 4 * p2k::kD, L = 2 * T - 1, Dh = p2k::kDh, H = p2k::kH;
-    {
-        const struct { const P2hWeight *w; int K, N; const char *name; } ws_[] = {
-            {blk->ff1_l1, D, FF, "ff1_l1"}, {blk->ff1_l2, FF, D, "ff1_l2"}, {blk->qkv, D, 3 * D, "qkv"},
-            {blk->pos, D, D, "pos"},        {blk->out, D, D, "out"},         {blk->pw1, D, 2 * D, "pw1"},
-            {blk->pw2, D, D, "pw2"},        {blk->ff2_l1, D, FF, "ff2_l1"}, {blk->ff2_l2, FF, D, "ff2_l2"}};
-        for (auto &x : ws_)
-            if (int rc = check_block_weight(x.w, x.K, x.N, x.name)) return rc;
-        const float *vecs[] = {blk->norm_ff1_w, blk->norm_ff1_b, blk->norm_sa_w,   blk->norm_sa_b,   blk->bias_u,
-                               blk->bias_v,     blk->norm_conv_w, blk->norm_conv_b, blk->dw_w,        blk->dw_b,
-                               blk->norm_ff2_w, blk->norm_ff2_b, blk->norm_out_w,  blk->norm_out_b};
-        for (const float *v : vecs)
-            if (!v) return fail(P2H_E_ARG, "p2h_conformer_block: a null norm, bias or convolution vector");
-    }
-    const BlockWs need = block_ws(mode, T, nullptr);
-    if (!workspace || workspace_bytes < need.total || !aligned(workspace, 256))
-        return fail(P2H_E_WORKSPACE, "p2h_conformer_block: workspace of %zu bytes (256-byte aligned) needed",
-                    need.total);
-    const BlockWs w = block_ws(mode, T, (char *)workspace);
-    hipStream_t s = stream_of(stream);
     const int ldD = p2h_q_ld(D), ldF = p2h_q_ld(FF);
 #define P2H_TRY(call) do { if (int rc_ = (call)) return rc_; } while (0)
     /* a linear from produced rows: quantised (int8 modes) or fp32 (exact) */
@@ -1644,9 +1643,12 @@ int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, 
     /* self_attention (encoder.c:471-541) */
     P2H_TRY(layer_norm(blk->norm_sa_w, blk->norm_sa_b));
     P2H_TRY(linear(blk->qkv, D, 3 * D, 1.0f, 0.0f, w.ln, w.qkv));
-    P2H_TRY(p2h_fvb_gemm(mode, L, D, D, 1.0f, dPE, D, blk->pos, 0.0f, w.p, D, w.gws, w.gws_bytes, s));
+    if (!dP) {   /* the positional projection, unless the caller made it (p2h_conformer_stack groups them) */
+        P2H_TRY(p2h_fvb_gemm(mode, L, D, D, 1.0f, dPE, D, blk->pos, 0.0f, w.p, D, w.gws, w.gws_bytes, s));
+        dP = w.p;
+    }
     if (fused_attention(T, blk)) {   /* scores, shift, softmax and the product with V in one kernel */
-        P2H_TRY(p2h_attention_heads(T, w.qkv, blk->bias_u, blk->bias_v, w.p, w.attn_h, s));
+        P2H_TRY(p2h_attention_heads(T, w.qkv, blk->bias_u, blk->bias_v, dP, w.attn_h, s));
     } else {
         /* Q_u, Q_v as [H, T, Dh] (the bias adds of gather_heads); the products read K, V and the positional rows
          * where they lie, head h at column offset h·Dh of its row (the transposes of gather_heads and transpose_pos
@@ -1656,7 +1658,7 @@ int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, 
         HIPCHK(hipGetLastError());
         P2H_TRY(p2h_sgemm_batched(0, 1, T, T, Dh, 1.0f, w.qu, Dh, (long long)T * Dh, w.qkv + D, 3 * D, Dh, 0.0f, w.ac,
                                   T, (long long)T * T, H, s));
-        P2H_TRY(p2h_sgemm_batched(0, 1, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, w.p, D, Dh, 0.0f, w.bd, L,
+        P2H_TRY(p2h_sgemm_batched(0, 1, T, L, Dh, 1.0f, w.qv, Dh, (long long)T * Dh, dP, D, Dh, 0.0f, w.bd, L,
                                   (long long)T * L, H, s));
         P2H_TRY(p2h_combine_softmax(T, w.ac, w.bd, s));
         P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.qkv + 2 * D, 3 * D, Dh, 0.0f,
@@ -1686,6 +1688,101 @@ int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, 
     P2H_TRY(feed_forward(blk->norm_ff2_w, blk->norm_ff2_b, blk->ff2_l1, blk->ff2_l2));
     P2H_TRY(p2h_layer_norm_rows(T, D, dX, D, blk->norm_out_w, blk->norm_out_b, dX, D, s));
 #undef P2H_TRY
+    return P2H_OK;
+}
+
+
+}  // namespace
+
+int p2h_conformer_block(int mode, const P2hBlock *blk, int T, const float *dPE, float *dX, void *workspace,
+                        size_t workspace_bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
+        return fail(P2H_E_ARG, "p2h_conformer_block: unknown mode %d", mode);
+    if (T <= 0 || !blk || !dPE || !dX) return fail(P2H_E_ARG, "p2h_conformer_block: T = %d or a null pointer", T);
+    if (int rc = check_block(blk)) return rc;
+    const BlockWs need = block_ws(mode, T, nullptr);
+    if (!workspace || workspace_bytes < need.total || !aligned(workspace, 256))
+        return fail(P2H_E_WORKSPACE, "p2h_conformer_block: workspace of %zu bytes (256-byte aligned) needed",
+                    need.total);
+    return run_block(mode, blk, T, dPE, nullptr, dX, block_ws(mode, T, (char *)workspace), stream_of(stream));
+}
+
+/* The block stack (encode_blocks, encoder.c:628-644): the stack's workspace is one block's, then (int8 modes) the
+ * n positional projections [n][2T − 1][1024] and the quantised positional rows. */
+namespace {
+struct StackWs {
+    char *block; float *P; signed char *qpe; float *spe; size_t total;
+};
+StackWs stack_ws(int mode, int T, int n, char *base)
+{
+    StackWs s{};
+    const size_t L = 2 * (size_t)T - 1, D = p2k::kD;
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> char * {
+        char *p = base ? base + off : nullptr;
+        off += align_up(bytes, 256);
+        return p;
+    };
+    s.block = take(block_ws(mode, T, nullptr).total);
+    if (mode != P2H_EXACT) {
+        s.P = (float *)take(4 * L * D * (size_t)n);
+        s.qpe = (signed char *)take(p2h_q_bytes((int)L, (int)D));
+        s.spe = (float *)take(4 * L);
+    }
+    s.total = off;
+    return s;
+}
+}  // namespace
+
+size_t p2h_conformer_stack_workspace_bytes(int mode, int T, int n_blocks)
+{
+    if (ensure_init() || T <= 0 || n_blocks <= 0 || (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT))
+        return 0;
+    return stack_ws(mode, T, n_blocks, nullptr).total;
+}
+
+int p2h_conformer_stack(int mode, const P2hBlock *blocks, int n_blocks, int T, const float *dPE, float *dX,
+                        void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (mode != P2H_INT8W && mode != P2H_INT8 && mode != P2H_EXACT)
+        return fail(P2H_E_ARG, "p2h_conformer_stack: unknown mode %d", mode);
+    if (T <= 0 || n_blocks < 0 || (n_blocks > 0 && !blocks) || !dPE || !dX)
+        return fail(P2H_E_ARG, "p2h_conformer_stack: T = %d, %d blocks or a null pointer", T, n_blocks);
+    if (n_blocks == 0) return P2H_OK;
+    for (int b = 0; b < n_blocks; b++)
+        if (int rc = check_block(&blocks[b])) return rc;
+    const StackWs need = stack_ws(mode, T, n_blocks, nullptr);
+    if (!workspace || workspace_bytes < need.total || !aligned(workspace, 256))
+        return fail(P2H_E_WORKSPACE, "p2h_conformer_stack: workspace of %zu bytes (256-byte aligned) needed",
+                    need.total);
+    const StackWs sw = stack_ws(mode, T, n_blocks, (char *)workspace);
+    const BlockWs w = block_ws(mode, T, sw.block);
+    hipStream_t s = stream_of(stream);
+    const int D = p2k::kD, L = 2 * T - 1;
+    if (mode != P2H_EXACT) {
+        /* the positional rows are the same for every block (encoder.c:630): quantised once, and the blocks'
+         * projections of them in grouped launches, the same products the blocks would make one by one */
+        const int ldq = p2h_q_ld(D);
+        if (int rc = p2h_quant_rows(L, D, dPE, D, sw.qpe, ldq, sw.spe, s)) return rc;
+        for (int b0 = 0; b0 < n_blocks; b0 += p2k::kMaxGroups) {
+            const int g = std::min(p2k::kMaxGroups, n_blocks - b0);
+            const P2hWeight *wq[p2k::kMaxGroups];
+            float *cq[p2k::kMaxGroups];
+            for (int q = 0; q < g; q++) {
+                wq[q] = blocks[b0 + q].pos;
+                cq[q] = sw.P + (size_t)(b0 + q) * L * D;
+            }
+            if (int rc = p2h_fvb_gemm_q8a_grouped(mode, L, D, D, 1.0f, sw.qpe, ldq, sw.spe, wq, g, 0.0f, cq, D, s))
+                return rc;
+        }
+    }
+    for (int b = 0; b < n_blocks; b++)
+        if (int rc = run_block(mode, &blocks[b], T, dPE, mode != P2H_EXACT ? sw.P + (size_t)b * L * D : nullptr, dX,
+                               w, s))
+            return rc;
     return P2H_OK;
 }
 

@@ -89,6 +89,8 @@ _HIP_SIG = {
     "p2h_transpose_pos": (_i, [_i, _vp, _vp, _vp]),
     "p2h_combine_softmax": (_i, [_i, _vp, _vp, _vp]),
     "p2h_attention_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_conformer_stack_workspace_bytes": (_sz, [_i, _i, _i]),
+    "p2h_conformer_stack": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "p2h_glu_channel_major": (_i, [_i, _vp, _vp, _vp]),
     "p2h_depthwise_conv_silu": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
     "p2h_silu": (_i, [_sz, _vp, _vp]),
@@ -720,6 +722,30 @@ class Block:
         ws = Workspace(block_workspace_bytes(mode, T))
         self.run_dev(mode, T, dPE.ptr, dX.ptr, ws)
         return dX.download(x.shape, np.float32)
+
+
+class Stack:
+    """The blocks of one window on the device (p2h_conformer_stack): a list of Block."""
+
+    def __init__(self, blocks):
+        self.blocks = list(blocks)
+        self.arr = (_P2hBlock * len(self.blocks))(*[b.c for b in self.blocks])
+
+    def run_dev(self, mode, T, dPE, dX, ws, stream=None):
+        _ok(hip().p2h_conformer_stack(MODES.get(mode, mode), C.byref(self.arr), len(self.blocks), T, dPE, dX, ws.ptr,
+                                      ws.nbytes, stream), "p2h_conformer_stack")
+
+    def run(self, mode, x, pe):
+        x = _f32(x)
+        T = x.shape[0]
+        dX, dPE = to_device(x), to_device(_f32(pe))
+        ws = Workspace(stack_workspace_bytes(mode, T, len(self.blocks)))
+        self.run_dev(mode, T, dPE.ptr, dX.ptr, ws)
+        return dX.download(x.shape, np.float32)
+
+
+def stack_workspace_bytes(mode, T, n_blocks):
+    return hip().p2h_conformer_stack_workspace_bytes(MODES.get(mode, mode), T, n_blocks)
 
 
 def block_workspace_bytes(mode, T):

@@ -253,3 +253,22 @@ def test_block_step_against_reference(mode, stage, tmp_path):
     print(f"  percentiles 90 / 99: {np.percentile(rel, 90):.3g} / {np.percentile(rel, 99):.3g}", flush=True)
     assert np.linalg.norm(contrib) > 1e-2 * np.linalg.norm(ref)   # the step does contribute
     assert np.median(rel) <= 1e-4 and rel.max() <= 1e-2
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8", "exact"])
+def test_stack_equals_blocks_one_by_one(mode):
+    """p2h_conformer_stack over three distinct blocks equals p2h_conformer_block called block after block, bit for
+    bit (in the int8 modes the stack quantises the positional rows once and projects them for all blocks in a
+    grouped launch; the products are the same)."""
+    print(f"conformer stack of 3 blocks, mode={mode}, T=375", flush=True)
+    sys.path.insert(0, HERE)
+    import refblock_child as RC
+    T = 375
+    blocks = [P.Block(P.block_params(SEED, 200 + 20 * b)) for b in range(3)]
+    x, pe = RC.block_input(SEED, T)
+    one_by_one = x
+    for b in blocks:
+        one_by_one = b.run(mode, one_by_one, pe)
+    stacked = P.Stack(blocks).run(mode, x, pe)
+    assert np.isfinite(stacked).all()
+    assert np.array_equal(stacked.view(np.uint32), one_by_one.view(np.uint32))
