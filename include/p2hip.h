@@ -250,6 +250,10 @@ int p2h_transpose_pos(int L, const float *dP, float *dPt, void *stream);
 int p2h_combine_softmax(int T, float *dAC, const float *dBD, void *stream);
 int p2h_glu_channel_major(int T, const float *dPW1, float *dGated, void *stream);
 int p2h_depthwise_conv_silu(int T, const float *dGated, const float *dW, const float *dB, float *dOut, void *stream);
+/* p2h_glu_channel_major then p2h_depthwise_conv_silu in one kernel (encoder.c:594-597): pw1 [T][2048] → out
+ * [1024][T], the same bits, without the gated buffer. */
+int p2h_glu_depthwise_conv_silu(int T, const float *dPW1, const float *dW, const float *dB, float *dOut,
+                                void *stream);
 int p2h_silu(size_t n, float *dX, void *stream);
 int p2h_add_residual(int T, float *dX, const float *dY, float alpha, void *stream);
 int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta, float *dY,

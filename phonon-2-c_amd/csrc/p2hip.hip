@@ -825,6 +825,19 @@ int p2h_depthwise_conv_silu(int T, const float *dGated, const float *dW, const f
     return P2H_OK;
 }
 
+int p2h_glu_depthwise_conv_silu(int T, const float *dPW1, const float *dW, const float *dB, float *dOut,
+                                void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dPW1 || !dW || !dB || !dOut) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu: null pointer");
+    hipLaunchKernelGGL(p2k::glu_dwconv_silu, dim3((unsigned)((T + 31) / 32), p2k::kD / 16), dim3(256), 0,
+                       stream_of(stream), T, dPW1, dW, dB, dOut);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
 int p2h_silu(size_t n, float *dX, void *stream)
 {
     if (int rc = ensure_init()) return rc;
@@ -1513,7 +1526,7 @@ namespace {
 /* The block's buffers in the caller's workspace, 256-byte aligned sections. With base == nullptr only the size. */
 struct BlockWs {
     signed char *q; float *sc;                   /* quantised rows [T][≤ 4096] and their scales (int8 modes) */
-    float *h, *qkv, *qu, *qv, *p, *ac, *bd, *attn_h, *gated, *dw;
+    float *h, *qkv, *qu, *qv, *p, *ac, *bd, *attn_h, *dw;
     float *ln, *out, *attn;                      /* exact mode: fp32 rows */
     void *gws; size_t gws_bytes;                 /* the GEMMs' own workspace */
     size_t total;
@@ -1557,7 +1570,6 @@ BlockWs block_ws(int mode, int T, char *base)
     w.ac = (float *)take(4 * p2k::kH * Tz * Tz);
     w.bd = (float *)take(4 * p2k::kH * Tz * L);
     w.attn_h = (float *)take(4 * Tz * D);
-    w.gated = (float *)take(4 * D * Tz);
     w.dw = (float *)take(4 * D * Tz);
     w.gws_bytes = gemm_ws_bytes(mode, T);
     w.gws = w.gws_bytes ? take(w.gws_bytes) : nullptr;
@@ -1675,8 +1687,7 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     /* conv_module (encoder.c:573-613) */
     P2H_TRY(layer_norm(blk->norm_conv_w, blk->norm_conv_b));
     P2H_TRY(linear(blk->pw1, D, 2 * D, 1.0f, 0.0f, w.ln, w.h));
-    P2H_TRY(p2h_glu_channel_major(T, w.h, w.gated, s));
-    P2H_TRY(p2h_depthwise_conv_silu(T, w.gated, blk->dw_w, blk->dw_b, w.dw, s));
+    P2H_TRY(p2h_glu_depthwise_conv_silu(T, w.h, blk->dw_w, blk->dw_b, w.dw, s));
     if (mode == P2H_EXACT) {
         P2H_TRY(p2h_channel_major_rows(T, w.dw, w.attn, s));
         P2H_TRY(linear(blk->pw2, D, D, 1.0f, 0.0f, w.attn, w.out));

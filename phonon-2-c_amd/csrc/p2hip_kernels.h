@@ -925,6 +925,44 @@ __global__ __launch_bounds__(256) void dwconv_silu(int T, const float *__restric
     out[(size_t)d * T + t] = silu_p2(v);
 }
 
+/* glu_channel_major and dwconv_silu in one pass (encoder.c:594-597): a 32-frame × 16-channel tile of the
+ * depthwise convolution's output takes the GLU of frames t0 − 4 .. t0 + 35 of its channels into LDS (the halo is
+ * computed twice, by both neighbouring tiles) and the channels' taps, then each output runs dwconv_silu's chain over
+ * the LDS values. Every value is made by the same operations as in the two kernels, so the result is the same bits;
+ * the gated [1024][T] buffer is never written. Grid (ceil(T / 32), 64): 768 workgroups at T = 375. */
+__global__ __launch_bounds__(256) void glu_dwconv_silu(int T, const float *__restrict__ pw1, const float *__restrict__ w,
+                                                       const float *__restrict__ bias, float *__restrict__ out)
+{
+    constexpr int TT = 32, CB = 16, HALO = kConvK / 2, TW = TT + 2 * HALO;
+    __shared__ float gt[CB][TW + 1];
+    __shared__ float wt[CB * kConvK + CB];
+    const int t0 = blockIdx.x * TT, d0 = blockIdx.y * CB, tid = threadIdx.x;
+    if (tid < CB * kConvK) wt[tid] = w[d0 * kConvK + tid];
+    else if (tid < CB * kConvK + CB) wt[tid] = bias[d0 + tid - CB * kConvK];
+    for (int i = tid; i < TW * CB; i += 256) {
+        const int tl = i / CB, dl = i % CB, t = t0 - HALO + tl;
+        float v = 0.0f;
+        if (t >= 0 && t < T) {
+            const float *row = pw1 + (size_t)t * 2 * kD;
+            const float g = row[kD + d0 + dl];
+            v = __fdiv_rn(row[d0 + dl], __fadd_rn(1.0f, expf(g < -87.0f ? 87.0f : -g)));
+        }
+        gt[dl][tl] = v;
+    }
+    __syncthreads();
+    for (int i = tid; i < TT * CB; i += 256) {
+        const int dl = i / TT, tl = i % TT, t = t0 + tl;
+        if (t >= T) continue;
+        float v = wt[CB * kConvK + dl];
+#pragma unroll
+        for (int k = 0; k < kConvK; k++) {
+            const int src = t - HALO + k;
+            if (src >= 0 && src < T) v = __builtin_fmaf(gt[dl][tl + k], wt[dl * kConvK + k], v);
+        }
+        out[(size_t)(d0 + dl) * T + t] = silu_p2(v);
+    }
+}
+
 /* p2_swish on a flat array in place (tensor_ops.c:437-491): elements below the last multiple of eight as silu_p2,
  * the tail as x · p2_sigmoid(x) (expf clamped at 87, phonon2.h:38-46). */
 __global__ __launch_bounds__(256) void silu_flat(size_t n, float *__restrict__ x)

@@ -89,6 +89,7 @@ _HIP_SIG = {
     "p2h_transpose_pos": (_i, [_i, _vp, _vp, _vp]),
     "p2h_combine_softmax": (_i, [_i, _vp, _vp, _vp]),
     "p2h_attention_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_glu_depthwise_conv_silu": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
     "p2h_conformer_stack_workspace_bytes": (_sz, [_i, _i, _i]),
     "p2h_conformer_stack": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "p2h_glu_channel_major": (_i, [_i, _vp, _vp, _vp]),
@@ -638,6 +639,15 @@ def depthwise_conv_silu(gated, w, b):
     dX, dW, dB, dO = to_device(gated), to_device(_f32(w)), to_device(_f32(b)), DeviceBuffer(gated.nbytes)
     _ok(hip().p2h_depthwise_conv_silu(T, dX.ptr, dW.ptr, dB.ptr, dO.ptr, None), "p2h_depthwise_conv_silu")
     return dO.download(gated.shape, np.float32)
+
+
+def glu_depthwise_conv_silu(pw1, w, b):
+    """pw1 [T, 2048] → SiLU(depthwise conv(GLU(pw1))) as [1024, T], one kernel."""
+    pw1 = _f32(pw1)
+    T = pw1.shape[0]
+    dP, dW, dB, dO = to_device(pw1), to_device(_f32(w)), to_device(_f32(b)), DeviceBuffer(T * D_MODEL * 4)
+    _ok(hip().p2h_glu_depthwise_conv_silu(T, dP.ptr, dW.ptr, dB.ptr, dO.ptr, None), "p2h_glu_depthwise_conv_silu")
+    return dO.download((D_MODEL, T), np.float32)
 
 
 def silu(x):

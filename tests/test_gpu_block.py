@@ -144,6 +144,20 @@ def test_depthwise_conv_silu(T):
     assert np.array_equal(got.view(np.uint32), O.dwconv_silu(x, w, b).view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [375, 300, 9, 4, 1, 33])
+def test_glu_depthwise_conv_silu_fused(T):
+    """The fused kernel equals the GLU kernel followed by the convolution kernel, bit for bit."""
+    print(f"glu_depthwise_conv_silu T={T}", flush=True)
+    rng = np.random.default_rng(SEED + 19 * T)
+    pw1 = (rng.standard_normal((T, 2 * D)) * 2).astype(np.float32)
+    pw1[0, D:D + 4] = [-100.0, 100.0, -87.5, 88.0]
+    w = (rng.standard_normal((D, 9)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    got = P.glu_depthwise_conv_silu(pw1, w, b)
+    two = P.depthwise_conv_silu(P.glu_channel_major(pw1), w, b)
+    assert np.array_equal(got.view(np.uint32), two.view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [375 * 4096, 1001])
 def test_silu_flat(n):
     """The eight-wide body bit-exact; the tail (n mod 8 elements, expf) within 4 ulp."""
