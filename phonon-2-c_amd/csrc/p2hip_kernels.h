@@ -659,6 +659,30 @@ __global__ __launch_bounds__(256) void combine_softmax_wave(int rows, int T, flo
     }
 }
 
+/* Direct global → LDS loads (16 bytes per lane into 16-byte lane slots at lds + 16·lane). Issued from inline
+ * assembly so that the compiler adds no waits of its own for them: the GEMM waits for them explicitly (wait_vm),
+ * and the compiler's waits for its own loads stay correct since the vector-memory counter retires in order. */
+__device__ __forceinline__ void dma_16(const void *src, const void *lds)
+{
+    const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
+}
+
+/* s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left open); a compiler barrier for memory operations */
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+
+/* this wave's LDS reads complete, then the workgroup barrier; no wait on vector memory */
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 /* Relative-position self-attention of one head for 16 query rows (encoder.c:495-523 between the projections): the
  * scores S[i][j] = (Q_u[i]·K[j] + Q_v[i]·P[j + T − 1 − i])·scale, their softmax over j as combine_softmax_rows
  * computes it (the AVX2 route's order, the same operations), and O[i] = Σ_j softmax(S)[i][j]·V[j], written to
@@ -672,7 +696,9 @@ __global__ __launch_bounds__(256) void combine_softmax_wave(int rows, int T, flo
  * touched 64 cache lines and the loads' address processing bounded the kernel); for O the 16 output dimensions are
  * A's rows, the queries B's columns, j = 4s + g.
  * Eight waves: key and position tiles round-robin over the waves, two softmax rows each, 16 output dimensions
- * each. Grid 8·ceil(T / 16); T <= 64·NM. */
+ * each. Grid 8·ceil(T / 16); T <= 64·NM. With NM <= 6 (T <= 384) the score tiles reach LDS by direct loads
+ * (RING below: whole 128-byte lines per load instead of half lines, 2.5 us less at T = 375, the same bits); the
+ * longer rows' scores leave no LDS room for the slots, and their tiles load into registers. */
 template <int NM>
 __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const float *__restrict__ qkv,
                                                      const float *__restrict__ bu, const float *__restrict__ bv,
@@ -681,9 +707,16 @@ __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const f
     constexpr int SP = 64 * NM + 4;   /* score row pitch (floats): 16 rows 4 banks apart */
     constexpr int CS = 8 * NM + 4;    /* softmax chain stride */
     constexpr int D3 = 3 * kD, NW = 8;
+    /* RING: two 8 KB tile slots per wave, the softmax chains in the same space once the scores are made, and a slot
+     * per lane for BD's out-of-range updates; else the chains (which also hold that slot) */
+    constexpr bool RING = (16 * SP + NW * 2 * 2048 + NW * 64) * 4 <= 160 * 1024;
+    static_assert(!RING || NW * 8 * CS <= NW * 2 * 2048, "chains inside the ring");
     __shared__ __align__(16) float S[16 * SP];
-    __shared__ __align__(16) float chains[NW][8 * CS];
+    __shared__ __align__(16) float ring[RING ? NW * 2 * 2048 : NW * 8 * CS];
+    __shared__ __align__(16) float spare[RING ? NW * 64 : 1];
+    float (*chains)[8 * CS] = reinterpret_cast<float (*)[8 * CS]>(ring);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, x = lane & 15;
+    float *dslot = RING ? spare + 64 * w : chains[w];   /* this wave's per-lane slots for BD's outside updates */
     /* workgroups reach the 8 XCDs round-robin by linear id: head = id % 8 keeps each head's K, V and positional
      * rows in one XCD's L2 (with the head as the grid's second index every XCD fetched every head) */
     const int i0 = (int)(blockIdx.x / 8) * 16, h = (int)(blockIdx.x % 8);
@@ -725,61 +758,117 @@ __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const f
         }
         return a0 + a1;   /* lane holds D[4g + e][x]: key / position 4g + e of the tile, query x */
     };
-    /* tiles t = w, w + NW, … < n of one kind, in groups of MAXT: a group's rows are all requested before its first
-     * product (the loads' latency, thousands of cycles from L2, is what bounds a tile; one tile in flight at a time
-     * left the matrix cores idle most of the time) */
-    constexpr int MAXT = 4;
-    /* `between` runs once in every wave after the first group's loads are issued (the barrier before BD: its rows
-     * are on their way while the other waves finish AC) */
-    auto run_tiles = [&](int n, const float (&qq)[32], auto row_of, auto consume, auto between)
-                         __attribute__((always_inline)) {
-        float r[MAXT][32];
-        int t0 = w;
+    /* BD, shifted into S: row i reads positions j + T − 1 − i, so the 16 rows need positions lbase .. 2T − 2 − i0 */
+    const int ilast = min(i0 + 15, T - 1), lbase = T - 1 - ilast;
+    const int n_ac = Tp / 16, n_bd = (2 * T - 1 - i0 - lbase + 15) / 16;
+    /* each (i, j) is one lane's, once; a lane whose (i, j) lies outside the scores updates a slot of its own instead
+     * (in the chain buffer without RING, written again before the softmax reads it), so the four reads and writes
+     * need no branch */
+    auto consume_bd = [&](int pt, v4f acc) __attribute__((always_inline)) {
+        const int i = i0 + x;
+        int at[4];
+        float sv[4];
 #pragma unroll
-        for (int q = 0; q < MAXT; q++)
-            if (t0 + NW * q < n) load_row(row_of(t0 + NW * q), r[q]);
-        between();
-        while (t0 < n) {
+        for (int e = 0; e < 4; e++) {
+            const int j = lbase + 16 * pt + 4 * g + e - (T - 1 - i);
+            at[e] = (i < T && j >= 0 && j < T) ? x * SP + j : -1;
+            sv[e] = at[e] >= 0 ? S[at[e]] : dslot[lane];
+        }
 #pragma unroll
-            for (int q = 0; q < MAXT; q++)
-                if (t0 + NW * q < n) consume(t0 + NW * q, dot16(r[q], qq));
-            t0 += NW * MAXT;
-            if (t0 >= n) break;
+        for (int e = 0; e < 4; e++) {
+            const float r = __fmul_rn(__fadd_rn(sv[e], acc[e]), scale);
+            if (at[e] >= 0) S[at[e]] = r;
+            else dslot[lane] = r;
+        }
+    };
+    if constexpr (RING) {
+        /* Tiles (16 key or position rows × the head's 128 values, 8 KB) reach LDS by direct loads of two rows per
+         * instruction, into two slots per wave: tile q + 2 is requested as soon as tile q is read out, so one tile
+         * is always on its way while another is multiplied. Row r's 16-byte chunk cc lands at place cc ^ r of the
+         * row, so the operand reads (lane (x, g): row x, chunks 4c + g) hit 16 distinct places of every 256-byte
+         * window. Wave w takes AC tiles w, w + 8, … then BD tiles w, w + 8, …; no other wave reads its slots. */
+        const int nac = n_ac > w ? (n_ac - w + NW - 1) / NW : 0;
+        const int nbd = n_bd > w ? (n_bd - w + NW - 1) / NW : 0;
+        const int n = nac + nbd;
+        float *mine = ring + w * 2 * 2048;
+        auto issue = [&](int q) __attribute__((always_inline)) {
+            const bool ac = q < nac;
+            const int t = w + NW * (ac ? q : q - nac);
+            float *slot = mine + (q & 1) * 2048;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int r = 2 * k + (lane >> 5), cc = (lane & 31) ^ r;
+                const float *row = ac ? qkv + (size_t)min(16 * t + r, T - 1) * D3 + kD + h * kDh
+                                      : P + (size_t)min(lbase + 16 * t + r, L - 1) * kD + h * kDh;
+                dma_16(row + 4 * cc, slot + 256 * k);
+            }
+        };
+        auto read_tile = [&](int q, float (&r)[32]) __attribute__((always_inline)) {
+            const float *slot = mine + (q & 1) * 2048 + x * 128;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const float4 a = *reinterpret_cast<const float4 *>(slot + 4 * ((4 * c + g) ^ x));
+                r[4 * c] = a.x; r[4 * c + 1] = a.y; r[4 * c + 2] = a.z; r[4 * c + 3] = a.w;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* the slot is read out before it is refilled */
+            if (q + 2 < n) issue(q + 2);
+        };
+        /* the query operands are in registers before the first direct load (the compiler's waits for its own
+         * loads do not count the direct ones) */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (n > 0) issue(0);
+        if (n > 1) issue(1);
+        int q = 0;
+        for (; q < nac; q++) {   /* AC into S: S[x][16·kt + 4g + e] */
+            if (q + 1 < n) wait_vm<8>(); else wait_vm<0>();
+            float r[32];
+            read_tile(q, r);
+            const int kt = w + NW * q;
+            *reinterpret_cast<v4f *>(&S[x * SP + 16 * kt + 4 * g]) = dot16(r, qu);
+        }
+        __syncthreads();   /* every AC tile is in S before BD adds to it */
+        for (; q < n; q++) {
+            if (q + 1 < n) wait_vm<8>(); else wait_vm<0>();
+            float r[32];
+            read_tile(q, r);
+            consume_bd(w + NW * (q - nac), dot16(r, qv));
+        }
+    } else {
+        /* tiles t = w, w + NW, … < n of one kind, in groups of MAXT: a group's rows are all requested before its
+         * first product (the loads' latency, thousands of cycles from L2, is what bounds a tile; one tile in flight
+         * at a time left the matrix cores idle most of the time) */
+        constexpr int MAXT = 4;
+        /* `between` runs once in every wave after the first group's loads are issued (the barrier before BD: its
+         * rows are on their way while the other waves finish AC) */
+        auto run_tiles = [&](int n, const float (&qq)[32], auto row_of, auto consume, auto between)
+                             __attribute__((always_inline)) {
+            float r[MAXT][32];
+            int t0 = w;
 #pragma unroll
             for (int q = 0; q < MAXT; q++)
                 if (t0 + NW * q < n) load_row(row_of(t0 + NW * q), r[q]);
-        }
-    };
+            between();
+            while (t0 < n) {
+#pragma unroll
+                for (int q = 0; q < MAXT; q++)
+                    if (t0 + NW * q < n) consume(t0 + NW * q, dot16(r[q], qq));
+                t0 += NW * MAXT;
+                if (t0 >= n) break;
+#pragma unroll
+                for (int q = 0; q < MAXT; q++)
+                    if (t0 + NW * q < n) load_row(row_of(t0 + NW * q), r[q]);
+            }
+        };
 
-    /* AC into S: S[x][16·kt + 4g + e] */
-    run_tiles(Tp / 16, qu,
-              [&](int kt) { return qkv + (size_t)min(16 * kt + x, T - 1) * D3 + kD + h * kDh; },
-              [&](int kt, v4f acc) { *reinterpret_cast<v4f *>(&S[x * SP + 16 * kt + 4 * g]) = acc; }, [] {});
-    /* BD, shifted into S: row i reads positions j + T − 1 − i, so the 16 rows need positions lbase .. 2T − 2 − i0 */
-    const int ilast = min(i0 + 15, T - 1), lbase = T - 1 - ilast;
-    run_tiles((2 * T - 1 - i0 - lbase + 15) / 16, qv,
-              [&](int pt) { return P + (size_t)min(lbase + 16 * pt + x, L - 1) * kD + h * kDh; },
-              [&](int pt, v4f acc) {
-                  /* each (i, j) is one lane's, once; a lane whose (i, j) lies outside the scores updates a slot of
-                   * its own in the chain buffer instead (written again before the softmax reads it), so the four
-                   * reads and writes need no branch */
-                  const int i = i0 + x;
-                  int at[4];
-                  float sv[4];
-#pragma unroll
-                  for (int e = 0; e < 4; e++) {
-                      const int j = lbase + 16 * pt + 4 * g + e - (T - 1 - i);
-                      at[e] = (i < T && j >= 0 && j < T) ? x * SP + j : -1;
-                      sv[e] = at[e] >= 0 ? S[at[e]] : chains[w][lane];
-                  }
-#pragma unroll
-                  for (int e = 0; e < 4; e++) {
-                      const float r = __fmul_rn(__fadd_rn(sv[e], acc[e]), scale);
-                      if (at[e] >= 0) S[at[e]] = r;
-                      else chains[w][lane] = r;
-                  }
-              },
-              [] { __syncthreads(); });
+        /* AC into S: S[x][16·kt + 4g + e] */
+        run_tiles(n_ac, qu,
+                  [&](int kt) { return qkv + (size_t)min(16 * kt + x, T - 1) * D3 + kD + h * kDh; },
+                  [&](int kt, v4f acc) { *reinterpret_cast<v4f *>(&S[x * SP + 16 * kt + 4 * g]) = acc; }, [] {});
+        run_tiles(n_bd, qv,
+                  [&](int pt) { return P + (size_t)min(lbase + 16 * pt + x, L - 1) * kD + h * kDh; },
+                  consume_bd,
+                  [] { __syncthreads(); });
+    }
     __syncthreads();
     /* O[i0 + x][16c + 4g + e] = Σ_j p[x][j]·V[j][16c + 4g + e], j = 4s + g, for output dimensions c = w, over
      * all steps: chunks of CH steps, the next chunk's V loaded while the current one is multiplied, four
@@ -1509,30 +1598,6 @@ struct FvGeo {
     static_assert(FN <= 4 && FM <= 16, "epilogue factors: one column and one row per thread");
     static_assert(D >= 2 && D * STAGE <= 160 * 1024, "LDS ring");
 };
-
-/* Direct global → LDS loads (16 bytes per lane into 16-byte lane slots at lds + 16·lane). Issued from inline
- * assembly so that the compiler adds no waits of its own for them: the GEMM waits for them explicitly (wait_vm),
- * and the compiler's waits for its own loads stay correct since the vector-memory counter retires in order. */
-__device__ __forceinline__ void dma_16(const void *src, const void *lds)
-{
-    const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(a) : "memory", "m0");
-}
-
-/* s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left open); a compiler barrier for memory operations */
-template <int N>
-__device__ __forceinline__ void wait_vm()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-    asm volatile("" ::: "memory");
-}
-
-/* this wave's LDS reads complete, then the workgroup barrier; no wait on vector memory */
-__device__ __forceinline__ void lds_barrier()
-{
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 /* The int8 five-value GEMM (sgemm_i8_worker, blas.c:1296-1370) on operand records.
  *  A workgroup of NW waves owns a BM × BN output tile; wave w owns its FN 16-column groups for all FM 16-row groups,
