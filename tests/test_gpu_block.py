@@ -106,7 +106,8 @@ def _attention_reference(qkv, bu, bv, pos):
     return np.matmul(p.astype(np.float64), v.astype(np.float64))
 
 
-@pytest.mark.parametrize("T,gain", [(375, 1.0), (375, 3.0), (1, 1.0), (17, 1.0), (100, 2.0), (700, 1.0)])
+@pytest.mark.parametrize("T,gain", [(375, 1.0), (375, 3.0), (1, 1.0), (17, 1.0), (100, 2.0), (384, 1.0), (385, 1.0),
+                                    (700, 1.0)])
 def test_attention_heads(T, gain):
     """p2h_attention_heads (one kernel: scores, relative shift, softmax, product with V) against float64 products
     around the oracle's softmax: the kernel's products are fp32 matrix-core sums, so per output row (128 values) the
