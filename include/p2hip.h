@@ -160,6 +160,13 @@ int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed ch
 int p2h_fvb_gemm_q8a_next(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                           const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
                           size_t workspace_bytes, const P2hWeight *next, void *stream);
+/* C [M][N] = SiLU(alpha·A·W) (beta 0, ldc = N, N % 8 == 0): the feed-forward's up-projection followed by the SiLU
+ * that p2_swish_quant_rows applies before quantising (tensor_ops.c:491-511, encoder.c:345-346), as the AVX2 body's
+ * polynomial per element, the same bits as p2h_fvb_gemm_q8a then p2h_silu. Small-M tiles apply it as they store C;
+ * the others by a second kernel. */
+int p2h_fvb_gemm_q8a_silu(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                          const float *dScales, const P2hWeight *w, float *dC, void *workspace,
+                          size_t workspace_bytes, void *stream);
 /* The same product for `groups` (<= 32) weights of one shape [K, N] against the same quantised rows, C_q = alpha·A·W_q
  * + beta·C_q, in one launch where the small-M kernel serves the shape (M <= 1024, K <= 4096), otherwise one call per
  * weight; results are those of p2h_fvb_gemm_q8a per weight. No counterpart in the reference: it batches products
@@ -254,6 +261,10 @@ int p2h_depthwise_conv_silu(int T, const float *dGated, const float *dW, const f
  * [1024][T], the same bits, without the gated buffer. */
 int p2h_glu_depthwise_conv_silu(int T, const float *dPW1, const float *dW, const float *dB, float *dOut,
                                 void *stream);
+/* The same with out [T][1024]: the transpose of the channel-major output, the rows that channel_major_to_rows
+ * (encoder.c:554-568) would make for the pw2 linear; the same bits. */
+int p2h_glu_depthwise_conv_silu_rows(int T, const float *dPW1, const float *dW, const float *dB, float *dOut,
+                                     void *stream);
 int p2h_silu(size_t n, float *dX, void *stream);
 int p2h_add_residual(int T, float *dX, const float *dY, float alpha, void *stream);
 int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta, float *dY,

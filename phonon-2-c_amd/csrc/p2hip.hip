@@ -832,7 +832,20 @@ int p2h_glu_depthwise_conv_silu(int T, const float *dPW1, const float *dW, const
     if (T < 0) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu: T = %d", T);
     if (T == 0) return P2H_OK;
     if (!dPW1 || !dW || !dB || !dOut) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu: null pointer");
-    hipLaunchKernelGGL(p2k::glu_dwconv_silu, dim3((unsigned)((T + 31) / 32), p2k::kD / 16), dim3(256), 0,
+    hipLaunchKernelGGL(p2k::glu_dwconv_silu<false>, dim3((unsigned)((T + 31) / 32), p2k::kD / 16), dim3(256), 0,
+                       stream_of(stream), T, dPW1, dW, dB, dOut);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_glu_depthwise_conv_silu_rows(int T, const float *dPW1, const float *dW, const float *dB, float *dOut,
+                                     void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    if (T < 0) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu_rows: T = %d", T);
+    if (T == 0) return P2H_OK;
+    if (!dPW1 || !dW || !dB || !dOut) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu_rows: null pointer");
+    hipLaunchKernelGGL(p2k::glu_dwconv_silu<true>, dim3((unsigned)((T + 31) / 32), p2k::kD / 16), dim3(256), 0,
                        stream_of(stream), T, dPW1, dW, dB, dOut);
     HIPCHK(hipGetLastError());
     return P2H_OK;
@@ -1090,7 +1103,7 @@ size_t p2h_fvb_q8a_workspace_bytes(int mode, int M, int N, int K)
 
 static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                         const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
-                        size_t workspace_bytes, const P2hWeight *next, void *stream);
+                        size_t workspace_bytes, const P2hWeight *next, void *stream, bool silu = false);
 
 int p2h_fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                      const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
@@ -1108,11 +1121,23 @@ int p2h_fvb_gemm_q8a_next(int mode, int M, int N, int K, float alpha, const sign
                         stream);
 }
 
+int p2h_fvb_gemm_q8a_silu(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
+                          const float *dScales, const P2hWeight *w, float *dC, void *workspace,
+                          size_t workspace_bytes, void *stream)
+{
+    return fvb_gemm_q8a(mode, M, N, K, alpha, dQ, ldq, dScales, w, 0.0f, dC, N, workspace, workspace_bytes, nullptr,
+                        stream, true);
+}
+
+/* silu: C = silu_p2(alpha·A·W) with beta 0, ldc = N and N % 8 == 0 (p2_swish over whole rows: every element in
+ * the eight-wide body); small-M tiles apply it in their epilogue, the others by p2h_silu after the GEMM. */
 static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed char *dQ, int ldq,
                         const float *dScales, const P2hWeight *w, float beta, float *dC, int ldc, void *workspace,
-                        size_t workspace_bytes, const P2hWeight *next, void *stream)
+                        size_t workspace_bytes, const P2hWeight *next, void *stream, bool silu)
 {
     if (int rc = ensure_init()) return rc;
+    if (silu && (beta != 0.0f || ldc != N || N % 8 != 0))
+        return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_silu: needs beta 0, ldc = N and N %% 8 == 0 (N = %d)", N);
     if (mode != P2H_INT8W && mode != P2H_INT8)
         return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a: mode %d is not an int8 mode", mode);
     if (!w || w->N != N || w->K != K)
@@ -1123,7 +1148,8 @@ static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed
     hipStream_t s = stream_of(stream);
     if (M == 0) return P2H_OK;
     if (alpha == 0.0f) return p2h_scale_c(M, N, beta, dC, ldc, s);            /* blas.c:1434 */
-    if (K == 0) return (beta != 0.0f) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;   /* no K block runs */
+    if (K == 0)   /* no K block runs (SiLU of the zero product: zeros) */
+        return (beta != 0.0f || silu) ? p2h_scale_c(M, N, beta, dC, ldc, s) : P2H_OK;
     Plan p = make_plan(mode, M, N, K, workspace != nullptr);
     if (int rc = check_split_ws("p2h_fvb_gemm_q8a", p, workspace, workspace_bytes)) return rc;
     p2k::GemmArgs g = gemm_args(M, N, K, alpha, beta, dQ, ldq, dScales, dC, ldc, p, workspace);
@@ -1134,6 +1160,8 @@ static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed
         g.warm = next->rec4;
         g.warm_lines = (int)std::min<size_t>((bytes + 127) / 128, 0x7fffffff);
     }
+    const bool silu_here = silu && is_small(p.cfg);
+    g.act = silu_here ? 1 : 0;
     if (mode == P2H_INT8W) {
         g.c1 = w->c1w;
         launch_fv_cfg<p2k::MODE_INT8W>(g, p, s);
@@ -1142,6 +1170,7 @@ static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed
         launch_fv_cfg<p2k::MODE_INT8>(g, p, s);
     }
     HIPCHK(hipGetLastError());
+    if (silu && !silu_here) return p2h_silu((size_t)M * N, dC, s);
     return P2H_OK;
 }
 
@@ -1642,13 +1671,18 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
     auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2) {
         P2H_TRY(layer_norm(g, b));
-        P2H_TRY(linear(l1, D, FF, 1.0f, 0.0f, w.ln, w.h));
+        if (mode != P2H_EXACT) {   /* SiLU in the up-projection's epilogue, then the plain quantiser */
+            P2H_TRY(fvb_gemm_q8a(mode, T, FF, D, 1.0f, w.q, ldD, w.sc, l1, 0.0f, w.h, FF, w.gws, w.gws_bytes,
+                                 nullptr, s, true));
+            P2H_TRY(p2h_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
+        } else {
+            P2H_TRY(linear(l1, D, FF, 1.0f, 0.0f, w.ln, w.h));
+        }
         if (mode == P2H_EXACT) {
             P2H_TRY(p2h_silu((size_t)T * FF, w.h, s));
             P2H_TRY(linear(l2, FF, D, 1.0f, 0.0f, w.h, w.out));
             return p2h_add_residual(T, dX, w.out, 0.5f, s);
         }
-        P2H_TRY(p2h_silu_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
         return linear(l2, FF, D, 0.5f, 1.0f, nullptr, dX);
     };
     P2H_TRY(feed_forward(blk->norm_ff1_w, blk->norm_ff1_b, blk->ff1_l1, blk->ff1_l2));
@@ -1687,13 +1721,13 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     /* conv_module (encoder.c:573-613) */
     P2H_TRY(layer_norm(blk->norm_conv_w, blk->norm_conv_b));
     P2H_TRY(linear(blk->pw1, D, 2 * D, 1.0f, 0.0f, w.ln, w.h));
-    P2H_TRY(p2h_glu_depthwise_conv_silu(T, w.h, blk->dw_w, blk->dw_b, w.dw, s));
+    /* the convolution's output as rows [T][1024] (channel_major_to_rows' transpose made by the kernel's stores) */
+    P2H_TRY(p2h_glu_depthwise_conv_silu_rows(T, w.h, blk->dw_w, blk->dw_b, w.dw, s));
     if (mode == P2H_EXACT) {
-        P2H_TRY(p2h_channel_major_rows(T, w.dw, w.attn, s));
-        P2H_TRY(linear(blk->pw2, D, D, 1.0f, 0.0f, w.attn, w.out));
+        P2H_TRY(linear(blk->pw2, D, D, 1.0f, 0.0f, w.dw, w.out));
         P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
     } else {
-        P2H_TRY(p2h_channel_major_quant_rows(D, T, w.dw, w.q, ldD, w.sc, s));
+        P2H_TRY(p2h_quant_rows(T, D, w.dw, D, w.q, ldD, w.sc, s));
         P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, nullptr, dX));
     }
     P2H_TRY(feed_forward(blk->norm_ff2_w, blk->norm_ff2_b, blk->ff2_l1, blk->ff2_l2));

@@ -1018,7 +1018,10 @@ __global__ __launch_bounds__(256) void dwconv_silu(int T, const float *__restric
  * depthwise convolution's output takes the GLU of frames t0 − 4 .. t0 + 35 of its channels into LDS (the halo is
  * computed twice, by both neighbouring tiles) and the channels' taps, then each output runs dwconv_silu's chain over
  * the LDS values. Every value is made by the same operations as in the two kernels, so the result is the same bits;
- * the gated [1024][T] buffer is never written. Grid (ceil(T / 32), 64): 768 workgroups at T = 375. */
+ * the gated [1024][T] buffer is never written. Grid (ceil(T / 32), 64): 768 workgroups at T = 375.
+ * ROWS: out is [T][1024] (the transpose of the reference's channel-major output, as the next linear reads it),
+ * consecutive threads writing consecutive channels of a frame; else [1024][T]. */
+template <bool ROWS>
 __global__ __launch_bounds__(256) void glu_dwconv_silu(int T, const float *__restrict__ pw1, const float *__restrict__ w,
                                                        const float *__restrict__ bias, float *__restrict__ out)
 {
@@ -1040,7 +1043,7 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu(int T, const float *__res
     }
     __syncthreads();
     for (int i = tid; i < TT * CB; i += 256) {
-        const int dl = i / TT, tl = i % TT, t = t0 + tl;
+        const int dl = ROWS ? i % CB : i / TT, tl = ROWS ? i / CB : i % TT, t = t0 + tl;
         if (t >= T) continue;
         float v = wt[CB * kConvK + dl];
 #pragma unroll
@@ -1048,7 +1051,8 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu(int T, const float *__res
             const int src = t - HALO + k;
             if (src >= 0 && src < T) v = __builtin_fmaf(gt[dl][tl + k], wt[dl * kConvK + k], v);
         }
-        out[(size_t)(d0 + dl) * T + t] = silu_p2(v);
+        if (ROWS) out[(size_t)t * kD + d0 + dl] = silu_p2(v);
+        else out[(size_t)(d0 + dl) * T + t] = silu_p2(v);
     }
 }
 
@@ -1091,6 +1095,7 @@ struct GemmArgs {
     int kst;                                              /* 64-column steps per 16-row group of Q: ldq / 64 */
     int mg_last, ng_last;                                 /* last 16-row group of Q, last 16-column group of C */
     const uint8_t *warm; int warm_lines;                  /* 128-byte lines a later kernel reads, loaded meanwhile */
+    int act;                                              /* small-M tiles: 1 stores silu_p2 of each output */
 };
 
 
@@ -2142,6 +2147,10 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
                 if (TWO) f = __builtin_fmaf((float)sumT[e], c2[e], f);
                 run[e] = (blk == 0 && beta_zero) ? f * as : __builtin_fmaf(f, as, run[e]);
             }
+        }
+        if (g.act) {   /* the feed-forward's SiLU (p2_swish_quant_rows' body, tensor_ops.c:491-511) on the output */
+#pragma unroll
+            for (int e = 0; e < 4; e++) run[e] = silu_p2(run[e]);
         }
         if (g.c_vec4) {
             *reinterpret_cast<v4f *>(cp) = v4f{run[0], run[1], run[2], run[3]};

@@ -73,6 +73,7 @@ _HIP_SIG = {
     "p2h_q_bytes": (C.c_size_t, [_i, _i]),
     "p2h_fvb_gemm_q8a": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp]),
     "p2h_fvb_gemm_q8a_next": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _sz, _vp, _vp]),
+    "p2h_fvb_gemm_q8a_silu": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "p2h_fvb_gemm_q8a_grouped": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _f, _vp, _i, _vp]),
     "p2h_fvb_q8a_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_fvb_plan": (C.c_char_p, [_i, _i, _i, _i, _i]),
@@ -90,6 +91,7 @@ _HIP_SIG = {
     "p2h_combine_softmax": (_i, [_i, _vp, _vp, _vp]),
     "p2h_attention_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "p2h_glu_depthwise_conv_silu": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_glu_depthwise_conv_silu_rows": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
     "p2h_conformer_stack_workspace_bytes": (_sz, [_i, _i, _i]),
     "p2h_conformer_stack": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "p2h_glu_channel_major": (_i, [_i, _vp, _vp, _vp]),
@@ -508,6 +510,22 @@ def fvb_gemm_q8a(mode, q, scales, w, alpha=1.0, beta=0.0, C0=None, split=True, w
     return dC.download(C0.shape, np.float32)
 
 
+def fvb_gemm_q8a_silu(mode, q, scales, w, alpha=1.0, ws=None):
+    """p2h_fvb_gemm_q8a_silu on a quantised host matrix q [M, K]: SiLU(alpha·A·W) as [M, N]."""
+    q = np.ascontiguousarray(q, np.int8)
+    M, K = q.shape
+    N = w.N
+    ldq = q_ld(K)
+    dQ, dS = to_device(q_tile(q, ldq)), to_device(np.ascontiguousarray(scales, np.float32))
+    dC = DeviceBuffer(max(M * N, 1) * 4)
+    dC.upload(np.full(max(M * N, 1), np.nan, np.float32))   # every output must be written
+    if ws is None:
+        ws = Workspace(q8a_workspace_bytes(mode, M, N, K))
+    _ok(hip().p2h_fvb_gemm_q8a_silu(MODES.get(mode, mode), M, N, K, alpha, dQ.ptr, ldq, dS.ptr, w.ptr, dC.ptr,
+                                    ws.ptr, ws.nbytes, None), "p2h_fvb_gemm_q8a_silu")
+    return dC.download((M, N), np.float32)
+
+
 def fvb_acc_i32(mode, q, w):
     """The raw int32 sums of the int8 kernel over all K: one matrix (int8w) or the S and T sums (int8)."""
     q = np.ascontiguousarray(q, np.int8)
@@ -641,11 +659,15 @@ def depthwise_conv_silu(gated, w, b):
     return dO.download(gated.shape, np.float32)
 
 
-def glu_depthwise_conv_silu(pw1, w, b):
-    """pw1 [T, 2048] → SiLU(depthwise conv(GLU(pw1))) as [1024, T], one kernel."""
+def glu_depthwise_conv_silu(pw1, w, b, rows=False):
+    """pw1 [T, 2048] → SiLU(depthwise conv(GLU(pw1))) as [1024, T] (rows: as [T, 1024]), one kernel."""
     pw1 = _f32(pw1)
     T = pw1.shape[0]
     dP, dW, dB, dO = to_device(pw1), to_device(_f32(w)), to_device(_f32(b)), DeviceBuffer(T * D_MODEL * 4)
+    if rows:
+        _ok(hip().p2h_glu_depthwise_conv_silu_rows(T, dP.ptr, dW.ptr, dB.ptr, dO.ptr, None),
+            "p2h_glu_depthwise_conv_silu_rows")
+        return dO.download((T, D_MODEL), np.float32)
     _ok(hip().p2h_glu_depthwise_conv_silu(T, dP.ptr, dW.ptr, dB.ptr, dO.ptr, None), "p2h_glu_depthwise_conv_silu")
     return dO.download((D_MODEL, T), np.float32)
 

@@ -159,6 +159,25 @@ def test_glu_depthwise_conv_silu_fused(T):
     assert np.array_equal(got.view(np.uint32), two.view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [375, 33, 32, 31, 1])
+def test_glu_depthwise_conv_silu_rows(T):
+    """The row-major variant is the transpose of the channel-major output bit for bit, and its rows quantised by
+    the plain quantiser equal the channel-major→int8 producer's codes and scales (the block's int8 route)."""
+    print(f"glu_depthwise_conv_silu_rows T={T}", flush=True)
+    rng = np.random.default_rng(SEED + 23 * T)
+    pw1 = (rng.standard_normal((T, 2 * D)) * 2).astype(np.float32)
+    w = (rng.standard_normal((D, 9)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    cm = P.glu_depthwise_conv_silu(pw1, w, b)
+    rows = P.glu_depthwise_conv_silu(pw1, w, b, rows=True)
+    assert rows.shape == (T, D)
+    assert np.array_equal(rows.view(np.uint32), np.ascontiguousarray(cm.T).view(np.uint32))
+    q1, s1 = P.quant_rows(rows)
+    q2, s2 = P.channel_major_quant_rows(cm)
+    assert np.array_equal(q1, q2)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [375 * 4096, 1001])
 def test_silu_flat(n):
     """The eight-wide body bit-exact; the tail (n mod 8 elements, expf) within 4 ulp."""

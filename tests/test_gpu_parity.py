@@ -309,6 +309,22 @@ def test_q8a_next_matches_q8a(mode, M, K, N, Kn, Nn, beta):
         assert _bits_equal(dC.download((M, N), np.float32), single), f"call {rep}"
 
 
+# ── the feed-forward's SiLU in the up-projection's epilogue ───────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+@pytest.mark.parametrize("M,K,N", [(375, 1024, 4096), (38, 1024, 4096), (375, 4096, 272), (2000, 1024, 1024)])
+def test_q8a_silu_matches_gemm_then_silu(mode, M, K, N):
+    """p2h_fvb_gemm_q8a_silu equals p2h_fvb_gemm_q8a followed by p2h_silu bit for bit: the small-M tiles apply
+    silu_p2 as they store C; at 2000 rows (the large-M kernel) the library runs the SiLU kernel after the GEMM."""
+    A = P.gen_activations(SEED, 1900 + M, M, K)
+    q, sc = O.quant_rows(A)
+    w = P.FvWeight(*_weight(K, N, 1910 + N), K, N)
+    got = P.fvb_gemm_q8a_silu(mode, q, sc, w, alpha=0.7)
+    ref = P.silu(P.fvb_gemm_q8a(mode, q, sc, w, alpha=0.7))
+    assert np.isfinite(got).all()
+    assert _bits_equal(got, ref)
+
+
 # ── several weights against the same quantised rows in one launch ─────────────────────────────────────────────────
 
 @pytest.mark.parametrize("mode", ["int8w", "int8"])
