@@ -281,6 +281,10 @@ int p2h_channel_major_rows(int T, const float *dDW, float *dY, void *stream);
 #define P2H_ATTENTION_TMAX 768
 int p2h_attention_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
                         float *dAttnH, void *stream);
+/* The same written as attn [T][1024], head h at columns 128·h: the rows concat_heads makes (encoder.c:449-463) for
+ * the output linear; the same bits. */
+int p2h_attention_rows(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
+                       float *dAttn, void *stream);
 
 /* One FastConformer block on the device (conformer_block, encoder.c:617-625): feed-forward ½, relative-position
  * self-attention, convolution module, feed-forward ½, final LayerNorm, on X [T][1024] in place. The five-value

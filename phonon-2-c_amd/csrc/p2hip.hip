@@ -781,23 +781,38 @@ int p2h_combine_softmax(int T, float *dAC, const float *dBD, void *stream)
     return P2H_OK;
 }
 
-int p2h_attention_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
-                        float *dAttnH, void *stream)
+static int attention(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
+                     float *dAttnH, int rows, void *stream)
 {
     if (int rc = ensure_init()) return rc;
     if (T < 0 || T > P2H_ATTENTION_TMAX)
-        return fail(P2H_E_ARG, "p2h_attention_heads: T = %d (1 .. %d)", T, P2H_ATTENTION_TMAX);
+        return fail(P2H_E_ARG, "p2h_attention: T = %d (1 .. %d)", T, P2H_ATTENTION_TMAX);
     if (T == 0) return P2H_OK;
-    if (!dQKV || !dBiasU || !dBiasV || !dP || !dAttnH) return fail(P2H_E_ARG, "p2h_attention_heads: null pointer");
+    if (!dQKV || !dBiasU || !dBiasV || !dP || !dAttnH) return fail(P2H_E_ARG, "p2h_attention: null pointer");
     if (!aligned(dQKV, 16) || !aligned(dBiasU, 16) || !aligned(dBiasV, 16) || !aligned(dP, 16) || !aligned(dAttnH, 16))
-        return fail(P2H_E_ARG, "p2h_attention_heads: operands must be 16-byte aligned");
+        return fail(P2H_E_ARG, "p2h_attention: operands must be 16-byte aligned");
     const float scale = 1.0f / sqrtf((float)p2k::kDh);   /* encoder.c:521 */
     const dim3 grid((unsigned)(p2k::kH * ((T + 15) / 16)));
     hipStream_t s = stream_of(stream);
-    if (T <= 64 * 6) hipLaunchKernelGGL(p2k::attention_rel<6>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH);
-    else hipLaunchKernelGGL(p2k::attention_rel<12>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH);
+    if (T <= 64 * 6)
+        hipLaunchKernelGGL(p2k::attention_rel<6>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH, rows);
+    else
+        hipLaunchKernelGGL(p2k::attention_rel<12>, grid, dim3(512), 0, s, T, scale, dQKV, dBiasU, dBiasV, dP, dAttnH,
+                           rows);
     HIPCHK(hipGetLastError());
     return P2H_OK;
+}
+
+int p2h_attention_heads(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
+                        float *dAttnH, void *stream)
+{
+    return attention(T, dQKV, dBiasU, dBiasV, dP, dAttnH, 0, stream);
+}
+
+int p2h_attention_rows(int T, const float *dQKV, const float *dBiasU, const float *dBiasV, const float *dP,
+                       float *dAttn, void *stream)
+{
+    return attention(T, dQKV, dBiasU, dBiasV, dP, dAttn, 1, stream);
 }
 
 int p2h_glu_channel_major(int T, const float *dPW1, float *dGated, void *stream)
@@ -1693,8 +1708,9 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         P2H_TRY(p2h_fvb_gemm(mode, L, D, D, 1.0f, dPE, D, blk->pos, 0.0f, w.p, D, w.gws, w.gws_bytes, s));
         dP = w.p;
     }
-    if (fused_attention(T, blk)) {   /* scores, shift, softmax and the product with V in one kernel */
-        P2H_TRY(p2h_attention_heads(T, w.qkv, blk->bias_u, blk->bias_v, dP, w.attn_h, s));
+    const bool fused = fused_attention(T, blk);
+    if (fused) {   /* scores, shift, softmax and the product with V in one kernel, written as the heads' rows */
+        P2H_TRY(p2h_attention_rows(T, w.qkv, blk->bias_u, blk->bias_v, dP, w.attn_h, s));
     } else {
         /* Q_u, Q_v as [H, T, Dh] (the bias adds of gather_heads); the products read K, V and the positional rows
          * where they lie, head h at column offset h·Dh of its row (the transposes of gather_heads and transpose_pos
@@ -1710,12 +1726,14 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         P2H_TRY(p2h_sgemm_batched(0, 0, T, Dh, T, 1.0f, w.ac, T, (long long)T * T, w.qkv + 2 * D, 3 * D, Dh, 0.0f,
                                   w.attn_h, Dh, (long long)T * Dh, H, s));
     }
+    /* w.attn_h: the heads' rows [T][1024] from the fused kernel, else [H][T][Dh] for the concatenation */
     if (mode == P2H_EXACT) {
-        P2H_TRY(p2h_concat_heads_rows(T, w.attn_h, w.attn, s));
-        P2H_TRY(linear(blk->out, D, D, 1.0f, 0.0f, w.attn, w.out));
+        if (!fused) P2H_TRY(p2h_concat_heads_rows(T, w.attn_h, w.attn, s));
+        P2H_TRY(linear(blk->out, D, D, 1.0f, 0.0f, fused ? w.attn_h : w.attn, w.out));
         P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
     } else {
-        P2H_TRY(p2h_concat_heads_quant_rows(H, T, Dh, w.attn_h, w.q, ldD, w.sc, s));
+        if (fused) P2H_TRY(p2h_quant_rows(T, D, w.attn_h, D, w.q, ldD, w.sc, s));
+        else P2H_TRY(p2h_concat_heads_quant_rows(H, T, Dh, w.attn_h, w.q, ldD, w.sc, s));
         P2H_TRY(linear(blk->out, D, D, 1.0f, 1.0f, nullptr, dX));
     }
     /* conv_module (encoder.c:573-613) */

@@ -686,7 +686,8 @@ __device__ __forceinline__ void lds_barrier()
 /* Relative-position self-attention of one head for 16 query rows (encoder.c:495-523 between the projections): the
  * scores S[i][j] = (Q_u[i]·K[j] + Q_v[i]·P[j + T − 1 − i])·scale, their softmax over j as combine_softmax_rows
  * computes it (the AVX2 route's order, the same operations), and O[i] = Σ_j softmax(S)[i][j]·V[j], written to
- * out [8][T][128]. Q_u = Q + bias_u and Q_v = Q + bias_v are formed as the operands load (gather_heads' additions);
+ * out [8][T][128] (with `rows`, [T][1024]). Q_u = Q + bias_u and Q_v = Q + bias_v are formed as the operands load
+ * (gather_heads' additions);
  * Q, K and V are read inside QKV [T][3·1024] and the positional rows inside P [2T − 1][1024], head h at column
  * offset 128·h. The scores live in LDS only: neither the [T, T] and [T, 2T − 1] products nor the half of the
  * positional product that no row reads is made. Products on v_mfma_f32_16x16x4_f32 (D = A·B with A's rows and B's
@@ -702,7 +703,7 @@ __device__ __forceinline__ void lds_barrier()
 template <int NM>
 __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const float *__restrict__ qkv,
                                                      const float *__restrict__ bu, const float *__restrict__ bv,
-                                                     const float *__restrict__ P, float *__restrict__ out)
+                                                     const float *__restrict__ P, float *__restrict__ out, int rows)
 {
     constexpr int SP = 64 * NM + 4;   /* score row pitch (floats): 16 rows 4 banks apart */
     constexpr int CS = 8 * NM + 4;    /* softmax chain stride */
@@ -967,7 +968,9 @@ __global__ __launch_bounds__(512) void attention_rel(int T, float scale, const f
         }
     }
     const v4f acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
-    if (i0 + x < T) *reinterpret_cast<v4f *>(out + ((size_t)h * T + i0 + x) * kDh + 16 * c + 4 * g) = acc;
+    /* rows: out [T][1024], head h at columns 128·h (concat_heads' layout, encoder.c:449-463); else [8][T][128] */
+    const size_t at = rows ? (size_t)(i0 + x) * kD + h * kDh : ((size_t)h * T + i0 + x) * kDh;
+    if (i0 + x < T) *reinterpret_cast<v4f *>(out + at + 16 * c + 4 * g) = acc;
 }
 
 /* glu_to_channel_major (encoder.c:543-555): gated[d][t] = pw1[t][d] / (1 + expf(−pw1[t][D + d])), the exponent's

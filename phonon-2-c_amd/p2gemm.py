@@ -90,6 +90,7 @@ _HIP_SIG = {
     "p2h_transpose_pos": (_i, [_i, _vp, _vp, _vp]),
     "p2h_combine_softmax": (_i, [_i, _vp, _vp, _vp]),
     "p2h_attention_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_attention_rows": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "p2h_glu_depthwise_conv_silu": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
     "p2h_glu_depthwise_conv_silu_rows": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
     "p2h_conformer_stack_workspace_bytes": (_sz, [_i, _i, _i]),
@@ -633,12 +634,16 @@ def combine_softmax(ac, bd):
     return dA.download(ac.shape, np.float32)
 
 
-def attention_heads(qkv, bias_u, bias_v, P):
-    """p2h_attention_heads on host arrays: QKV [T, 3072], bias_u / bias_v [1024], P [2T − 1, 1024] → [8, T, 128]."""
+def attention_heads(qkv, bias_u, bias_v, P, rows=False):
+    """p2h_attention_heads on host arrays: QKV [T, 3072], bias_u / bias_v [1024], P [2T − 1, 1024] → [8, T, 128]
+    (rows: p2h_attention_rows → [T, 1024])."""
     qkv = _f32(qkv)
     T = qkv.shape[0]
     dq, du, dv, dp = to_device(qkv), to_device(_f32(bias_u)), to_device(_f32(bias_v)), to_device(_f32(P))
     dO = DeviceBuffer(T * D_MODEL * 4)
+    if rows:
+        _ok(hip().p2h_attention_rows(T, dq.ptr, du.ptr, dv.ptr, dp.ptr, dO.ptr, None), "p2h_attention_rows")
+        return dO.download((T, D_MODEL), np.float32)
     _ok(hip().p2h_attention_heads(T, dq.ptr, du.ptr, dv.ptr, dp.ptr, dO.ptr, None), "p2h_attention_heads")
     return dO.download((N_HEADS, T, HEAD_DIM), np.float32)
 

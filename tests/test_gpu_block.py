@@ -125,6 +125,25 @@ def test_attention_heads(T, gain):
     assert d.max() <= 2e-5
 
 
+@pytest.mark.parametrize("T", [375, 17, 385])
+def test_attention_rows(T):
+    """p2h_attention_rows is p2h_attention_heads' output concatenated by head (concat_heads' rows), bit for bit, and
+    its rows quantised by the plain quantiser equal the concatenation→int8 producer's codes and scales."""
+    print(f"attention_rows T={T}", flush=True)
+    rng = np.random.default_rng(SEED + 29 * T)
+    qkv = rng.standard_normal((T, 3 * D)).astype(np.float32)
+    bu, bv = (rng.standard_normal(D) * 0.1).astype(np.float32), (rng.standard_normal(D) * 0.1).astype(np.float32)
+    pos = rng.standard_normal((2 * T - 1, D)).astype(np.float32)
+    heads = P.attention_heads(qkv, bu, bv, pos)
+    rows = P.attention_heads(qkv, bu, bv, pos, rows=True)
+    cat = np.ascontiguousarray(heads.transpose(1, 0, 2).reshape(T, D))
+    assert np.array_equal(rows.view(np.uint32), cat.view(np.uint32))
+    q1, s1 = P.quant_rows(rows)
+    q2, s2 = P.concat_heads_quant_rows(heads)
+    assert np.array_equal(q1, q2)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [375, 7])
 def test_glu_channel_major(T):
     print(f"glu T={T}", flush=True)
