@@ -1683,15 +1683,17 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         if (mode == P2H_EXACT) return p2h_layer_norm_rows(T, D, dX, D, g, b, w.ln, D, s);
         return p2h_layer_norm_quant_rows(T, D, dX, D, g, b, w.q, ldD, w.sc, s);
     };
+    static const bool silu_epilogue = env_int("P2H_SILU_EPILOGUE", 1) != 0;   /* 0: the SiLU→int8 producer instead */
     /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
     auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2) {
         P2H_TRY(layer_norm(g, b));
-        if (mode != P2H_EXACT) {   /* SiLU in the up-projection's epilogue, then the plain quantiser */
+        if (mode != P2H_EXACT && silu_epilogue) {   /* SiLU in the up-projection's epilogue, then the plain quantiser */
             P2H_TRY(fvb_gemm_q8a(mode, T, FF, D, 1.0f, w.q, ldD, w.sc, l1, 0.0f, w.h, FF, w.gws, w.gws_bytes,
                                  nullptr, s, true));
             P2H_TRY(p2h_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
         } else {
             P2H_TRY(linear(l1, D, FF, 1.0f, 0.0f, w.ln, w.h));
+            if (mode != P2H_EXACT) P2H_TRY(p2h_silu_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
         }
         if (mode == P2H_EXACT) {
             P2H_TRY(p2h_silu((size_t)T * FF, w.h, s));
