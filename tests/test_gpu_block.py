@@ -266,8 +266,11 @@ def _distance(a, ref):
 
 @pytest.mark.skipif(not O.refblock_available(), reason="reference block library not built")
 @pytest.mark.parametrize("mode,T", [("int8w", 375), ("int8", 375), ("exact", 375), ("int8w", 40), ("exact", 9),
-                                    ("int8", 1)])
+                                    ("int8", 1), ("int8w", 500), ("exact", 520), ("int8w", 800)])
 def test_block_against_reference(mode, T, tmp_path):
+    """The device block against the reference engine's conformer_block (built from its sources) at T where the
+    attention runs in each of its forms: T <= 384 the fused kernel with its tiles in LDS, 385..768 the fused kernel
+    with its tiles in registers, beyond the separate products and softmax."""
     print(f"conformer block mode={mode} T={T}", flush=True)
     sys.path.insert(0, HERE)
     import refblock_child as RC
