@@ -138,6 +138,13 @@ int p2h_recip_selftest(unsigned long long *result3);
 
 int p2h_layer_norm_quant_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta,
                               signed char *dQ, int ldq, float *dScales, void *stream);
+/* Two LayerNorms of the same rows in one pass (the block's output norm, then the next block's first norm:
+ * encoder.c:623 then 342): Y = LayerNorm(X; gamma1, beta1) as fp32 rows [M][ldy] (Y may be X), then the int8 rows
+ * and scales of LayerNorm(Y; gamma2, beta2), each as p2h_layer_norm_quant_rows / p2h_layer_norm_rows makes them, the
+ * same bits. D <= 1024. */
+int p2h_layer_norm2_quant_rows(int M, int D, const float *dX, int ldx, const float *dGamma1, const float *dBeta1,
+                               float *dY, int ldy, const float *dGamma2, const float *dBeta2, signed char *dQ, int ldq,
+                               float *dScales, void *stream);
 int p2h_silu_quant_rows(int M, int K, const float *dH, int ldh, signed char *dQ, int ldq, float *dScales, void *stream);
 int p2h_concat_heads_quant_rows(int H, int T, int Dh, const float *dAttnH, signed char *dQ, int ldq, float *dScales,
                                 void *stream);

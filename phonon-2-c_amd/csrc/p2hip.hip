@@ -663,6 +663,38 @@ int p2h_layer_norm_quant_rows(int M, int D, const float *dX, int ldx, const floa
                    stream_of(stream));
 }
 
+int p2h_layer_norm2_quant_rows(int M, int D, const float *dX, int ldx, const float *dGamma1, const float *dBeta1,
+                               float *dY, int ldy, const float *dGamma2, const float *dBeta2, signed char *dQ, int ldq,
+                               float *dScales, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    const char *name = "p2h_layer_norm2_quant_rows";
+    if (M < 0 || D < 1 || D > 1024) return fail(P2H_E_ARG, "%s: %d rows of %d columns (columns 1..1024)", name, M, D);
+    if (M == 0) return P2H_OK;
+    if (!dX || !dY || !dGamma1 || !dBeta1 || !dGamma2 || !dBeta2 || !dQ || !dScales || ldx < D || ldy < D)
+        return fail(P2H_E_ARG, "%s: null pointer, or ldx = %d / ldy = %d < D = %d", name, ldx, ldy, D);
+    if (ldq < p2h_q_ld(D) || ldq % P2H_Q_KALIGN != 0 || ldq > 1024 || !aligned(dQ, 16))
+        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d, <= 1024 and a multiple of %d, Q 16-byte aligned", name,
+                    ldq, p2h_q_ld(D), P2H_Q_KALIGN);
+    p2k::ProdArgs a{};
+    a.M = M; a.K = D; a.X = dX; a.ldx = ldx; a.gamma = dGamma1; a.beta = dBeta1;
+    a.gamma2 = dGamma2; a.beta2 = dBeta2; a.Y1 = dY; a.ldy1 = ldy;
+    a.Q = (int8_t *)dQ; a.ldq = ldq; a.scales = dScales;
+    a.Mp = (int)align_up((size_t)M, 16);
+    const bool vec = D % 4 == 0 && ldx % 4 == 0 && aligned(dX, 16) && aligned(dGamma1, 16) && aligned(dBeta1, 16);
+    const dim3 grid((unsigned)((a.Mp + 3) / 4)), block(256);
+    hipStream_t s = stream_of(stream);
+    const bool regs = a.Mp <= 2048;   /* as p2h_layer_norm_quant_rows: the sums from registers when rows are few */
+    using p2k::produce_rows;
+    constexpr int LN = p2k::PROD_LN;
+    if (vec && regs) hipLaunchKernelGGL((produce_rows<LN, 1, true, 1, true, true>), grid, block, 0, s, a);
+    else if (vec) hipLaunchKernelGGL((produce_rows<LN, 1, true, 1, false, true>), grid, block, 0, s, a);
+    else if (regs) hipLaunchKernelGGL((produce_rows<LN, 1, false, 1, true, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((produce_rows<LN, 1, false, 1, false, true>), grid, block, 0, s, a);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
 int p2h_silu_quant_rows(int M, int K, const float *dH, int ldh, signed char *dQ, int ldq, float *dScales, void *stream)
 {
     if (int rc = ensure_init()) return rc;
@@ -1665,9 +1697,11 @@ int check_block(const P2hBlock *blk)
 }
 
 /* one block on x in place (encoder.c:617-625); dP: its positional projection [2T − 1][1024] when the caller made
- * it, else null (made here from dPE) */
+ * it, else null (made here from dPE). int8 modes, between the blocks of a stack: first_norm_done says that w.q /
+ * w.sc already hold the int8 rows of this block's first LayerNorm (made with the previous block's output norm);
+ * next, when set, has this block's output norm made together with next's first LayerNorm into w.q / w.sc. */
 int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const float *dP, float *dX, const BlockWs &w,
-              hipStream_t s)
+              hipStream_t s, bool first_norm_done = false, const P2hBlock *next = nullptr)
 {
     const int D = p2k::kD, FF = 4 * p2k::kD, L = 2 * T - 1, Dh = p2k::kDh, H = p2k::kH;
     const int ldD = p2h_q_ld(D), ldF = p2h_q_ld(FF);
@@ -1685,8 +1719,9 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     };
     static const bool silu_epilogue = env_int("P2H_SILU_EPILOGUE", 1) != 0;   /* 0: the SiLU→int8 producer instead */
     /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
-    auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2) {
-        P2H_TRY(layer_norm(g, b));
+    auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2,
+                            bool norm_done) {
+        if (!norm_done) P2H_TRY(layer_norm(g, b));
         if (mode != P2H_EXACT && silu_epilogue) {   /* SiLU in the up-projection's epilogue, then the plain quantiser */
             P2H_TRY(fvb_gemm_q8a(mode, T, FF, D, 1.0f, w.q, ldD, w.sc, l1, 0.0f, w.h, FF, w.gws, w.gws_bytes,
                                  nullptr, s, true));
@@ -1702,7 +1737,8 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         }
         return linear(l2, FF, D, 0.5f, 1.0f, nullptr, dX);
     };
-    P2H_TRY(feed_forward(blk->norm_ff1_w, blk->norm_ff1_b, blk->ff1_l1, blk->ff1_l2));
+    P2H_TRY(feed_forward(blk->norm_ff1_w, blk->norm_ff1_b, blk->ff1_l1, blk->ff1_l2,
+                         first_norm_done && mode != P2H_EXACT));
     /* self_attention (encoder.c:471-541) */
     P2H_TRY(layer_norm(blk->norm_sa_w, blk->norm_sa_b));
     P2H_TRY(linear(blk->qkv, D, 3 * D, 1.0f, 0.0f, w.ln, w.qkv));
@@ -1750,8 +1786,12 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         P2H_TRY(p2h_quant_rows(T, D, w.dw, D, w.q, ldD, w.sc, s));
         P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, nullptr, dX));
     }
-    P2H_TRY(feed_forward(blk->norm_ff2_w, blk->norm_ff2_b, blk->ff2_l1, blk->ff2_l2));
-    P2H_TRY(p2h_layer_norm_rows(T, D, dX, D, blk->norm_out_w, blk->norm_out_b, dX, D, s));
+    P2H_TRY(feed_forward(blk->norm_ff2_w, blk->norm_ff2_b, blk->ff2_l1, blk->ff2_l2, false));
+    if (next && mode != P2H_EXACT)   /* x = LayerNorm(x), and the next block's first LayerNorm of it as int8 rows */
+        P2H_TRY(p2h_layer_norm2_quant_rows(T, D, dX, D, blk->norm_out_w, blk->norm_out_b, dX, D, next->norm_ff1_w,
+                                           next->norm_ff1_b, w.q, ldD, w.sc, s));
+    else
+        P2H_TRY(p2h_layer_norm_rows(T, D, dX, D, blk->norm_out_w, blk->norm_out_b, dX, D, s));
 #undef P2H_TRY
     return P2H_OK;
 }
@@ -1844,10 +1884,14 @@ int p2h_conformer_stack(int mode, const P2hBlock *blocks, int n_blocks, int T, c
                 return rc;
         }
     }
-    for (int b = 0; b < n_blocks; b++)
+    /* int8 modes: each block's output norm and the next block's first norm in one kernel */
+    const bool pair_norms = mode != P2H_EXACT && env_int("P2H_STACK_NORM_PAIRS", 1) != 0;
+    for (int b = 0; b < n_blocks; b++) {
+        const P2hBlock *next = pair_norms && b + 1 < n_blocks ? &blocks[b + 1] : nullptr;
         if (int rc = run_block(mode, &blocks[b], T, dPE, mode != P2H_EXACT ? sw.P + (size_t)b * L * D : nullptr, dX,
-                               w, s))
+                               w, s, pair_norms && b > 0, next))
             return rc;
+    }
     return P2H_OK;
 }
 

@@ -195,6 +195,8 @@ struct ProdArgs {
     const float *gamma, *beta;                /* LN */
     int8_t *Q; int ldq; float *scales;
     float *Y; int ldy;                        /* when set: the made rows as fp32 [M][ldy] instead of quantised rows */
+    const float *gamma2, *beta2;              /* LN2: the second LayerNorm's factors; the first one's rows go out */
+    float *Y1; int ldy1;                      /* as fp32 [M][ldy1] (in place over X allowed) */
 };
 
 /* e^x as the reference's AVX2 exp (tensor_ops.c:154-175) in IEEE operations: clamp to ±87, k = rint(x·log2e),
@@ -259,7 +261,7 @@ __global__ void recip_check(uint32_t lo, uint32_t hi, unsigned long long *out)
  *                y = fmaf((x − mean)·inv_std, gamma, beta). The row is staged in LDS for the eight sums.
  * NCH chunks of 16 columns per lane (ldq <= 1024·WPR·NCH). LNR: LayerNorm's sums from registers (below). VEC: rows read as float4 — SILU / LN with K % 4 == 0,
  * ldx % 4 == 0 (LN: gamma and beta 16-byte aligned too); HEADS with Dh % 16 == 0; X 16-byte aligned. */
-template <int KIND, int NCH, bool VEC, int WPR = 1, bool LNR = false>
+template <int KIND, int NCH, bool VEC, int WPR = 1, bool LNR = false, bool LN2 = false>
 __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
 {
     static_assert(WPR == 1 || (WPR == 4 && KIND != PROD_LN), "LayerNorm keeps one wave per row");
@@ -278,6 +280,25 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
         return;
     }
     float x[NCH][16];
+    /* the made row as fp32: 16-byte stores of the lane's 16 columns where the row is aligned and the chunk whole
+     * (each store instruction then writes whole 128-byte lines), else one value at a time */
+    auto store_row = [&](float *yr, const float (&v)[NCH][16]) __attribute__((always_inline)) {
+        const bool al = (reinterpret_cast<uintptr_t>(yr) & 15) == 0;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int k0 = 16 * (lr + STRIDE * c);
+            if (al && k0 + 16 <= K) {
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    *reinterpret_cast<v4f *>(yr + k0 + 4 * u) = v4f{v[c][4 * u], v[c][4 * u + 1], v[c][4 * u + 2],
+                                                                    v[c][4 * u + 3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (k0 + e < K) yr[k0 + e] = v[c][e];
+            }
+        }
+    };
     /* LN: gamma and beta for the lane's columns, requested before the row's statistics need the wave for a while */
     constexpr int GB = KIND == PROD_LN && NCH <= 2 ? NCH : 1;
     float gam[GB][16], bet[GB][16];
@@ -326,112 +347,130 @@ __global__ __launch_bounds__(256) void produce_rows(ProdArgs a)
         }
     }
     if (KIND == PROD_LN) {
-        /* The row in LDS by chain: element k at rt[(k % 8)·S + k / 8], so chain j's elements are contiguous and read
-         * as float4; S = 128·NCH + 20 leaves each chain 16 elements of padding past its 128·NCH (a prefetch of one
-         * batch past the end stays inside the chain's row) and puts the eight chains in different banks. Lane L's
-         * element e of chunk c is k = 16·(L + 64c) + e: x[e] and x[e + 8] are neighbours in chain e. Zeros beyond
-         * K. */
-        constexpr int S = 128 * NCH + 20;
-        float *rt = stage + w * 8 * S;
+        /* LN2, two passes: LayerNorm(x), out as fp32 rows, then LayerNorm of those rows with gamma2 / beta2 (the
+         * block's output norm followed by the next block's first norm, encoder.c:623 then 342) */
 #pragma unroll
-        for (int c = 0; c < NCH; c++)
+        for (int pass = 0; pass < (LN2 ? 2 : 1); pass++) {
+            const float *gptr = pass ? a.gamma2 : a.gamma, *bptr = pass ? a.beta2 : a.beta;
+            if (LN2 && pass == 1) {
+                store_row(a.Y1 + (size_t)m * a.ldy1, x);
+                if (NCH <= 2) {
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                *reinterpret_cast<float2 *>(rt + e * S + 2 * (lane + 64 * c)) = make_float2(x[c][e], x[c][e + 8]);
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const int body = K / 8 * 8, n8 = body / 8, nb = n8 / 16;
-        /* chain j = lane (j < 8): rt[j·S + 0 .. n8 − 1] in order, in batches of 16, the next batch's LDS reads in
-         * flight while the current one is added */
-        auto chain = [&](auto add) {
-            float p = 0.0f;
-            if (lane < 8) {
-                const float *cj = rt + lane * S;
-                auto add16 = [&](float p, const float4 (&v)[4]) {
+                    for (int c = 0; c < GB; c++) {
+                        const int k0 = 16 * (lane + 64 * c);
 #pragma unroll
-                    for (int u = 0; u < 4; u++) p = add(add(add(add(p, v[u].x), v[u].y), v[u].z), v[u].w);
-                    return p;
-                };
-                float4 va[4], vb[4];
-#pragma unroll
-                for (int u = 0; u < 4; u++) va[u] = *reinterpret_cast<const float4 *>(cj + 4 * u);
-                int b = 0;
-                for (; b + 2 <= nb; b += 2) {   /* loads are unconditional: batch nb lies in the row's padding */
-#pragma unroll
-                    for (int u = 0; u < 4; u++) vb[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 1) + 4 * u);
-                    __builtin_amdgcn_sched_barrier(0);   /* the next batch's reads stay ahead of these additions */
-                    p = add16(p, va);
-#pragma unroll
-                    for (int u = 0; u < 4; u++) va[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 2) + 4 * u);
-                    __builtin_amdgcn_sched_barrier(0);
-                    p = add16(p, vb);
+                        for (int e = 0; e < 16; e++) {
+                            gam[c][e] = k0 + e < K ? a.gamma2[k0 + e] : 0.0f;
+                            bet[c][e] = k0 + e < K ? a.beta2[k0 + e] : 0.0f;
+                        }
+                    }
                 }
-                if (b < nb) p = add16(p, va);
-                for (int i = 16 * nb; i < n8; i++) p = add(p, cj[i]);
+                __builtin_amdgcn_wave_barrier();   /* the first pass's reads of the staged row are done */
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             }
-            /* p2_hsum_avx2: lanes i and i + 4, then pairs */
-            float v8[8];
+            /* The row in LDS by chain: element k at rt[(k % 8)·S + k / 8], so chain j's elements are contiguous and
+             * read as float4; S = 128·NCH + 20 leaves each chain 16 elements of padding past its 128·NCH (a prefetch
+             * of one batch past the end stays inside the chain's row) and puts the eight chains in different banks.
+             * Lane L's element e of chunk c is k = 16·(L + 64c) + e: x[e] and x[e + 8] are neighbours in chain e.
+             * Zeros beyond K. */
+            constexpr int S = 128 * NCH + 20;
+            float *rt = stage + w * 8 * S;
 #pragma unroll
-            for (int j = 0; j < 8; j++) v8[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
-            return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
-                             __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
-        };
-        /* LNR (NCH = 1, K = 1024 .. 1031: every LayerNorm of the encoder, chosen when the rows are few): each chain's
-         * 128 elements read into registers once, for both sums, with one wait; the chains then run without LDS round
-         * trips between batches. 4.5 against 5.3 us at 375 rows; at 6000 rows its 237 VGPRs cost occupancy (13.0
-         * against 11.3 us), so many rows take the LDS batches. */
-        float4 cv[LNR ? 32 : 1];
-        const bool whole = LNR && n8 == 128;
-        if (LNR && whole) {   /* lanes 8.. read chain lane % 8 again (broadcast reads), their sums unused */
+            for (int c = 0; c < NCH; c++)
 #pragma unroll
-            for (int u = 0; u < (LNR ? 32 : 1); u++)
-                cv[u] = *reinterpret_cast<const float4 *>(rt + (lane & 7) * S + 4 * u);
-        }
-        auto chain_regs = [&](auto add) {
-            float p = 0.0f;
+                for (int e = 0; e < 8; e++)
+                    *reinterpret_cast<float2 *>(rt + e * S + 2 * (lane + 64 * c)) = make_float2(x[c][e], x[c][e + 8]);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const int body = K / 8 * 8, n8 = body / 8, nb = n8 / 16;
+            /* chain j = lane (j < 8): rt[j·S + 0 .. n8 − 1] in order, in batches of 16, the next batch's LDS reads in
+             * flight while the current one is added */
+            auto chain = [&](auto add) {
+                float p = 0.0f;
+                if (lane < 8) {
+                    const float *cj = rt + lane * S;
+                    auto add16 = [&](float p, const float4 (&v)[4]) {
 #pragma unroll
-            for (int u = 0; u < (LNR ? 32 : 1); u++) p = add(add(add(add(p, cv[u].x), cv[u].y), cv[u].z), cv[u].w);
-            float v8[8];
+                        for (int u = 0; u < 4; u++) p = add(add(add(add(p, v[u].x), v[u].y), v[u].z), v[u].w);
+                        return p;
+                    };
+                    float4 va[4], vb[4];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v8[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
-            return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
-                             __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
-        };
-        auto add_sum = [](float p, float v) { return __fadd_rn(p, v); };
-        auto at = [&](int k) { return rt[(k & 7) * S + (k >> 3)]; };
-        float sum = whole ? chain_regs(add_sum) : chain(add_sum);
-        for (int k = body; k < K; k++) sum = __fadd_rn(sum, at(k));
-        const float mean = __fdiv_rn(sum, (float)K);
-        auto add_sq = [mean](float p, float v) {
-            const float d = __fsub_rn(v, mean);
-            return __builtin_fmaf(d, d, p);
-        };
-        float var_sum = whole ? chain_regs(add_sq) : chain(add_sq);
-        for (int k = body; k < K; k++) {
-            const float d = __fsub_rn(at(k), mean);
-            var_sum = __builtin_fmaf(d, d, var_sum);
-        }
-        const float inv_std = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(var_sum, (float)K), 1e-5f)));
+                    for (int u = 0; u < 4; u++) va[u] = *reinterpret_cast<const float4 *>(cj + 4 * u);
+                    int b = 0;
+                    for (; b + 2 <= nb; b += 2) {   /* loads are unconditional: batch nb lies in the row's padding */
 #pragma unroll
-        for (int c = 0; c < NCH; c++)
+                        for (int u = 0; u < 4; u++)
+                            vb[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 1) + 4 * u);
+                        __builtin_amdgcn_sched_barrier(0);   /* the next batch's reads stay ahead of these additions */
+                        p = add16(p, va);
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int k = min(16 * (lane + 64 * c) + e, K - 1);
-                const float g = NCH <= 2 ? gam[NCH <= 2 ? c : 0][e] : a.gamma[k];
-                const float b = NCH <= 2 ? bet[NCH <= 2 ? c : 0][e] : a.beta[k];
-                const float y = __builtin_fmaf(__fmul_rn(__fsub_rn(x[c][e], mean), inv_std), g, b);
-                x[c][e] = (16 * (lane + 64 * c) + e < K) ? y : 0.0f;
+                        for (int u = 0; u < 4; u++)
+                            va[u] = *reinterpret_cast<const float4 *>(cj + 16 * (b + 2) + 4 * u);
+                        __builtin_amdgcn_sched_barrier(0);
+                        p = add16(p, vb);
+                    }
+                    if (b < nb) p = add16(p, va);
+                    for (int i = 16 * nb; i < n8; i++) p = add(p, cj[i]);
+                }
+                /* p2_hsum_avx2: lanes i and i + 4, then pairs */
+                float v8[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v8[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+                return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
+                                 __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+            };
+            /* LNR (NCH = 1, K = 1024 .. 1031: every LayerNorm of the encoder, chosen when the rows are few): each
+             * chain's 128 elements read into registers once, for both sums, with one wait; the chains then run
+             * without LDS round trips between batches. 4.5 against 5.3 us at 375 rows; at 6000 rows its 237 VGPRs
+             * cost occupancy (13.0 against 11.3 us), so many rows take the LDS batches. */
+            float4 cv[LNR ? 32 : 1];
+            const bool whole = LNR && n8 == 128;
+            if (LNR && whole) {   /* lanes 8.. read chain lane % 8 again (broadcast reads), their sums unused */
+#pragma unroll
+                for (int u = 0; u < (LNR ? 32 : 1); u++)
+                    cv[u] = *reinterpret_cast<const float4 *>(rt + (lane & 7) * S + 4 * u);
             }
+            auto chain_regs = [&](auto add) {
+                float p = 0.0f;
+#pragma unroll
+                for (int u = 0; u < (LNR ? 32 : 1); u++) p = add(add(add(add(p, cv[u].x), cv[u].y), cv[u].z), cv[u].w);
+                float v8[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v8[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+                return __fadd_rn(__fadd_rn(__fadd_rn(v8[0], v8[4]), __fadd_rn(v8[2], v8[6])),
+                                 __fadd_rn(__fadd_rn(v8[1], v8[5]), __fadd_rn(v8[3], v8[7])));
+            };
+            auto add_sum = [](float p, float v) { return __fadd_rn(p, v); };
+            auto at = [&](int k) { return rt[(k & 7) * S + (k >> 3)]; };
+            float sum = whole ? chain_regs(add_sum) : chain(add_sum);
+            for (int k = body; k < K; k++) sum = __fadd_rn(sum, at(k));
+            const float mean = __fdiv_rn(sum, (float)K);
+            auto add_sq = [mean](float p, float v) {
+                const float d = __fsub_rn(v, mean);
+                return __builtin_fmaf(d, d, p);
+            };
+            float var_sum = whole ? chain_regs(add_sq) : chain(add_sq);
+            for (int k = body; k < K; k++) {
+                const float d = __fsub_rn(at(k), mean);
+                var_sum = __builtin_fmaf(d, d, var_sum);
+            }
+            const float inv_std = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(var_sum, (float)K), 1e-5f)));
+#pragma unroll
+            for (int c = 0; c < NCH; c++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int k = min(16 * (lane + 64 * c) + e, K - 1);
+                    const float g = NCH <= 2 ? gam[NCH <= 2 ? c : 0][e] : gptr[k];
+                    const float b = NCH <= 2 ? bet[NCH <= 2 ? c : 0][e] : bptr[k];
+                    const float y = __builtin_fmaf(__fmul_rn(__fsub_rn(x[c][e], mean), inv_std), g, b);
+                    x[c][e] = (16 * (lane + 64 * c) + e < K) ? y : 0.0f;
+                }
+    
+        }
     }
     if (a.Y) {   /* fp32 rows (the exact route's LayerNorm, SiLU, head concatenation and transpose) */
-        float *yr = a.Y + (size_t)m * a.ldy;
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
-            const int k0 = 16 * (lr + STRIDE * c);
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                if (k0 + e < K) yr[k0 + e] = x[c][e];
-        }
+        store_row(a.Y + (size_t)m * a.ldy, x);
         return;
     }
     float amax = 0.0f;

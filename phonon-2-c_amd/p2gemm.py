@@ -66,6 +66,7 @@ _HIP_SIG = {
     "p2h_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_q_ld": (_i, [_i]),
     "p2h_layer_norm_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    "p2h_layer_norm2_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp]),
     "p2h_recip_selftest": (_i, [C.POINTER(C.c_ulonglong)]),
     "p2h_silu_quant_rows": (_i, [_i, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "p2h_concat_heads_quant_rows": (_i, [_i, _i, _i, _vp, _vp, _i, _vp, _vp]),
@@ -689,6 +690,19 @@ def add_residual(X, Y, alpha):
     dX, dY = to_device(X), to_device(_f32(Y))
     _ok(hip().p2h_add_residual(X.shape[0], dX.ptr, dY.ptr, alpha, None), "p2h_add_residual")
     return dX.download(X.shape, np.float32)
+
+
+def layer_norm2_quant_rows(X, gamma1, beta1, gamma2, beta2, in_place=False):
+    """p2h_layer_norm2_quant_rows on host arrays X [M, D]: (Y = LayerNorm(X; gamma1, beta1) as fp32 [M, D],
+    q untiled [roundup(M, 16), ldq], scales [M]) of LayerNorm(Y; gamma2, beta2)."""
+    X = _f32(X)
+    M, D = X.shape
+    dX = to_device(X)
+    dY = dX if in_place else DeviceBuffer(X.nbytes)
+    g1, b1, g2, b2 = (to_device(_f32(v)) for v in (gamma1, beta1, gamma2, beta2))
+    q, s = _produced(M, D, lambda dQ, ldq, dS: _ok(hip().p2h_layer_norm2_quant_rows(
+        M, D, dX.ptr, D, g1.ptr, b1.ptr, dY.ptr, D, g2.ptr, b2.ptr, dQ, ldq, dS, None), "p2h_layer_norm2_quant_rows"))
+    return dY.download(X.shape, np.float32), q, s
 
 
 def layer_norm_rows(X, gamma, beta, in_place=False):

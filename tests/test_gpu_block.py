@@ -144,6 +144,25 @@ def test_attention_rows(T):
     assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
 
 
+@pytest.mark.parametrize("M", [375, 3000, 1])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_layer_norm2_quant_rows(M, in_place):
+    """Two LayerNorms in one kernel equal p2h_layer_norm_rows followed by p2h_layer_norm_quant_rows, bit for bit:
+    the fp32 rows of the first and the codes and scales of the second (375 rows: sums from registers; 3000: from
+    LDS batches)."""
+    print(f"layer_norm2_quant_rows M={M} in_place={in_place}", flush=True)
+    rng = np.random.default_rng(SEED + 31 * M)
+    x = (rng.standard_normal((M, D)) * 3 + 0.5).astype(np.float32)
+    g1, g2 = (rng.uniform(0.5, 1.5, D).astype(np.float32) for _ in range(2))
+    b1, b2 = ((rng.uniform(-0.2, 0.2, D)).astype(np.float32) for _ in range(2))
+    y, q, s = P.layer_norm2_quant_rows(x, g1, b1, g2, b2, in_place=in_place)
+    y_ref = P.layer_norm_rows(x, g1, b1)
+    q_ref, s_ref = P.layer_norm_quant_rows(y_ref, g2, b2)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+    assert np.array_equal(q, q_ref)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [375, 7])
 def test_glu_channel_major(T):
     print(f"glu T={T}", flush=True)
