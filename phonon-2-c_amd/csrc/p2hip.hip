@@ -1339,8 +1339,10 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
 }
 
 /* The exact five-value route on the fp32 matrix cores (gemm_xf): 32 × 64 tiles, or 32 × 32 where 32 × 64 would leave
- * fewer than two workgroups per CU. P2H_EXACT_CHAIN=1 selects gemm_exact instead, the reference's per-output fmaf
- * chain bit for bit; P2H_XF_TILE = 32 or 64 forces the tile width. */
+ * fewer than two workgroups per CU; rows staged through LDS by direct loads where K % 128 == 0 and the rows allow
+ * 16-byte loads (the same bits as the register path, which P2H_XF_STAGED=0 selects). P2H_EXACT_CHAIN=1 selects
+ * gemm_exact instead, the reference's per-output fmaf chain bit for bit; P2H_XF_TILE = 32 or 64 forces the tile
+ * width. */
 }  // extern "C"
 
 namespace {
@@ -1350,7 +1352,9 @@ void launch_xf_tile(const p2k::ExactArgs &g, hipStream_t s)
 {
     const dim3 grid((unsigned)((size_t)g.tiles_n * ((g.M + 31) / 32))), block(256);
     const bool vec = g.K % 4 == 0 && g.lda % 4 == 0 && aligned(g.A, 16);
-    if (vec) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true>), grid, block, 0, s, g);
+    const bool staged = vec && g.K % 128 == 0 && env_int("P2H_XF_STAGED", 1) != 0;
+    if (staged) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true, true>), grid, block, 0, s, g);
+    else if (vec) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true>), grid, block, 0, s, g);
     else hipLaunchKernelGGL((p2k::gemm_xf<2, FN, false>), grid, block, 0, s, g);
 }
 

@@ -424,6 +424,36 @@ def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
     assert _bits_equal(got4, (got * np.float32(4.0)).astype(np.float32))
 
 
+@pytest.mark.parametrize("M,K,N,lda,ldc,tile", [
+    (375, 1024, 4096, 1024, 4096, 0), (375, 4096, 1024, 4096, 1024, 0), (375, 1024, 1024, 1028, 1030, 0),
+    (749, 1024, 1024, 1024, 1024, 64), (37, 256, 64, 260, 64, 32), (1, 128, 48, 128, 50, 0), (130, 384, 208, 388, 211, 64)])
+def test_exact_staged_rows_match_register_path(monkeypatch, M, K, N, lda, ldc, tile):
+    """gemm_xf's two ways of bringing the fp32 rows to the matrix cores (staged through LDS by direct loads where
+    K % 128 == 0 and the rows allow 16-byte loads; into registers otherwise, P2H_XF_STAGED=0) run the same MFMAs in
+    the same order: the outputs are equal bit for bit, with beta = 0, 1 and 0.3, strided A and C, a last row tile cut
+    short, and both tile widths; and within 1e-4 of the oracle's exact route."""
+    print(f"exact staged M={M} K={K} N={N} lda={lda} ldc={ldc} tile={tile}", flush=True)
+    signs, flags, lo, hi = _weight(K, N, 930 + K + N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = np.full((M, lda), np.nan, np.float32)   # columns past K are never read
+    A[:, :K] = P.gen_activations(SEED, 950 + M, M, K)
+    if tile:
+        monkeypatch.setenv("P2H_XF_TILE", str(tile))
+    C0 = np.random.default_rng(M + N).standard_normal((M, ldc)).astype(np.float32)
+    for alpha, beta in [(1.0, 0.0), (0.5, 1.0), (-1.5, 0.3)]:
+        got = P.fvb_gemm("exact", A, w, alpha=alpha, beta=beta, C0=C0)
+        monkeypatch.setenv("P2H_XF_STAGED", "0")
+        try:
+            reg = P.fvb_gemm("exact", A, w, alpha=alpha, beta=beta, C0=C0)
+        finally:
+            monkeypatch.delenv("P2H_XF_STAGED")
+        assert _bits_equal(got, reg), f"alpha={alpha} beta={beta}: staged and register paths differ"
+        assert _bits_equal(got[:, N:], C0[:, N:])
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(K).choice(M, min(M, 24), replace=False)]))
+    ref = O.sgemm_fvb("exact", A[rows, :K], signs, flags, lo, hi, N, alpha=-1.5, beta=0.3, C0=C0[rows, :N])
+    _assert_exact(got[rows, :N], ref)
+
+
 # ── every tile configuration and K split (the planner's choices forced through its tuning variables) ─────────────
 
 _TILE_CASES = {}
