@@ -1722,6 +1722,12 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         return p2h_layer_norm_quant_rows(T, D, dX, D, g, b, w.q, ldD, w.sc, s);
     };
     static const bool silu_epilogue = env_int("P2H_SILU_EPILOGUE", 1) != 0;   /* 0: the SiLU→int8 producer instead */
+    /* Exact mode's residuals (add_residual, encoder.c:252-275: x = fmaf(y, α, x) over y = the linear's output) in the
+     * matrix-core GEMM's epilogue: fmaf(α, sum, x) with β = 1 is the same value, y being the sum itself (α = 1,
+     * β = 0: fmaf(1, sum, 0)); only a −0 sum onto a −0 x would differ. The fmaf-chain route (P2H_EXACT_CHAIN=1)
+     * keeps the separate pass, as the reference computes it; so does P2H_EXACT_RESIDUAL_EPILOGUE=0. */
+    const bool res_epilogue = mode == P2H_EXACT && env_int("P2H_EXACT_CHAIN", 0) == 0 &&
+                              env_int("P2H_EXACT_RESIDUAL_EPILOGUE", 1) != 0;
     /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
     auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2,
                             bool norm_done) {
@@ -1736,6 +1742,7 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         }
         if (mode == P2H_EXACT) {
             P2H_TRY(p2h_silu((size_t)T * FF, w.h, s));
+            if (res_epilogue) return linear(l2, FF, D, 0.5f, 1.0f, w.h, dX);
             P2H_TRY(linear(l2, FF, D, 1.0f, 0.0f, w.h, w.out));
             return p2h_add_residual(T, dX, w.out, 0.5f, s);
         }
@@ -1771,8 +1778,12 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     /* w.attn_h: the heads' rows [T][1024] from the fused kernel, else [H][T][Dh] for the concatenation */
     if (mode == P2H_EXACT) {
         if (!fused) P2H_TRY(p2h_concat_heads_rows(T, w.attn_h, w.attn, s));
-        P2H_TRY(linear(blk->out, D, D, 1.0f, 0.0f, fused ? w.attn_h : w.attn, w.out));
-        P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
+        if (res_epilogue) {
+            P2H_TRY(linear(blk->out, D, D, 1.0f, 1.0f, fused ? w.attn_h : w.attn, dX));
+        } else {
+            P2H_TRY(linear(blk->out, D, D, 1.0f, 0.0f, fused ? w.attn_h : w.attn, w.out));
+            P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
+        }
     } else {
         if (fused) P2H_TRY(p2h_quant_rows(T, D, w.attn_h, D, w.q, ldD, w.sc, s));
         else P2H_TRY(p2h_concat_heads_quant_rows(H, T, Dh, w.attn_h, w.q, ldD, w.sc, s));
@@ -1784,8 +1795,12 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     /* the convolution's output as rows [T][1024] (channel_major_to_rows' transpose made by the kernel's stores) */
     P2H_TRY(p2h_glu_depthwise_conv_silu_rows(T, w.h, blk->dw_w, blk->dw_b, w.dw, s));
     if (mode == P2H_EXACT) {
-        P2H_TRY(linear(blk->pw2, D, D, 1.0f, 0.0f, w.dw, w.out));
-        P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
+        if (res_epilogue) {
+            P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, w.dw, dX));
+        } else {
+            P2H_TRY(linear(blk->pw2, D, D, 1.0f, 0.0f, w.dw, w.out));
+            P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
+        }
     } else {
         P2H_TRY(p2h_quant_rows(T, D, w.dw, D, w.q, ldD, w.sc, s));
         P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, nullptr, dX));

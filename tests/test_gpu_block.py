@@ -330,6 +330,23 @@ def test_block_step_against_reference(mode, stage, tmp_path):
     assert np.median(rel) <= 1e-4 and rel.max() <= 1e-2
 
 
+@pytest.mark.parametrize("T", [375, 520])
+def test_exact_residual_epilogue_same_bits(monkeypatch, T):
+    """Exact mode adds its three residuals (x = fmaf(y, α, x) over the linear's output y) in the matrix-core GEMM's
+    epilogue, fmaf(α, sum, x) with β = 1; the block equals the one with the separate residual pass
+    (P2H_EXACT_RESIDUAL_EPILOGUE=0) bit for bit."""
+    print(f"exact residual epilogue T={T}", flush=True)
+    sys.path.insert(0, HERE)
+    import refblock_child as RC
+    x, pe = RC.block_input(SEED, T)
+    blk = _device_block(SEED)
+    fused = blk.run("exact", x, pe)
+    monkeypatch.setenv("P2H_EXACT_RESIDUAL_EPILOGUE", "0")
+    separate = blk.run("exact", x, pe)
+    assert np.isfinite(fused).all()
+    assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
+
+
 @pytest.mark.parametrize("mode", ["int8w", "int8", "exact"])
 def test_stack_equals_blocks_one_by_one(mode):
     """p2h_conformer_stack over three distinct blocks equals p2h_conformer_block called block after block, bit for
