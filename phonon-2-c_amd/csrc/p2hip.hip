@@ -1399,6 +1399,30 @@ static int quant_into_workspace(const char *who, int mode, int M, int N, int K, 
     return p2h_quant_rows(M, K, dA, lda, *dQ, p2h_q_ld(K), *dS, s);
 }
 
+/* The exact route after p2h_fvb_gemm's checks (M > 0). silu: the block's feed-forward up-projection, h =
+ * p2_swish(A·W) (encoder.c:353-354) with the SiLU in the matrix-core GEMM's epilogue; beta 0, ldc = N and N % 8 == 0,
+ * where p2_swish's eight-wide body (silu_p2) covers every element, so the bits are those of the GEMM followed by
+ * p2h_silu. The fmaf-chain route keeps the separate pass. */
+static int exact_gemm(int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w, float beta,
+                      float *dC, int ldc, hipStream_t s, bool silu)
+{
+    if (silu && (beta != 0.0f || ldc != N || N % 8 != 0))
+        return fail(P2H_E_ARG, "exact GEMM with SiLU: needs beta 0, ldc = N and N %% 8 == 0");
+    p2k::ExactArgs g;
+    memset(&g, 0, sizeof g);
+    g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
+    g.A = dA; g.lda = lda;
+    g.signs = w->signs; g.flags = w->flags; g.lo = w->lo; g.hi = w->hi;
+    g.C = dC; g.ldc = ldc;
+    g.rec = w->rec4; g.units = w->units;
+    if (env_int("P2H_EXACT_CHAIN", 0) != 0 || K == 0) {
+        if (int rc = launch_exact(p2k::EXB_FV, g, s)) return rc;
+        return silu ? p2h_silu((size_t)M * N, dC, s) : P2H_OK;
+    }
+    g.act = silu ? 1 : 0;
+    return launch_xf(g, s);
+}
+
 int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const P2hWeight *w,
                  float beta, float *dC, int ldc, void *workspace, size_t workspace_bytes, void *stream)
 {
@@ -1427,15 +1451,7 @@ int p2h_fvb_gemm(int mode, int M, int N, int K, float alpha, const float *dA, in
         return p2h_fvb_gemm_q8a(mode, M, N, K, alpha, dQ, p2h_q_ld(K), dS, w, beta, dC, ldc, workspace,
                                 (size_t)((char *)dQ - (char *)workspace), s);
     }
-    p2k::ExactArgs g;
-    memset(&g, 0, sizeof g);
-    g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
-    g.A = dA; g.lda = lda;
-    g.signs = w->signs; g.flags = w->flags; g.lo = w->lo; g.hi = w->hi;
-    g.C = dC; g.ldc = ldc;
-    g.rec = w->rec4; g.units = w->units;
-    if (env_int("P2H_EXACT_CHAIN", 0) != 0 || K == 0) return launch_exact(p2k::EXB_FV, g, s);
-    return launch_xf(g, s);
+    return exact_gemm(M, N, K, alpha, dA, lda, w, beta, dC, ldc, s, false);
 }
 
 size_t p2h_noalloc_scratch_bytes(void) { return kScratchBytes; }
@@ -1724,10 +1740,11 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     static const bool silu_epilogue = env_int("P2H_SILU_EPILOGUE", 1) != 0;   /* 0: the SiLU→int8 producer instead */
     /* Exact mode's residuals (add_residual, encoder.c:252-275: x = fmaf(y, α, x) over y = the linear's output) in the
      * matrix-core GEMM's epilogue: fmaf(α, sum, x) with β = 1 is the same value, y being the sum itself (α = 1,
-     * β = 0: fmaf(1, sum, 0)); only a −0 sum onto a −0 x would differ. The fmaf-chain route (P2H_EXACT_CHAIN=1)
-     * keeps the separate pass, as the reference computes it; so does P2H_EXACT_RESIDUAL_EPILOGUE=0. */
+     * β = 0: fmaf(1, sum, 0)); only a −0 sum onto a −0 x would differ. The feed-forward's SiLU there too (see
+     * exact_gemm). The fmaf-chain route (P2H_EXACT_CHAIN=1) keeps the separate passes, as the reference computes
+     * them; so does P2H_EXACT_EPILOGUE=0. */
     const bool res_epilogue = mode == P2H_EXACT && env_int("P2H_EXACT_CHAIN", 0) == 0 &&
-                              env_int("P2H_EXACT_RESIDUAL_EPILOGUE", 1) != 0;
+                              env_int("P2H_EXACT_EPILOGUE", 1) != 0;
     /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
     auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2,
                             bool norm_done) {
@@ -1736,12 +1753,14 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
             P2H_TRY(fvb_gemm_q8a(mode, T, FF, D, 1.0f, w.q, ldD, w.sc, l1, 0.0f, w.h, FF, w.gws, w.gws_bytes,
                                  nullptr, s, true));
             P2H_TRY(p2h_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
+        } else if (res_epilogue) {
+            P2H_TRY(exact_gemm(T, FF, D, 1.0f, w.ln, D, l1, 0.0f, w.h, FF, s, true));
         } else {
             P2H_TRY(linear(l1, D, FF, 1.0f, 0.0f, w.ln, w.h));
             if (mode != P2H_EXACT) P2H_TRY(p2h_silu_quant_rows(T, FF, w.h, FF, w.q, ldF, w.sc, s));
+            else P2H_TRY(p2h_silu((size_t)T * FF, w.h, s));
         }
         if (mode == P2H_EXACT) {
-            P2H_TRY(p2h_silu((size_t)T * FF, w.h, s));
             if (res_epilogue) return linear(l2, FF, D, 0.5f, 1.0f, w.h, dX);
             P2H_TRY(linear(l2, FF, D, 1.0f, 0.0f, w.h, w.out));
             return p2h_add_residual(T, dX, w.out, 0.5f, s);

@@ -2294,6 +2294,8 @@ struct ExactArgs {
     float *C; int ldc;
     int tiles_n;
     const uint8_t *rec; int units;                        /* 4-bit selector records (fv_repack4) for gemm_xf */
+    int act;                                              /* gemm_xf: 1 stores silu_p2 of each output (beta 0,
+                                                             ldc = N, N % 8 == 0: p2_swish's eight-wide body) */
 };
 
 constexpr int EBM = 64, EBN = 64, EBK = 32;
@@ -2625,6 +2627,10 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
             v4f r;
 #pragma unroll
             for (int e = 0; e < 4; e++) r[e] = __builtin_fmaf(g.alpha, sum[e], c0[e]);
+            if (g.act) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) r[e] = silu_p2(r[e]);
+            }
             *reinterpret_cast<v4f *>(cp) = r;
             continue;
         }
@@ -2632,7 +2638,8 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
         for (int e = 0; e < 4; e++) {
             if (n + e >= N) break;
             const float c0 = g.beta == 0.0f ? 0.0f : (g.beta == 1.0f ? cp[e] : cp[e] * g.beta);
-            cp[e] = __builtin_fmaf(g.alpha, sum[e], c0);
+            const float r = __builtin_fmaf(g.alpha, sum[e], c0);
+            cp[e] = g.act ? silu_p2(r) : r;
         }
     }
 }

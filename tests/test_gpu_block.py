@@ -331,17 +331,17 @@ def test_block_step_against_reference(mode, stage, tmp_path):
 
 
 @pytest.mark.parametrize("T", [375, 520])
-def test_exact_residual_epilogue_same_bits(monkeypatch, T):
+def test_exact_epilogues_same_bits(monkeypatch, T):
     """Exact mode adds its three residuals (x = fmaf(y, α, x) over the linear's output y) in the matrix-core GEMM's
-    epilogue, fmaf(α, sum, x) with β = 1; the block equals the one with the separate residual pass
-    (P2H_EXACT_RESIDUAL_EPILOGUE=0) bit for bit."""
+    epilogue, fmaf(α, sum, x) with β = 1, and applies the feed-forward's SiLU there; the block equals the one with
+    the separate passes (P2H_EXACT_EPILOGUE=0) bit for bit."""
     print(f"exact residual epilogue T={T}", flush=True)
     sys.path.insert(0, HERE)
     import refblock_child as RC
     x, pe = RC.block_input(SEED, T)
     blk = _device_block(SEED)
     fused = blk.run("exact", x, pe)
-    monkeypatch.setenv("P2H_EXACT_RESIDUAL_EPILOGUE", "0")
+    monkeypatch.setenv("P2H_EXACT_EPILOGUE", "0")
     separate = blk.run("exact", x, pe)
     assert np.isfinite(fused).all()
     assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
