@@ -2438,30 +2438,31 @@ __global__ __launch_bounds__(256) void gemm_exact(ExactArgs g)
  * multiplies; lane l of the step t MFMA takes k = 16·(l / 16) + t of a 64-row step, which is the record's own order.
  * The four partial tiles meet in LDS and are added in wave order.
  * The fp32 rows reach the lanes in one of two ways, with the same MFMAs in the same order (the same bits):
- *   STAGED (K % 128 == 0 and VEC): each wave brings its 64-row K stages of the BM rows into its own two LDS slots by
+ *   STAGED (K % 128 == 0 and VEC): each wave brings its 64-row K stages of the BM rows into its own LDS slot by
  *     direct loads of whole 256-byte row segments (four rows per instruction, 16-byte chunk c of row r stored at
- *     place c ^ (r % 16), so the operand reads below are free of bank conflicts), the next stage in flight while the
- *     current one is multiplied; no barrier, each wave reads only its own slots. 43.3 → 35.9 us at M = 375,
- *     1024 → 4096 (16.5 → 13.7 us at 1024 → 1024): loads straight into the matrix-core layout touch 16 rows × 64
- *     bytes per instruction, and the lines per instruction, not the bytes, set their pace.
+ *     place c ^ (r % 16), so the operand reads below are free of bank conflicts); no barrier, each wave reads only its
+ *     own slot. 43.3 → 31.5 us at M = 375, 1024 → 4096 (16.5 → 12.9 us at 1024 → 1024, 51.9 → 44.1 us at
+ *     4096 → 1024): loads straight into the matrix-core layout touch 16 rows × 64 bytes per instruction, and the
+ *     lines per instruction, not the bytes, set their pace.
  *   else: loads into registers in the matrix-core layout, units double-buffered.
  * VEC: K % 4 == 0, lda % 4 == 0 and A 16-byte aligned. */
 template <int FM, int FN, bool VEC, bool STAGED = false>
 __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
 {
     static_assert(!STAGED || VEC, "the staged rows are read as 16-byte chunks");
+    constexpr int NW = 4, NT = 64 * NW;
     constexpr int BM = 16 * FM, BN = 16 * FN, PITCH = BN + 4, TILE = BM * PITCH;
     constexpr int ABUF = BM * 256;                    /* STAGED: one 64-row K stage of one wave, BM rows × 256 bytes */
     constexpr int NQ = BM / 4;                        /* STAGED: direct loads per stage, four rows each */
-    constexpr int SMEM = (STAGED && 8 * ABUF > 16 * TILE) ? 8 * ABUF : 16 * TILE;   /* bytes; partial tiles reuse it */
-    __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
+    constexpr int SMEM = (STAGED && NW * ABUF > 4 * NW * TILE) ? NW * ABUF : 4 * NW * TILE;   /* bytes */
+    __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];   /* the partial tiles reuse the staging slots */
     float *part = reinterpret_cast<float *>(smem);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
     const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
     const int n0 = tile_n * BN, m0 = tile_m * BM;
     const int M = g.M, N = g.N, K = g.K, units = g.units;
-    const int su = (units + 3) / 4;
+    const int su = (units + NW - 1) / NW;
     const int nseg = (units + su - 1) / su;
     const int u_begin = min(units, wave * su), u_end = min(units, u_begin + su);
 
@@ -2469,7 +2470,7 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
      * selector code | flag << 2: built once per tile into LDS (rows of 9 floats, so the 16 columns a wave reads
      * spread over the banks), then one extract and one LDS read per weight. */
     __shared__ float wtab[BN * 9];
-    for (int c = tid; c < BN * 8; c += 256) {
+    for (int c = tid; c < BN * 8; c += NT) {
         const int col = c >> 3, sel = c & 7, n = min(n0 + col, N - 1);
         const float lo = g.lo[n], d = g.hi[n] - lo;
         wtab[col * 9 + sel] = (float)((sel & 3) - 1) * __builtin_fmaf((float)(sel >> 2), d, lo);
@@ -2527,49 +2528,46 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
         }
     };
     if constexpr (STAGED) {
-        /* stage st = 2·(u − u_begin) + s into slot st % 2 of this wave; load q brings rows 4q .. 4q + 3, lane L
-         * filling place L % 16 of row 4q + L / 16 with that row's chunk (L % 16) ^ (row % 16) */
+        /* stage st = 2·(u − u_begin) + s into this wave's slot; load q brings rows 4q .. 4q + 3, lane L filling place
+         * L % 16 of row 4q + L / 16 with that row's chunk (L % 16) ^ (row % 16) */
         const float *a_src[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
             const int rr = 4 * q + (lane >> 4);
             a_src[q] = g.A + (size_t)min(m0 + rr, M - 1) * g.lda + 4 * ((lane & 15) ^ (rr & 15));
         }
-        int8_t *slots = smem + wave * 2 * ABUF;
+        int8_t *slot = smem + wave * ABUF;
         const int n_st = 2 * (u_end - u_begin);
         auto issue = [&](int st) __attribute__((always_inline)) {
             const int u = u_begin + (st >> 1);
-            int8_t *dst = slots + (st & 1) * ABUF;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* this wave's reads of the slot are complete */
 #pragma unroll
-            for (int q = 0; q < NQ; q++) dma_16(a_src[q] + 128 * u + 64 * (st & 1), dst + q * 1024);
-            if ((st & 1) == 0) load_records((st >> 1) & 1, u);
+            for (int q = 0; q < NQ; q++) dma_16(a_src[q] + 128 * u + 64 * (st & 1), slot + q * 1024);
+            if ((st & 1) == 0) load_records(0, u);
         };
         auto compute = [&](int st) __attribute__((always_inline)) {
-            const int8_t *src = slots + (st & 1) * ABUF;
             float x[FM][16];
 #pragma unroll
             for (int j = 0; j < FM; j++) {
-                const int8_t *row = src + (16 * j + (lane & 15)) * 256;
+                const int8_t *row = slot + (16 * j + (lane & 15)) * 256;
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
                     const float4 v = *reinterpret_cast<const float4 *>(row + 16 * ((4 * grp + q4) ^ (lane & 15)));
                     x[j][4 * q4] = v.x; x[j][4 * q4 + 1] = v.y; x[j][4 * q4 + 2] = v.z; x[j][4 * q4 + 3] = v.w;
                 }
             }
-            mma_step((st >> 1) & 1, st & 1, x);
+            mma_step(0, st & 1, x);
         };
-        if (n_st > 0) issue(0);
+        /* one slot per wave, every load waited before its stage is multiplied: the other waves of the CU (up to four
+         * per SIMD: 34 KB of LDS and at most 128 VGPRs per wave) cover each wave's wait. Two slots per wave with the
+         * next stage in flight measured 5-14 % slower (the doubled LDS halves the workgroups per CU), and eight
+         * waves splitting K no faster. */
         for (int st = 0; st < n_st; st += 2) {
-            issue(st + 1);           /* step 1 of the unit: direct loads only */
-            wait_vm<NQ>();           /* step 0 (and the unit's records) landed */
+            issue(st);        /* step 0 of the unit and its records */
+            wait_vm<0>();
             compute(st);
-            if (st + 2 < n_st) {
-                issue(st + 2);       /* the next unit's step 0 and records */
-                wait_vm<NQ + FN>();
-            } else {
-                wait_vm<0>();
-            }
+            issue(st + 1);    /* step 1 */
+            wait_vm<0>();
             compute(st + 1);
         }
         __syncthreads();   /* every wave is done with its slots: the partial tiles reuse the area */
@@ -2606,7 +2604,7 @@ __global__ __launch_bounds__(256, 2) void gemm_xf(ExactArgs g)
     }
     __syncthreads();
 
-    constexpr int TPR = BN / 4, RPP = 256 / TPR;
+    constexpr int TPR = BN / 4, RPP = NT / TPR;
     const int cq = tid % TPR, n = n0 + 4 * cq;
     if (n >= N) return;
     for (int row = tid / TPR; row < BM; row += RPP) {
