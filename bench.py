@@ -270,6 +270,26 @@ def measure_chain(spec, stream, steps, warmup, kreps, per=1):
     return ch.linears, ms, wall, qt, gt, grouped
 
 
+def exact_sweep_config(stream, steps=20, warmup=3):
+    """The 216 linears of one 30 s window in exact mode, the reference's only route on x86 (blas.c:1021-1023): each
+    linear's fp32 rows straight into the exact GEMM on the fp32 matrix cores (p2h_fvb_gemm, no quantisation), the
+    24 positional projections one by one (the grouped launch is the int8 modes'), one graph per window."""
+    spec = sweep_spec(375)
+    linears, inputs, _, keep = build_chain(spec, None)
+
+    def body():
+        for lin, (dA, lda) in zip(linears, inputs):
+            P.fvb_gemm_dev("exact", lin.M, lin.N, lin.K, lin.alpha, dA, lda, lin.w, 0.0, lin.out.ptr, lin.N, None, 0,
+                           stream.ptr)
+
+    ms, _ = StepGraphs(stream, body, 1, steps).time(steps, warmup)
+    flops = sum(2.0 * l.M * l.N * l.K for l in linears)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"what": "216 encoder linears of one 30 s window (M=375, pos M=749), exact mode (fp32 matrix cores)",
+            "ms_per_30s_window": round(ms, 4), "tflops": round(tf, 2),
+            "pct_fp32_peak": round(100.0 * tf / PEAK_FP32_TFLOPS, 2)}
+
+
 def summarize(linears, ms, qt, gt):
     ops = sum(gemm_ops(l.M, l.N, l.K) for l in linears)
     planes = sum(l.K * l.N * 3 / 8 + 8 * l.N for l in linears)
@@ -581,6 +601,8 @@ def main():
             _, rr = run(name, specs[name](), steps, 20, kreps)
             extra[name] = rr
         extra["exact375"] = exact_config(stream)
+        if not args.no_sweep:
+            extra["sweep_exact"] = exact_sweep_config(stream)
         extra["attention375"] = attention_config(stream)
         extra["producers"] = producer_config(stream)
         extra["ffn_module375"] = ffn_module_config(stream)
