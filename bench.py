@@ -273,19 +273,28 @@ def measure_chain(spec, stream, steps, warmup, kreps, per=1):
     return ch.linears, ms, wall, qt, gt, grouped
 
 
-def exact_sweep_config(stream, steps=20, warmup=3):
-    """The 216 linears of one 30 s window in exact mode, the reference's only route on x86 (blas.c:1021-1023): each
-    linear's fp32 rows straight into the exact GEMM on the fp32 matrix cores (p2h_fvb_gemm, no quantisation), the
-    24 positional projections one by one (the grouped launch is the int8 modes'), one graph per window."""
-    spec = sweep_spec(375)
-    linears, inputs, _, keep = build_chain(spec, None)
+class ExactChain:
+    """A chain of five-value linears in exact mode, the reference's only route on x86 (blas.c:1021-1023): each
+    linear's fp32 rows straight into the exact GEMM (p2h_fvb_gemm, no quantisation; the fp32 matrix cores, or the
+    per-output fmaf chain when P2H_EXACT_CHAIN=1 at capture), every linear, the positional projections included,
+    with its own alpha. body() queues one pass; it can be captured into a graph."""
 
-    def body():
-        for lin, (dA, lda) in zip(linears, inputs):
+    def __init__(self, spec):
+        self.spec = spec
+        self.linears, self.inputs, _, self.keep = build_chain(spec, None)
+
+    def body(self, stream):
+        for lin, (dA, lda) in zip(self.linears, self.inputs):
             P.fvb_gemm_dev("exact", lin.M, lin.N, lin.K, lin.alpha, dA, lda, lin.w, 0.0, lin.out.ptr, lin.N, None, 0,
                            stream.ptr)
 
-    ms, _ = StepGraphs(stream, body, 1, steps).time(steps, warmup)
+
+def exact_sweep_config(stream, steps=20, warmup=3):
+    """The 216 linears of one 30 s window in exact mode (ExactChain): the 24 positional projections one by one (the
+    grouped launch is the int8 modes'), one graph per window."""
+    ch = ExactChain(sweep_spec(375))
+    linears = ch.linears
+    ms, _ = StepGraphs(stream, lambda: ch.body(stream), 1, steps).time(steps, warmup)
     flops = sum(2.0 * l.M * l.N * l.K for l in linears)
     tf = flops / (ms * 1e-3) / 1e12
     return {"what": "216 encoder linears of one 30 s window (M=375, pos M=749), exact mode (fp32 matrix cores)",

@@ -11,6 +11,8 @@
 #include <cstdio>
 #include <cstring>
 #include <cstdlib>
+#include <climits>
+#include <atomic>
 #include <mutex>
 
 #include "p2hip_kernels.h"
@@ -51,6 +53,8 @@ int fail(int rc, const char *fmt, ...)
         if (e_ != hipSuccess) return fail(P2H_E_DEVICE, "%s: %s", #call, hipGetErrorString(e_));              \
     } while (0)
 
+void load_switches();
+
 void do_init()
 {
     int n = 0;
@@ -72,6 +76,7 @@ void do_init()
         return;
     }
     g_cus = prop.multiProcessorCount;
+    load_switches();
     if (hipDeviceGetAttribute(&g_wall_khz, hipDeviceAttributeWallClockRate, 0) != hipSuccess || g_wall_khz <= 0)
         g_wall_khz = 100000;
     e = hipSetDevice(0);
@@ -123,6 +128,41 @@ int env_int(const char *name, int dflt)
     const char *v = getenv(name);
     return (v && *v) ? atoi(v) : dflt;
 }
+
+/* The tuning and comparison switches, read from the environment once at initialisation and again only by
+ * p2h_reload_switches: no launch reads the environment, so a host thread calling setenv races with nothing but an
+ * explicit reload. kUnset marks a tile that is not forced. */
+constexpr int kUnset = INT_MIN;
+struct Switches {
+    std::atomic<int> tile{kUnset};          /* P2H_TILE: force a five-value tile */
+    std::atomic<int> split_rows{0};         /* P2H_SPLIT_ROWS: force a K split (-1: never) */
+    std::atomic<int> xf_staged{1};          /* P2H_XF_STAGED: 0 loads the exact route's rows into registers */
+    std::atomic<int> xf_tile{0};            /* P2H_XF_TILE: force the exact route's tile width */
+    std::atomic<int> exact_chain{0};        /* P2H_EXACT_CHAIN: the exact route's per-output fmaf chain */
+    std::atomic<int> sgemm_any{0};          /* P2H_SGEMM_ANY: the fp32 GEMM's element loads */
+    std::atomic<int> attention_fused{1};    /* P2H_ATTENTION_FUSED: 0 runs the attention as separate products */
+    std::atomic<int> silu_epilogue{1};      /* P2H_SILU_EPILOGUE: 0 uses the SiLU→int8 producer in the block */
+    std::atomic<int> exact_epilogue{1};     /* P2H_EXACT_EPILOGUE: 0 runs exact mode's residuals and SiLU apart */
+    std::atomic<int> stack_norm_pairs{1};   /* P2H_STACK_NORM_PAIRS: 0 keeps the stack's LayerNorms unpaired */
+};
+Switches g_sw;
+
+void load_switches()
+{
+    const auto r = std::memory_order_relaxed;
+    g_sw.tile.store(env_int("P2H_TILE", kUnset), r);
+    g_sw.split_rows.store(env_int("P2H_SPLIT_ROWS", 0), r);
+    g_sw.xf_staged.store(env_int("P2H_XF_STAGED", 1), r);
+    g_sw.xf_tile.store(env_int("P2H_XF_TILE", 0), r);
+    g_sw.exact_chain.store(env_int("P2H_EXACT_CHAIN", 0), r);
+    g_sw.sgemm_any.store(env_int("P2H_SGEMM_ANY", 0), r);
+    g_sw.attention_fused.store(env_int("P2H_ATTENTION_FUSED", 1), r);
+    g_sw.silu_epilogue.store(env_int("P2H_SILU_EPILOGUE", 1), r);
+    g_sw.exact_epilogue.store(env_int("P2H_EXACT_EPILOGUE", 1), r);
+    g_sw.stack_norm_pairs.store(env_int("P2H_STACK_NORM_PAIRS", 1), r);
+}
+
+inline int switch_of(const std::atomic<int> &v) { return v.load(std::memory_order_relaxed); }
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
@@ -145,6 +185,12 @@ extern "C" {
 /* ── runtime ────────────────────────────────────────────────────────────────────────────────────────────────── */
 
 int p2h_init(void) { return ensure_init(); }
+
+int p2h_reload_switches(void)
+{
+    load_switches();
+    return P2H_OK;
+}
 
 const char *p2h_last_error(void) { return t_err; }
 
@@ -1008,7 +1054,7 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     }
     else
         cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_WK : FV_W6) : FV_L;
-    cfg = env_int("P2H_TILE", cfg);
+    if (switch_of(g_sw.tile) != kUnset) cfg = switch_of(g_sw.tile);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
     if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_WK)) cfg = FV_L;
     if (mode == P2H_INT8 && (cfg == FV_SW || cfg == FV_SD)) cfg = FV_SS;
@@ -1024,7 +1070,7 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     p.split_rows = K > 0 ? K : 1;
     int rows = 0;
     if (K > p2k::kFoldRows) rows = (M <= 64 && tiles * (K / 512) <= 2 * cus) ? 512 : p2k::kFoldRows;
-    const int forced = env_int("P2H_SPLIT_ROWS", 0);
+    const int forced = switch_of(g_sw.split_rows);
     if (forced < 0) rows = 0;
     else if (forced > 0 && forced <= p2k::kFoldRows && p2k::kFoldRows % forced == 0 && forced % 128 == 0) rows = forced;
     if (can_split && !large && K > 0 && rows > 0 && (K + rows - 1) / rows > 1) {
@@ -1246,7 +1292,8 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
     if (is_small(p.cfg) && mode == P2H_INT8W &&
         make_plan(mode, M, (int)std::min<long long>((long long)N * groups, 1 << 30), K, false).cfg == FV_SW) {
         const long long w6_tiles = (long long)((M + FvW6::BM - 1) / FvW6::BM) * ((N + FvW6::BN - 1) / FvW6::BN) * groups;
-        wide = M >= 512 && w6_tiles >= (g_cus > 0 ? g_cus : 256) && env_int("P2H_TILE", -1) < 0;
+        const int forced_tile = switch_of(g_sw.tile);
+        wide = M >= 512 && w6_tiles >= (g_cus > 0 ? g_cus : 256) && (forced_tile == kUnset || forced_tile < 0);
         p.cfg = wide ? FV_W6 : FV_SW;
         p.tiles_m = wide ? (M + FvW6::BM - 1) / FvW6::BM : (M + SmW::BM - 1) / SmW::BM;
         p.tiles_n = wide ? (N + FvW6::BN - 1) / FvW6::BN : (N + SmW::BN - 1) / SmW::BN;
@@ -1352,7 +1399,7 @@ void launch_xf_tile(const p2k::ExactArgs &g, hipStream_t s)
 {
     const dim3 grid((unsigned)((size_t)g.tiles_n * ((g.M + 31) / 32))), block(256);
     const bool vec = g.K % 4 == 0 && g.lda % 4 == 0 && aligned(g.A, 16);
-    const bool staged = vec && g.K % 128 == 0 && env_int("P2H_XF_STAGED", 1) != 0;
+    const bool staged = vec && g.K % 128 == 0 && switch_of(g_sw.xf_staged) != 0;
     if (staged) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true, true>), grid, block, 0, s, g);
     else if (vec) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true>), grid, block, 0, s, g);
     else hipLaunchKernelGGL((p2k::gemm_xf<2, FN, false>), grid, block, 0, s, g);
@@ -1363,7 +1410,7 @@ int launch_xf(const p2k::ExactArgs &g0, hipStream_t s)
     p2k::ExactArgs g = g0;
     const int cus = g_cus > 0 ? g_cus : 256;
     int bn = ((size_t)((g.N + 63) / 64) * ((g.M + 31) / 32) >= (size_t)2 * cus) ? 64 : 32;
-    const int forced = env_int("P2H_XF_TILE", 0);
+    const int forced = switch_of(g_sw.xf_tile);
     if (forced == 32 || forced == 64) bn = forced;
     g.tiles_n = (g.N + bn - 1) / bn;
     if (bn == 64) launch_xf_tile<4>(g, s);
@@ -1415,7 +1462,7 @@ static int exact_gemm(int M, int N, int K, float alpha, const float *dA, int lda
     g.signs = w->signs; g.flags = w->flags; g.lo = w->lo; g.hi = w->hi;
     g.C = dC; g.ldc = ldc;
     g.rec = w->rec4; g.units = w->units;
-    if (env_int("P2H_EXACT_CHAIN", 0) != 0 || K == 0) {
+    if (switch_of(g_sw.exact_chain) != 0 || K == 0) {
         if (int rc = launch_exact(p2k::EXB_FV, g, s)) return rc;
         return silu ? p2h_silu((size_t)M * N, dC, s) : P2H_OK;
     }
@@ -1593,7 +1640,7 @@ int p2h_sgemm_batched(int transA, int transB, int M, int N, int K, float alpha, 
                                            decltype(lb)::value>),
                            grid, dim3(256), 0, s, g);
     };
-    const bool any = !small || env_int("P2H_SGEMM_ANY", 0) != 0;   /* the variable forces the element loads (tests) */
+    const bool any = !small || switch_of(g_sw.sgemm_any) != 0;   /* the variable forces the element loads (tests) */
     auto by_load = [&](auto ta, auto tb) {
         if (any) go(ta, tb, AnyT{}, AnyT{});
         else if (va && vb) go(ta, tb, VecT{}, VecT{});
@@ -1678,7 +1725,7 @@ BlockWs block_ws(int mode, int T, char *base)
 bool fused_attention(int T, const P2hBlock *blk)
 {
     return T <= P2H_ATTENTION_TMAX && aligned(blk->bias_u, 16) && aligned(blk->bias_v, 16) &&
-           env_int("P2H_ATTENTION_FUSED", 1) != 0;
+           switch_of(g_sw.attention_fused) != 0;
 }
 
 int check_block_weight(const P2hWeight *w, int K, int N, const char *name)
@@ -1737,14 +1784,14 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
         if (mode == P2H_EXACT) return p2h_layer_norm_rows(T, D, dX, D, g, b, w.ln, D, s);
         return p2h_layer_norm_quant_rows(T, D, dX, D, g, b, w.q, ldD, w.sc, s);
     };
-    static const bool silu_epilogue = env_int("P2H_SILU_EPILOGUE", 1) != 0;   /* 0: the SiLU→int8 producer instead */
+    const bool silu_epilogue = switch_of(g_sw.silu_epilogue) != 0;   /* 0: the SiLU→int8 producer instead */
     /* Exact mode's residuals (add_residual, encoder.c:252-275: x = fmaf(y, α, x) over y = the linear's output) in the
      * matrix-core GEMM's epilogue: fmaf(α, sum, x) with β = 1 is the same value, y being the sum itself (α = 1,
      * β = 0: fmaf(1, sum, 0)); only a −0 sum onto a −0 x would differ. The feed-forward's SiLU there too (see
      * exact_gemm). The fmaf-chain route (P2H_EXACT_CHAIN=1) keeps the separate passes, as the reference computes
      * them; so does P2H_EXACT_EPILOGUE=0. */
-    const bool res_epilogue = mode == P2H_EXACT && env_int("P2H_EXACT_CHAIN", 0) == 0 &&
-                              env_int("P2H_EXACT_EPILOGUE", 1) != 0;
+    const bool res_epilogue = mode == P2H_EXACT && switch_of(g_sw.exact_chain) == 0 &&
+                              switch_of(g_sw.exact_epilogue) != 0;
     /* feed_forward (encoder.c:333-362): x += ½ · W2 · SiLU(W1 · LN(x)) */
     auto feed_forward = [&](const float *g, const float *b, const P2hWeight *l1, const P2hWeight *l2,
                             bool norm_done) {
@@ -1923,7 +1970,7 @@ int p2h_conformer_stack(int mode, const P2hBlock *blocks, int n_blocks, int T, c
         }
     }
     /* int8 modes: each block's output norm and the next block's first norm in one kernel */
-    const bool pair_norms = mode != P2H_EXACT && env_int("P2H_STACK_NORM_PAIRS", 1) != 0;
+    const bool pair_norms = mode != P2H_EXACT && switch_of(g_sw.stack_norm_pairs) != 0;
     for (int b = 0; b < n_blocks; b++) {
         const P2hBlock *next = pair_norms && b + 1 < n_blocks ? &blocks[b + 1] : nullptr;
         if (int rc = run_block(mode, &blocks[b], T, dPE, mode != P2H_EXACT ? sw.P + (size_t)b * L * D : nullptr, dX,

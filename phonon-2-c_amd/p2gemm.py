@@ -29,6 +29,7 @@ _vp, _sz, _i, _f = C.c_void_p, C.c_size_t, C.c_int, C.c_float
 
 _HIP_SIG = {
     "p2h_init": (_i, []),
+    "p2h_reload_switches": (_i, []),
     "p2h_last_error": (C.c_char_p, []),
     "p2h_device_name": (C.c_char_p, []),
     "p2h_device_cu_count": (_i, []),
@@ -133,6 +134,11 @@ def last_error():
 def _ok(rc, what):
     if rc != 0:
         raise P2Error(f"{what}: {last_error()} (rc {rc})")
+
+
+def reload_switches():
+    """Re-read the library's P2H_* tuning and comparison switches from the environment (read once at init)."""
+    _ok(hip().p2h_reload_switches(), "p2h_reload_switches")
 
 
 def init():

@@ -301,8 +301,8 @@ def test_block_against_reference(mode, T, tmp_path):
     print(f"  per-frame max {row_rel.max():.3g}, block {total_rel:.3g}", flush=True)
     if mode == "exact":
         assert row_rel.max() <= 2e-5
-    else:
-        assert row_rel.max() <= 2e-2 and total_rel <= 1e-2
+    else:   # measured on MI355X: per frame at most 5.8e-3, over the block 2.9e-3 to 3.4e-3 (T = 375, 500, 800)
+        assert row_rel.max() <= 8e-3 and total_rel <= 5e-3
 
 
 @pytest.mark.skipif(not O.refblock_available(), reason="reference block library not built")
@@ -327,7 +327,12 @@ def test_block_step_against_reference(mode, stage, tmp_path):
           f"per frame max {rel.max():.3g} median {np.median(rel):.3g} of the contribution", flush=True)
     print(f"  percentiles 90 / 99: {np.percentile(rel, 90):.3g} / {np.percentile(rel, 99):.3g}", flush=True)
     assert np.linalg.norm(contrib) > 1e-2 * np.linalg.norm(ref)   # the step does contribute
-    assert np.median(rel) <= 1e-4 and rel.max() <= 1e-2
+    # measured on MI355X (both int8 modes): the median frame within 1.6e-5 of the contribution on every step; the
+    # 99th percentile 1.8e-3 on step 1 (where a moved code propagates through the convolution) and at most 2.2e-6
+    # on the others; the worst frame 3.0e-3, 1.7e-3 on step 2, 1.6e-6 on step 3
+    p99_bound, max_bound = {0: (1e-5, 2e-3), 1: (3e-3, 5e-3), 2: (1e-5, 3e-3), 3: (1e-5, 1e-4)}[stage]
+    assert np.median(rel) <= 5e-5
+    assert np.percentile(rel, 99) <= p99_bound and rel.max() <= max_bound
 
 
 @pytest.mark.parametrize("T", [375, 520])
@@ -343,6 +348,23 @@ def test_exact_epilogues_same_bits(monkeypatch, T):
     fused = blk.run("exact", x, pe)
     monkeypatch.setenv("P2H_EXACT_EPILOGUE", "0")
     separate = blk.run("exact", x, pe)
+    assert np.isfinite(fused).all()
+    assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode,T", [("int8w", 375), ("int8", 375), ("int8w", 40)])
+def test_silu_epilogue_same_bits(monkeypatch, mode, T):
+    """The int8 modes apply the feed-forward's SiLU in the up-projection's epilogue and quantise its rows with the
+    plain quantiser; the block equals the one with the SiLU→int8 producer after a plain GEMM (P2H_SILU_EPILOGUE=0,
+    p2_swish_quant_rows' order, tensor_ops.c:491-511) bit for bit."""
+    print(f"SiLU epilogue mode={mode} T={T}", flush=True)
+    sys.path.insert(0, HERE)
+    import refblock_child as RC
+    x, pe = RC.block_input(SEED, T)
+    blk = _device_block(SEED)
+    fused = blk.run(mode, x, pe)
+    monkeypatch.setenv("P2H_SILU_EPILOGUE", "0")
+    separate = blk.run(mode, x, pe)
     assert np.isfinite(fused).all()
     assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
 
