@@ -173,12 +173,18 @@ typedef struct Entry {
     void *dq8; float *dsc;       /* int8 table: [K][N] int8, [N] scales */
     int refs;                    /* calls using the copy now */
     int dead;                    /* unlinked from the cache: freed when refs drops to 0 */
+    int ready;                   /* the device copy is complete (0 while its first caller uploads it) */
     struct Entry *next;
+    struct Entry *free_next;     /* on a list of entries to free once cache_mu is released */
 } Entry;
 
 #define CACHE_BUCKETS 1024
 static Entry *cache[CACHE_BUCKETS];
+/* cache_mu guards the table and the entries' refs / dead / ready; uploads and frees run outside it, so one thread's
+ * first-touch upload or a cache clear does not stall other threads' calls on weights already on the device. A
+ * caller that finds an entry still being uploaded waits on cache_cv for it. */
 static pthread_mutex_t cache_mu = PTHREAD_MUTEX_INITIALIZER;
+static pthread_cond_t cache_cv = PTHREAD_COND_INITIALIZER;
 
 /* P2_GPU_WEIGHT_CACHE=0: every call uploads its weight and frees the copy afterwards (for callers that change
  * weights in place, which the fingerprint does not fully cover) */
@@ -225,25 +231,54 @@ static void entry_free(Entry *e)
     free(e);
 }
 
-/* cache_mu held: take e out of the cache; free it now if no call holds it, else its last holder does */
-static void entry_drop_locked(Entry *e)
+/* frees a list made under cache_mu, after it is released (hipFree synchronises the device) */
+static void free_list(Entry *list)
+{
+    while (list) {
+        Entry *n = list->free_next;
+        entry_free(list);
+        list = n;
+    }
+}
+
+/* cache_mu held: take e out of the cache; put it on *to_free if no call holds it, else its last holder frees it */
+static void entry_drop_locked(Entry *e, Entry **to_free)
 {
     e->dead = 1;
-    if (e->refs == 0) entry_free(e);
+    if (e->refs == 0) {
+        e->free_next = *to_free;
+        *to_free = e;
+    }
 }
 
 /* a call is done with e (its kernels have finished) */
 static void entry_put(Entry *e)
 {
     pthread_mutex_lock(&cache_mu);
-    if (--e->refs == 0 && e->dead) entry_free(e);
+    const int last = --e->refs == 0 && e->dead;
+    pthread_mutex_unlock(&cache_mu);
+    if (last) entry_free(e);
+}
+
+/* cache_mu held: e was found in the cache; wait until its first caller has finished uploading it */
+static void entry_wait_ready_locked(Entry *e)
+{
+    while (!e->ready) pthread_cond_wait(&cache_cv, &cache_mu);
+}
+
+/* the uploader's device copy is complete: wake the callers waiting for it */
+static void entry_publish(Entry *e)
+{
+    pthread_mutex_lock(&cache_mu);
+    e->ready = 1;
+    pthread_cond_broadcast(&cache_cv);
     pthread_mutex_unlock(&cache_mu);
 }
 
 /* cache_mu held: the live entry for this key with this fingerprint, taken (refs + 1); a stale entry at the same key
- * is dropped; NULL when there is none */
+ * is dropped (onto *to_free when nothing holds it); NULL when there is none */
 static Entry *entry_find_locked(size_t h, int kind, const void *a, const void *b, const void *c, const void *d, int K,
-                                int N, int ld, uint64_t fp)
+                                int N, int ld, uint64_t fp, Entry **to_free)
 {
     for (Entry **pe = &cache[h]; *pe; pe = &(*pe)->next) {
         Entry *e = *pe;
@@ -254,7 +289,7 @@ static Entry *entry_find_locked(size_t h, int kind, const void *a, const void *b
                 return e;
             }
             *pe = e->next;   /* same addresses, new contents: drop the stale copy */
-            entry_drop_locked(e);
+            entry_drop_locked(e, to_free);
             return NULL;
         }
     }
@@ -279,6 +314,8 @@ static Entry *entry_new_locked(size_t h, int kind, const void *a, const void *b,
     return e;
 }
 
+/* The cache entry of a five-value weight, taken (refs + 1): found, waiting for its upload if another thread is
+ * making it, or made here: a placeholder goes into the cache under cache_mu, the upload runs outside it. */
 static Entry *fv_weight(const FiveValueB *B, int K, int N)
 {
     pthread_once(&cache_env_once, cache_env_init);
@@ -286,14 +323,21 @@ static Entry *fv_weight(const FiveValueB *B, int K, int N)
     uint64_t fp = fingerprint(B->signs, kn / 4 ? kn / 4 : 1, B->flags, kn / 8 ? kn / 8 : 1, B->lo, B->hi,
                               (size_t)N * sizeof(float));
     size_t h = bucket(B->signs, K, N);
+    Entry *to_free = NULL;
     pthread_mutex_lock(&cache_mu);
-    Entry *e = cache_on ? entry_find_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp) : NULL;
-    if (!e) {
-        e = entry_new_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp, "p2_sgemm_fvb");
-        e->w = p2h_fv_weight_upload(B->signs, B->flags, B->lo, B->hi, K, N);
-        if (!e->w) die("p2_sgemm_fvb: weight upload", p2h_last_error());
+    Entry *e = cache_on ? entry_find_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp, &to_free) : NULL;
+    if (e) {
+        entry_wait_ready_locked(e);
+        pthread_mutex_unlock(&cache_mu);
+        free_list(to_free);
+        return e;
     }
+    e = entry_new_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp, "p2_sgemm_fvb");
     pthread_mutex_unlock(&cache_mu);
+    free_list(to_free);
+    e->w = p2h_fv_weight_upload(B->signs, B->flags, B->lo, B->hi, K, N);
+    if (!e->w) die("p2_sgemm_fvb: weight upload", p2h_last_error());
+    entry_publish(e);
     return e;
 }
 
@@ -303,34 +347,43 @@ static Entry *q8_weight(const signed char *B, const float *scales, int ldb, int 
     size_t rows_bytes = K > 0 ? (size_t)(K - 1) * ldb + N : 1;
     uint64_t fp = fingerprint(B, rows_bytes, NULL, 0, scales, NULL, (size_t)N * sizeof(float));
     size_t h = bucket(B, K, N);
+    Entry *to_free = NULL;
     pthread_mutex_lock(&cache_mu);
-    Entry *e = cache_on ? entry_find_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp) : NULL;
-    if (!e) {
-        e = entry_new_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp, "p2_sgemm_q8b");
-        e->dq8 = p2h_malloc((size_t)K * N + 16);
-        e->dsc = (float *)p2h_malloc((size_t)N * sizeof(float));
-        if (!e->dq8 || !e->dsc) die("p2_sgemm_q8b: weight upload", p2h_last_error());
-        check(p2h_memcpy2d_h2d(e->dq8, (size_t)N, B, (size_t)ldb, (size_t)N, (size_t)K, stream), "p2_sgemm_q8b");
-        check(p2h_memcpy_h2d(e->dsc, scales, (size_t)N * sizeof(float), stream), "p2_sgemm_q8b");
-        check(p2h_stream_sync(stream), "p2_sgemm_q8b");
+    Entry *e = cache_on ? entry_find_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp, &to_free) : NULL;
+    if (e) {
+        entry_wait_ready_locked(e);
+        pthread_mutex_unlock(&cache_mu);
+        free_list(to_free);
+        return e;
     }
+    e = entry_new_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp, "p2_sgemm_q8b");
     pthread_mutex_unlock(&cache_mu);
+    free_list(to_free);
+    e->dq8 = p2h_malloc((size_t)K * N + 16);
+    e->dsc = (float *)p2h_malloc((size_t)N * sizeof(float));
+    if (!e->dq8 || !e->dsc) die("p2_sgemm_q8b: weight upload", p2h_last_error());
+    check(p2h_memcpy2d_h2d(e->dq8, (size_t)N, B, (size_t)ldb, (size_t)N, (size_t)K, stream), "p2_sgemm_q8b");
+    check(p2h_memcpy_h2d(e->dsc, scales, (size_t)N * sizeof(float), stream), "p2_sgemm_q8b");
+    check(p2h_stream_sync(stream), "p2_sgemm_q8b");
+    entry_publish(e);
     return e;
 }
 
 void p2_gpu_weight_cache_clear(void)
 {
+    Entry *to_free = NULL;
     pthread_mutex_lock(&cache_mu);
     for (int i = 0; i < CACHE_BUCKETS; i++) {
         Entry *e = cache[i];
         while (e) {
             Entry *n = e->next;
-            entry_drop_locked(e);
+            entry_drop_locked(e, &to_free);
             e = n;
         }
         cache[i] = NULL;
     }
     pthread_mutex_unlock(&cache_mu);
+    free_list(to_free);
 }
 
 /* ── operand staging ───────────────────────────────────────────────────────────────────────────────────────── */

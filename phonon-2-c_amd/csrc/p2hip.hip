@@ -165,6 +165,14 @@ void load_switches()
 inline int switch_of(const std::atomic<int> &v) { return v.load(std::memory_order_relaxed); }
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+/* Whether M rows of Y (pitch ldy floats) overlap M rows of X (pitch ldx) other than as the very same rows. */
+inline bool rows_overlap(const float *dX, int ldx, const float *dY, int ldy, int M)
+{
+    if (dX == dY) return false;
+    return (const char *)dY < (const char *)(dX + (size_t)M * ldx) &&
+           (const char *)dX < (const char *)(dY + (size_t)M * ldy);
+}
+
 }  // namespace
 
 struct P2hWeight {
@@ -713,15 +721,21 @@ int p2h_layer_norm2_quant_rows(int M, int D, const float *dX, int ldx, const flo
                                float *dY, int ldy, const float *dGamma2, const float *dBeta2, signed char *dQ, int ldq,
                                float *dScales, void *stream)
 {
-    if (int rc = ensure_init()) return rc;
+    /* the arguments first, so that they fail the same way with or without a device */
     const char *name = "p2h_layer_norm2_quant_rows";
     if (M < 0 || D < 1 || D > 1024) return fail(P2H_E_ARG, "%s: %d rows of %d columns (columns 1..1024)", name, M, D);
     if (M == 0) return P2H_OK;
     if (!dX || !dY || !dGamma1 || !dBeta1 || !dGamma2 || !dBeta2 || !dQ || !dScales || ldx < D || ldy < D)
         return fail(P2H_E_ARG, "%s: null pointer, or ldx = %d / ldy = %d < D = %d", name, ldx, ldy, D);
+    /* Y may be X itself (each wave reads its whole row before writing it), but not part of other rows of X: a
+     * wave's stores would land in rows another wave has not read yet */
+    if (rows_overlap(dX, ldx, dY, ldy, M))
+        return fail(P2H_E_ARG, "%s: X and Y overlap without being the same rows", name);
+    if (dX == dY && ldx != ldy) return fail(P2H_E_ARG, "%s: in place needs ldy == ldx", name);
     if (ldq < p2h_q_ld(D) || ldq % P2H_Q_KALIGN != 0 || ldq > 1024 || !aligned(dQ, 16))
         return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d, <= 1024 and a multiple of %d, Q 16-byte aligned", name,
                     ldq, p2h_q_ld(D), P2H_Q_KALIGN);
+    if (int rc = ensure_init()) return rc;
     p2k::ProdArgs a{};
     a.M = M; a.K = D; a.X = dX; a.ldx = ldx; a.gamma = dGamma1; a.beta = dBeta1;
     a.gamma2 = dGamma2; a.beta2 = dBeta2; a.Y1 = dY; a.ldy1 = ldy;
@@ -774,13 +788,13 @@ int p2h_channel_major_quant_rows(int D, int T, const float *dDW, signed char *dQ
 int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta, float *dY,
                         int ldy, void *stream)
 {
-    if (int rc = ensure_init()) return rc;
+    /* the arguments first, so that they fail the same way with or without a device */
     if (M > 0 && (ldx < D || !dGamma || !dBeta || !dY))
         return fail(P2H_E_ARG, "p2h_layer_norm_rows: ldx = %d < D = %d or a null pointer", ldx, D);
-    if (M > 0 && dX != dY && ((const char *)dY < (const char *)(dX + (size_t)M * ldx) &&
-                              (const char *)dX < (const char *)(dY + (size_t)M * ldy)))
+    if (M > 0 && rows_overlap(dX, ldx, dY, ldy, M))
         return fail(P2H_E_ARG, "p2h_layer_norm_rows: X and Y overlap without being the same rows");
     if (M > 0 && dX == dY && ldx != ldy) return fail(P2H_E_ARG, "p2h_layer_norm_rows: in place needs ldy == ldx");
+    if (int rc = ensure_init()) return rc;
     p2k::ProdArgs a{};
     a.M = M; a.K = D; a.X = dX; a.ldx = ldx; a.gamma = dGamma; a.beta = dBeta; a.Y = dY; a.ldy = ldy;
     return produce("p2h_layer_norm_rows", p2k::PROD_LN, a,

@@ -66,3 +66,36 @@ def test_q_tile_layout_matches_the_documented_index():
         assert np.array_equal(t, expect)
         back = P.q_untile(t, M, ldq)
         assert np.array_equal(back[:M, :K], q) and not back[M:].any() and not back[:, K:].any()
+
+
+def test_layer_norm_entries_reject_overlapping_rows():
+    """p2h_layer_norm_rows and p2h_layer_norm2_quant_rows check their arguments before touching a device: Y may be X
+    itself with the same pitch, but rows of Y that overlap other rows of X are refused (a wave's stores would land
+    in rows another wave has not read), as is in place with another pitch. The pointers are never dereferenced."""
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("fake device pointers: run where no GPU can be reached")
+    lib = P.hip()
+    vp = C.c_void_p
+    base = 0x7f0000000000   # a fake device address: every call here must fail in its argument checks
+    M, D = 8, 1024
+    X = base
+    g1, b1, g2, b2, Q, S = (base + 0x1000000 * k for k in range(1, 7))
+
+    def ln2(Y, ldx, ldy, ldq=1024):
+        return lib.p2h_layer_norm2_quant_rows(M, D, vp(X), ldx, vp(g1), vp(b1), vp(Y), ldy, vp(g2), vp(b2), vp(Q),
+                                              ldq, vp(S), None)
+
+    def ln(Y, ldx, ldy):
+        return lib.p2h_layer_norm_rows(M, D, vp(X), ldx, vp(g1), vp(b1), vp(Y), ldy, None)
+
+    for call in (ln2, ln):
+        name = "p2h_layer_norm2_quant_rows" if call is ln2 else "p2h_layer_norm_rows"
+        rc = call(X + 4 * D * 3, D, D)          # Y starts at row 3 of X: overlaps rows 3..7
+        assert rc == -1 and "overlap" in P.last_error() and name in P.last_error(), (rc, P.last_error())
+        rc = call(X - 4 * D * 2, D, D)          # Y ends inside X's first rows
+        assert rc == -1 and "overlap" in P.last_error(), (rc, P.last_error())
+        rc = call(X, D, D + 16)                 # in place with another pitch
+        assert rc == -1 and "in place" in P.last_error(), (rc, P.last_error())
+    # the rows right after X do not overlap: the call passes those checks and stops at the next one (an invalid ldq)
+    rc = ln2(X + 4 * D * M, D, D, ldq=1000)
+    assert rc == -1 and "ldq" in P.last_error(), (rc, P.last_error())
