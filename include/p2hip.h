@@ -86,16 +86,19 @@ float p2h_event_elapsed_ms(void *start, void *stop);   /* < 0 on error */
 int   p2h_stream_hold(void *stream, unsigned usec);
 
 /* ── five-value weights ─────────────────────────────────────────────────────────────────────────────────────────
- *  A device-resident five-value weight [K, N] (blas.h:38-45 FiveValueB; phonon2.h:116-126 Weight): the sign and
- *  flag planes byte for byte as the reference stores them (signs [K][N/4], flags [K][N/8]), lo[N], hi[N], and the
- *  per-column epilogue tables derived from them on the device: clo[n] (blas.c:1319-1326), hi[n]/127
- *  (blas.c:1327-1328), lo[n] and hi[n]-lo[n] (blas.c:1329-1333). N % 16 == 0. */
+ *  A device-resident five-value weight [K, N] (blas.h:38-45 FiveValueB; phonon2.h:116-126 Weight), made from the
+ *  sign and flag planes as the reference stores them (signs [K][N/4], flags [K][N/8]) and lo[N], hi[N]: the 4-bit
+ *  selector records every kernel reads (half a byte per weight), lo and hi, and the per-column epilogue tables
+ *  derived on the device: clo[n] (blas.c:1319-1326), hi[n]/127 (blas.c:1327-1328), lo[n] and hi[n]-lo[n]
+ *  (blas.c:1329-1333). The planes themselves are not kept. N % 16 == 0. */
 typedef struct P2hWeight P2hWeight;
 
-/* Upload from host memory (an mmap of weights.bin, weights.c:300-312). Synchronous. NULL on failure. */
+/* Upload from host memory (an mmap of weights.bin, weights.c:300-312); the planes pass through a device staging
+ * buffer freed before the call returns. Synchronous. NULL on failure. */
 P2hWeight *p2h_fv_weight_upload(const unsigned char *signs, const unsigned char *flags, const float *lo,
                                 const float *hi, int K, int N);
-/* Wrap planes already in device memory (not copied; they must outlive the handle). Synchronous. */
+/* Make a weight from planes already in device memory: the records are built from them during the call, lo and hi
+ * are used in place (they must outlive the handle); the planes are not read again. Synchronous. */
 P2hWeight *p2h_fv_weight_wrap(const void *d_signs, const void *d_flags, const float *d_lo, const float *d_hi,
                               int K, int N);
 void   p2h_weight_free(P2hWeight *w);

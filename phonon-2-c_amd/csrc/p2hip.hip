@@ -177,10 +177,9 @@ inline bool rows_overlap(const float *dX, int ldx, const float *dY, int ldy, int
 
 struct P2hWeight {
     int K, N;
-    const uint8_t *signs, *flags;
+    const uint8_t *signs, *flags;   /* the planes, set only while the records and tables are made from them */
     const float *lo, *hi;
     uint8_t *clo;
-    float *c1w, *c2;
     uint8_t *rec4;    /* 4-bit selector records, the operand of every GEMM route (fv_repack4):
                          [N/16][units][64 lanes][16 B] */
     int units;        /* 128-row K units: K rounded up / 128 */
@@ -440,17 +439,12 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
         fail(P2H_E_ARG, "five-value weight: N = %d must be a positive multiple of 16 (K = %d)", N, K);
         return nullptr;
     }
-    size_t kn = (size_t)K * N;
-    size_t off_signs = 0, off_flags = 0, off_lo = 0, off_hi = 0, off = 0;
-    if (copy_planes) {
-        off_signs = off; off += align_up(kn / 4 ? kn / 4 : 1, 256);
-        off_flags = off; off += align_up(kn / 8 ? kn / 8 : 1, 256);
+    size_t off_lo = 0, off_hi = 0, off = 0;
+    if (copy_planes) {   /* lo and hi stay (the exact route reads them); the sign and flag planes do not */
         off_lo = off; off += align_up((size_t)N * 4, 256);
         off_hi = off; off += align_up((size_t)N * 4, 256);
     }
     size_t off_clo = off; off += align_up((size_t)N, 256);
-    size_t off_c1 = off; off += align_up((size_t)N * 4, 256);
-    size_t off_c2 = off; off += align_up((size_t)N * 4, 256);
     const int units = (K + 127) / 128;
     size_t off_rec4 = off; off += align_up((size_t)(N / 16) * units * 1024 + 16, 256);
     void *base = nullptr;
@@ -462,14 +456,10 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
     w->K = K; w->N = N;
     uint8_t *b = (uint8_t *)base;
     if (copy_planes) {
-        w->signs = b + off_signs;
-        w->flags = b + off_flags;
         w->lo = (const float *)(b + off_lo);
         w->hi = (const float *)(b + off_hi);
     }
     w->clo = b + off_clo;
-    w->c1w = (float *)(b + off_c1);
-    w->c2 = (float *)(b + off_c2);
     w->rec4 = b + off_rec4;
     w->units = units;
     w->own = base;
@@ -480,8 +470,7 @@ static P2hWeight *weight_new(int K, int N, bool copy_planes)
 static int weight_tables(P2hWeight *w)
 {
     hipStream_t s = stream_of(nullptr);
-    hipLaunchKernelGGL(p2k::fv_tables, dim3((w->N + 255) / 256), dim3(256), 0, s, w->N, w->lo, w->hi, w->clo,
-                       w->c1w, w->c2);
+    hipLaunchKernelGGL(p2k::fv_tables, dim3((w->N + 255) / 256), dim3(256), 0, s, w->N, w->lo, w->hi, w->clo);
     HIPCHK(hipGetLastError());
     const size_t recs = (size_t)(w->N / 16) * w->units * 64;
     if (recs > 0) {
@@ -503,14 +492,28 @@ P2hWeight *p2h_fv_weight_upload(const unsigned char *signs, const unsigned char 
     }
     P2hWeight *w = weight_new(K, N, true);
     if (!w) return nullptr;
+    /* the planes only pass through the device: a staging buffer the records and tables are made from, freed once
+     * they are (the device copy keeps 0.5 byte per weight, the records, against 0.875 with the planes kept) */
     size_t kn = (size_t)K * N;
+    const size_t sb = align_up(kn / 4 ? kn / 4 : 1, 256), fb = align_up(kn / 8 ? kn / 8 : 1, 256);
+    void *stage = nullptr;
+    if (hipMalloc(&stage, sb + fb) != hipSuccess) {
+        fail(P2H_E_NOMEM, "p2h_fv_weight_upload: hipMalloc(%zu) for the planes failed", sb + fb);
+        p2h_weight_free(w);
+        return nullptr;
+    }
+    w->signs = (const uint8_t *)stage;
+    w->flags = (const uint8_t *)stage + sb;
     hipStream_t s = stream_of(nullptr);
     bool ok = hipMemcpyAsync((void *)w->signs, signs, kn / 4, hipMemcpyHostToDevice, s) == hipSuccess &&
               hipMemcpyAsync((void *)w->flags, flags, kn / 8, hipMemcpyHostToDevice, s) == hipSuccess &&
               hipMemcpyAsync((void *)w->lo, lo, (size_t)N * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
               hipMemcpyAsync((void *)w->hi, hi, (size_t)N * 4, hipMemcpyHostToDevice, s) == hipSuccess;
-    if (!ok || weight_tables(w) != P2H_OK) {
-        if (!ok) fail(P2H_E_DEVICE, "p2h_fv_weight_upload: copy failed");
+    const int rc = ok ? weight_tables(w) : fail(P2H_E_DEVICE, "p2h_fv_weight_upload: copy failed");
+    if (!ok) (void)hipStreamSynchronize(s);   /* no copy may still read host memory or write the staging buffer */
+    (void)hipFree(stage);                      /* weight_tables synchronised: nothing reads the planes any more */
+    w->signs = w->flags = nullptr;
+    if (rc != P2H_OK) {
         p2h_weight_free(w);
         return nullptr;
     }
@@ -532,7 +535,9 @@ P2hWeight *p2h_fv_weight_wrap(const void *d_signs, const void *d_flags, const fl
     w->flags = (const uint8_t *)d_flags;
     w->lo = d_lo;
     w->hi = d_hi;
-    if (weight_tables(w) != P2H_OK) {
+    const int rc = weight_tables(w);
+    w->signs = w->flags = nullptr;   /* every kernel reads the records: the caller's planes are not needed again */
+    if (rc != P2H_OK) {
         p2h_weight_free(w);
         return nullptr;
     }
@@ -565,7 +570,7 @@ int p2h_fv_pack_codes(const P2hWeight *w, signed char *d_codes, void *stream)
     size_t total = (size_t)(w->N / 16) * (w->K / 4) * 16;
     if (total == 0) return P2H_OK;
     hipLaunchKernelGGL(p2k::fv_pack_codes, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream_of(stream),
-                       w->K, w->N, w->signs, w->flags, w->clo, (uint32_t *)d_codes);
+                       w->K, w->N, w->units, w->rec4, w->clo, (uint32_t *)d_codes);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -1270,10 +1275,10 @@ static int fvb_gemm_q8a(int mode, int M, int N, int K, float alpha, const signed
     const bool silu_here = silu && is_small(p.cfg);
     g.act = silu_here ? 1 : 0;
     if (mode == P2H_INT8W) {
-        g.c1 = w->c1w;
+        g.c1 = w->hi; g.c1_hi = 1;
         launch_fv_cfg<p2k::MODE_INT8W>(g, p, s);
     } else {
-        g.c1 = w->lo; g.c2 = w->c2;
+        g.c1 = w->lo; g.c2 = w->hi;
         launch_fv_cfg<p2k::MODE_INT8>(g, p, s);
     }
     HIPCHK(hipGetLastError());
@@ -1329,11 +1334,12 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
     memset(&ga, 0, sizeof ga);
     for (int q = 0; q < groups; q++) {
         ga.rec[q] = w[q]->rec4; ga.clo[q] = w[q]->clo; ga.C[q] = dC[q];
-        ga.c1[q] = mode == P2H_INT8W ? w[q]->c1w : w[q]->lo;
-        ga.c2[q] = w[q]->c2;
+        ga.c1[q] = mode == P2H_INT8W ? w[q]->hi : w[q]->lo;
+        ga.c2[q] = w[q]->hi;
         if (!aligned(dC[q], 16)) g.c_vec4 = 0;
     }
     g.units = w[0]->units;
+    g.c1_hi = mode == P2H_INT8W ? 1 : 0;
     /* the kernel of the plan's tile: the grid and g.tiles_n/tiles_m were sized for exactly that tile */
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n), (unsigned)groups);
     if (wide)
@@ -1473,7 +1479,7 @@ static int exact_gemm(int M, int N, int K, float alpha, const float *dA, int lda
     memset(&g, 0, sizeof g);
     g.M = M; g.N = N; g.K = K; g.alpha = alpha; g.beta = beta;
     g.A = dA; g.lda = lda;
-    g.signs = w->signs; g.flags = w->flags; g.lo = w->lo; g.hi = w->hi;
+    g.lo = w->lo; g.hi = w->hi;
     g.C = dC; g.ldc = ldc;
     g.rec = w->rec4; g.units = w->units;
     if (switch_of(g_sw.exact_chain) != 0 || K == 0) {

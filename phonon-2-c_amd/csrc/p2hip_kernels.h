@@ -45,10 +45,9 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 
 /* ── per-column tables ─────────────────────────────────────────────────────────────────────────────────────── */
 
-/* clo[n] = clamp(lrintf(127·lo/hi), 0, 127), 0 when hi <= 0 (blas.c:1319-1326); c1w[n] = hi·(1/127)
- * (blas.c:1327-1328); c2[n] = hi − lo (blas.c:1332). */
-__global__ void fv_tables(int N, const float *__restrict__ lo, const float *__restrict__ hi,
-                          uint8_t *__restrict__ clo, float *__restrict__ c1w, float *__restrict__ c2)
+/* clo[n] = clamp(lrintf(127·lo/hi), 0, 127), 0 when hi <= 0 (blas.c:1319-1326). The fold's other factors,
+ * hi·(1/127) and hi − lo (blas.c:1327-1333), are made from lo and hi where they are used (c1_factor, c2_factor). */
+__global__ void fv_tables(int N, const float *__restrict__ lo, const float *__restrict__ hi, uint8_t *__restrict__ clo)
 {
     int n = blockIdx.x * blockDim.x + threadIdx.x;
     if (n >= N) return;
@@ -59,8 +58,6 @@ __global__ void fv_tables(int N, const float *__restrict__ lo, const float *__re
         c = r < 0.0f ? 0 : r > 127.0f ? 127 : (int)r;
     }
     clo[n] = (uint8_t)c;
-    c1w[n] = h * (1.0f / 127.0f);
-    c2[n] = h - l;
 }
 
 /* ── activation quantisation ───────────────────────────────────────────────────────────────────────────────── */
@@ -1124,7 +1121,8 @@ struct GemmArgs {
     float alpha, beta;
     const int8_t *Q; int ldq; const float *a_scales;     /* quantised activations [M][ldq], row scales [M] */
     const uint8_t *signs; const uint8_t *flags;           /* five-value planes [K][N/4], [K][N/8] */
-    const uint8_t *clo; const float *c1; const float *c2; /* per-column epilogue tables */
+    const uint8_t *clo; const float *c1; const float *c2; /* per-column epilogue factors (c1_factor, c2_factor) */
+    int c1_hi;                                            /* 1: c1 holds hi, the factor is hi·(1/127) (int8w) */
     const int8_t *B8; int ldb;                            /* int8 table [K][ldb] (MODE_Q8B) */
     float *C; int ldc; int c_vec4;                        /* fp32 output; c_vec4: ldc % 4 == 0 and C 16-B aligned */
     int32_t *acc1; int32_t *acc2; int ldacc;              /* OUT_ACC: raw sums */
@@ -1139,6 +1137,16 @@ struct GemmArgs {
     const uint8_t *warm; int warm_lines;                  /* 128-byte lines a later kernel reads, loaded meanwhile */
     int act;                                              /* small-M tiles: 1 stores silu_p2 of each output */
 };
+
+/* The fold's per-column factors (blas.c:1316-1336), made from the weight's lo and hi as the reference makes them:
+ * int8w c1 = hi·(1/127) (c1 holds hi, c1_hi = 1); int8 two-plane c1 = lo (c1 holds lo) and c2 = hi − lo (c2 holds
+ * hi); the int8-table route's c1 is its column scale. */
+__device__ __forceinline__ float c1_factor(const GemmArgs &g, int n)
+{
+    const float v = g.c1[n];
+    return g.c1_hi ? v * (1.0f / 127.0f) : v;
+}
+__device__ __forceinline__ float c2_factor(const GemmArgs &g, int n) { return g.c2[n] - g.c1[n]; }
 
 
 
@@ -1312,8 +1320,8 @@ void gemm_i8(GemmArgs g)
     if (FOLD) {
         if (tid < G::BN) {
             const int n = min(n0 + tid, N - 1);
-            r_c1 = g.c1[n];
-            if (TWO) r_c2 = g.c2[n];
+            r_c1 = c1_factor(g, n);
+            if (TWO) r_c2 = c2_factor(g, n);
         }
         if (tid < G::BM) r_as = g.a_scales[min(m0 + tid, M - 1)] * g.alpha;
     }
@@ -1631,6 +1639,17 @@ __global__ void fv_repack4(int K, int N, int units, const uint8_t *__restrict__ 
     rec[idx] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+/* The selector nibble (code | flag << 2, fv_repack4's layout) of weight (k, n) lives in record (n / 16, k / 128),
+ * lane 16·((k % 64) / 16) + n % 16, dword 2·((k % 128) / 64) + (k % 16) / 8, byte k % 4, nibble ((k % 16) / 4) % 2;
+ * the four rows of a quad 4·q .. 4·q + 3 are the four bytes of one dword. This is that dword's byte offset in the
+ * records and the nibble's shift within each byte. */
+__device__ __forceinline__ size_t rec_quad_offset(int units, int k, int n, int &shift)
+{
+    const int u = k >> 7, s = (k >> 6) & 1, q = (k >> 4) & 3, d = (k >> 2) & 3;
+    shift = 4 * (d & 1);
+    return (((size_t)(n >> 4) * units + u) * 64 + 16 * q + (n & 15)) * 16 + 4 * (2 * s + (d >> 1));
+}
+
 template <int FM_, int FN_, int NW_, int D_>
 struct FvGeo {
     static constexpr int FM = FM_, FN = FN_, NW = NW_, D = D_;
@@ -1705,8 +1724,8 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
     if (FOLD) {
         if (tid < G::BN) {
             const int n = min(n0 + tid, N - 1);
-            r_c1 = g.c1[n];
-            if (TWO) r_c2 = g.c2[n];
+            r_c1 = c1_factor(g, n);
+            if (TWO) r_c2 = c2_factor(g, n);
         }
         if (tid < G::BM) r_as = g.a_scales[min(m0 + tid, M - 1)];
     }
@@ -2082,9 +2101,10 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     constexpr int RPP = G::NT / TPR;             /* rows per pass */
     constexpr int PASSES = (BM + RPP - 1) / RPP;
     const int cq = tid % TPR, n = n0 + 4 * cq, r0 = tid / TPR;
-    const v4f c1 = *reinterpret_cast<const v4f *>(g.c1 + min(n, N - 4));
+    v4f c1 = *reinterpret_cast<const v4f *>(g.c1 + min(n, N - 4));
     v4f c2 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if (TWO) c2 = *reinterpret_cast<const v4f *>(g.c2 + min(n, N - 4));
+    if (TWO) c2 = *reinterpret_cast<const v4f *>(g.c2 + min(n, N - 4)) - c1;   /* hi − lo */
+    if (g.c1_hi) c1 = c1 * (1.0f / 127.0f);                                      /* hi·(1/127) */
     float row_scale[PASSES];
 #pragma unroll
     for (int p = 0; p < PASSES; p++) row_scale[p] = g.a_scales[min(m0 + r0 + RPP * p, M - 1)];
@@ -2257,8 +2277,8 @@ __global__ __launch_bounds__(256) void fold_splits(GemmArgs g)
     float c1v[4], c2v[4] = {0, 0, 0, 0}, run[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        c1v[r] = g.c1[n + r];
-        if (TWO) c2v[r] = g.c2[n + r];
+        c1v[r] = c1_factor(g, n + r);
+        if (TWO) c2v[r] = c2_factor(g, n + r);
     }
     if (g.beta != 0.0f) {
 #pragma unroll
@@ -2351,15 +2371,19 @@ __global__ __launch_bounds__(256) void gemm_exact(ExactArgs g)
             ra[c] = g.alpha * v;
         }
         const int k = k0 + wk;
-        if (BKIND == EXB_FV) {
-            uint32_t s = 0x5555u, f = 0;
+        if (BKIND == EXB_FV) {   /* the 8 columns' selector nibbles of row k from the records (code 1 outside) */
+            uint32_t sel[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) sel[c] = 1u;
             if (wcol_ok && k < K) {
-                s = *reinterpret_cast<const uint16_t *>(g.signs + (size_t)k * (N / 4) + (n0 + wn) / 4);
-                f = g.flags[(size_t)k * (N / 8) + (n0 + wn) / 8];
+                int shift;
+                const uint8_t *rb = g.rec + rec_quad_offset(g.units, k & ~3, n0 + wn, shift) + (k & 3);
+#pragma unroll
+                for (int c = 0; c < 8; c++) sel[c] = (rb[16 * c] >> shift) & 7u;
             }
 #pragma unroll
             for (int c = 0; c < 8; c++) {
-                const int code = (s >> (2 * c)) & 3, fl = (f >> c) & 1;
+                const int code = (int)(sel[c] & 3u), fl = (int)(sel[c] >> 2);
                 rw[c] = (float)(code - 1) * __builtin_fmaf((float)fl, wd[c], wlo[c]);
             }
         } else {
@@ -2855,8 +2879,9 @@ __global__ __launch_bounds__(256, 3) void sgemm_f32(SgemmArgs g)
 /* ── small kernels ─────────────────────────────────────────────────────────────────────────────────────────── */
 
 /* One thread per (panel p, quad kq, column j): the dword of rows 4kq..4kq+3 at
- * out[((p·K/4 + kq)·16 + j)·4 ..] (vst4q_s8 order, blas.c:1229-1239). */
-__global__ void fv_pack_codes(int K, int N, const uint8_t *__restrict__ signs, const uint8_t *__restrict__ flags,
+ * out[((p·K/4 + kq)·16 + j)·4 ..] (vst4q_s8 order, blas.c:1229-1239), code = (code − 1)·(flag ? 127 : clo) as an
+ * int8 product (blas.c:1233-1236), from the weight's 4-bit records. */
+__global__ void fv_pack_codes(int K, int N, int units, const uint8_t *__restrict__ rec,
                               const uint8_t *__restrict__ clo, uint32_t *__restrict__ out)
 {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -2868,15 +2893,16 @@ __global__ void fv_pack_codes(int K, int N, const uint8_t *__restrict__ signs, c
     const int p = (int)(pk / (K / 4));
     const int n = 16 * p + j;
     const int cl = clo[n];
+    int shift;
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(rec + rec_quad_offset(units, 4 * kq, n, shift));
     uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int k = 4 * kq + i;
-        const int code = (signs[(size_t)k * (N / 4) + (n >> 2)] >> (2 * (n & 3))) & 3;
-        const int flag = (flags[(size_t)k * (N / 8) + (n >> 3)] >> (n & 7)) & 1;
-        const int s = code - 1;
-        const int mag = (flag && s != 0) ? 127 : cl;
-        word |= ((uint32_t)(s * mag) & 0xFFu) << (8 * i);
+        const uint32_t sel = (w >> (8 * i + shift)) & 7u;
+        const int code = (int)(sel & 3u), flag = (int)(sel >> 2);
+        const int sv = code - 1;
+        const int mag = (flag && sv != 0) ? 127 : cl;
+        word |= ((uint32_t)(sv * mag) & 0xFFu) << (8 * i);
     }
     out[idx] = word;
 }

@@ -301,6 +301,17 @@ class FvWeight:
         if not self.ptr:
             raise P2Error(f"p2h_fv_weight_upload: {last_error()}")
 
+    @classmethod
+    def wrap(cls, d_signs, d_flags, d_lo, d_hi, K, N, keep=()):
+        """A weight made from planes already in device memory (p2h_fv_weight_wrap); `keep` holds the device
+        buffers whose lo and hi the weight goes on using."""
+        self = cls.__new__(cls)
+        self.K, self.N, self._keep = K, N, tuple(keep)
+        self.ptr = hip().p2h_fv_weight_wrap(d_signs, d_flags, d_lo, d_hi, K, N)
+        if not self.ptr:
+            raise P2Error(f"p2h_fv_weight_wrap: {last_error()}")
+        return self
+
     def device_bytes(self):
         return hip().p2h_weight_device_bytes(self.ptr)
 

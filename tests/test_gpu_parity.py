@@ -209,6 +209,33 @@ def test_pack_codes_bit_exact(K, N):
     assert np.array_equal(P.fv_pack_codes(w), O.fv_pack_codes(signs, flags, lo, hi, K, N))
 
 
+@pytest.mark.parametrize("K,N", [(100, 48), (1024, 1024), (1024, 4096), (4096, 1024)])
+def test_weight_records_only(monkeypatch, K, N):
+    """A device weight keeps its 4-bit records, lo, hi and clo, not the planes: at most 0.51 byte per weight at the
+    encoder's shapes. Every route works from the records: the int8w and int8 GEMMs, the fmaf-chain exact route (bit
+    for bit the oracle's exact GEMM, which reads the planes), and the reference's packed codes (bit for bit the
+    oracle's p2_fv_pack_codes); a weight made from device planes (p2h_fv_weight_wrap) gives the same bits as one
+    uploaded from the host. K = 100 leaves rows 100..127 of the last unit as padding; code 3 is planted."""
+    signs, flags, lo, hi = _weight(K, N, 47 + K, code3=True)
+    up = P.FvWeight(signs, flags, lo, hi, K, N)
+    dev = [P.to_device(np.ascontiguousarray(x)) for x in (signs, flags, lo, hi)]
+    wr = P.FvWeight.wrap(*(d.ptr for d in dev), K, N, keep=dev)
+    if K >= 1024:
+        assert up.device_bytes() <= 0.51 * K * N, up.device_bytes() / (K * N)
+    A = P.gen_activations(SEED, 48 + K, 37, K)
+    for mode in ("int8w", "int8"):
+        got = P.fvb_gemm(mode, A, up)
+        _assert_fp32(got, O.sgemm_fvb(mode, A, signs, flags, lo, hi, N))
+        assert _bits_equal(got, P.fvb_gemm(mode, A, wr))
+    ref = O.sgemm_fvb("exact", A, signs, flags, lo, hi, N)
+    for w in (up, wr):
+        assert _bits_equal(_chain(monkeypatch, lambda: P.fvb_gemm("exact", A, w)), ref)
+        _assert_exact(P.fvb_gemm("exact", A, w), ref)
+    if K % 4 == 0:
+        packed = O.fv_pack_codes(signs, flags, lo, hi, K, N)
+        assert np.array_equal(P.fv_pack_codes(up), packed) and np.array_equal(P.fv_pack_codes(wr), packed)
+
+
 @pytest.mark.parametrize("mode", ["int8w", "exact"])
 @pytest.mark.parametrize("M,K,N,beta", [(11, 96, 32, 0.0), (375, 4096, 1024, 1.0), (3, 1030, 48, 0.0)])
 def test_q8b_parity(mode, M, K, N, beta):
