@@ -335,7 +335,11 @@ def engine_window(seconds=30.0, timeout=300):
     on this host's cores (encdump_cpu, exact: the x86 build's only GEMM route), and the same engine with its
     quantised GEMMs bound to this library (encdump_gpu: every linear crosses PCIe both ways, the attention and
     convolution steps stay on the CPU), int8w and exact. The first GPU-linked run moves the weights to the device;
-    the figure is the best of the runs after it."""
+    the figure is the best of the runs after it. With P2_CACHE_CODES=1 the engine's loader calls p2_cache_codes
+    (weights.c:525-529), whose p2_fv_pack_codes calls upload every weight at load, before the first window.
+    `*_breakdown`: for the best run, the library's own accounting (p2_gpu_stats_take) of the time inside its GEMM
+    entries (operand copies over PCIe and kernels), the weight uploads among it, the bytes moved each way, and the
+    rest of the window: the engine's CPU steps."""
     import re
     import subprocess
     import tempfile
@@ -350,10 +354,13 @@ def engine_window(seconds=30.0, timeout=300):
         model.write_model(os.path.join(d, "model"))
         wav = os.path.join(d, "a.wav")
         model.write_wav(wav, seconds, seed=5)
-        for name, exe, env_mode, repeat in (("encdump_cpu_exact_ms", exes["cpu"], {"P2_EXACT": "1"}, 2),
-                                            ("encdump_gpu_int8w_ms", exes["gpu"], {"P2_GEMM": "int8w"}, 4),
-                                            ("encdump_gpu_exact_ms", exes["gpu"], {"P2_EXACT": "1"}, 4)):
-            env = {k: v for k, v in os.environ.items() if k not in ("P2_GEMM", "P2_EXACT", "P2H_EXACT_CHAIN")}
+        for name, exe, env_mode, repeat in (
+                ("encdump_cpu_exact_ms", exes["cpu"], {"P2_EXACT": "1"}, 2),
+                ("encdump_gpu_int8w_ms", exes["gpu"], {"P2_GEMM": "int8w"}, 4),
+                ("encdump_gpu_int8w_cache_codes_ms", exes["gpu"], {"P2_GEMM": "int8w", "P2_CACHE_CODES": "1"}, 4),
+                ("encdump_gpu_exact_ms", exes["gpu"], {"P2_EXACT": "1"}, 4)):
+            env = {k: v for k, v in os.environ.items()
+                   if k not in ("P2_GEMM", "P2_EXACT", "P2H_EXACT_CHAIN", "P2_CACHE_CODES")}
             env.update(env_mode, P2_THREADS=str(cores), ENCDUMP_REPEAT=str(repeat))
             try:
                 r = subprocess.run([exe, os.path.join(d, "model"), wav, os.path.join(d, "out.f32")],
@@ -365,6 +372,24 @@ def engine_window(seconds=30.0, timeout=300):
             res[name] = round(min(ms[1:]), 2) if r.returncode == 0 and len(ms) > 1 else None
             if name.startswith("encdump_gpu") and len(ms) > 0:
                 res[name.replace("_ms", "_first_run_ms")] = round(ms[0], 2)
+            stats = [{k: float(v) for k, v in re.findall(r"(\w+) ([\d.]+)", line)}
+                     for line in re.findall(r"^gpu_stats (.*)$", r.stderr, re.M)]
+            load = re.findall(r"^gpu_stats_load upload_ms ([\d.]+)", r.stderr, re.M)
+            if r.returncode == 0 and len(stats) == len(ms) and len(ms) > 1:
+                best = 1 + int(np.argmin(ms[1:]))
+                st = stats[best]
+                gemm = st["fvb_ms"] + st["q8b_ms"] + st["sgemm_ms"]
+                res[name.replace("_ms", "_breakdown")] = {
+                    "window_ms": round(ms[best], 2), "gemm_entries_ms": round(gemm, 2),
+                    "of_which_upload_ms": round(st["upload_ms"], 2), "other_ms": round(ms[best] - gemm, 2),
+                    "fvb_calls": int(st["fvb_calls"]), "q8b_calls": int(st["q8b_calls"]),
+                    "sgemm_calls": int(st["sgemm_calls"]), "h2d_mb": round(st["h2d_mb"], 1),
+                    "d2h_mb": round(st["d2h_mb"], 1),
+                    "load_upload_ms": round(float(load[0]), 2) if load else None,
+                    "first_run": {"window_ms": round(ms[0], 2),
+                                  "gemm_entries_ms": round(stats[0]["fvb_ms"] + stats[0]["q8b_ms"] +
+                                                           stats[0]["sgemm_ms"], 2),
+                                  "of_which_upload_ms": round(stats[0]["upload_ms"], 2)}}
     return res
 
 

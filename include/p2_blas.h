@@ -91,6 +91,13 @@ void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const s
  * new ones at the same addresses call it in between; p2_free_weights, weights.c:578-580, is where). */
 void p2_gpu_weight_cache_clear(void);
 
+/* No counterpart in the reference: the calls made since the last take, then reset. out[0..8]: five-value GEMM calls
+ * (p2_sgemm_fvb, p2_sgemm_fvb_q8a) and ms inside them; int8-table calls and ms; fp32 p2_sgemm / p2_sgemm_st calls
+ * and ms; ms of those spent uploading weights on first touch; MB of operands copied host to device and device to
+ * host. The ms are summed over calling threads. For measuring what an engine window spends in the GEMMs. */
+#define P2_GPU_STATS_N 9
+void p2_gpu_stats_take(double out[P2_GPU_STATS_N]);
+
 #ifdef __cplusplus
 }
 #endif

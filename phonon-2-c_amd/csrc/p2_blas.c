@@ -7,10 +7,12 @@
 #include "p2hip.h"
 
 #include <pthread.h>
+#include <stdatomic.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* ── failure ───────────────────────────────────────────────────────────────────────────────────────────────── */
 
@@ -68,6 +70,39 @@ const char *p2_gemm_mode(void)
     case P2H_INT8W: return "int8 dot products, int8 weights";
     default:        return "fp32 expansion (exact)";
     }
+}
+
+/* ── call accounting (p2_gpu_stats_take) ───────────────────────────────────────────────────────────────────── */
+
+/* Nanoseconds inside each family of entries (summed over calling threads), the part of them spent uploading
+ * weights on first touch, and the operand bytes moved each way over PCIe. */
+enum { ST_FVB_CALLS, ST_FVB_NS, ST_Q8B_CALLS, ST_Q8B_NS, ST_SG_CALLS, ST_SG_NS, ST_UPLOAD_NS, ST_H2D, ST_D2H, ST_N };
+static _Atomic long long stats[ST_N];
+
+static long long now_ns(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (long long)ts.tv_sec * 1000000000ll + ts.tv_nsec;
+}
+
+static void stat_add(int k, long long v) { atomic_fetch_add_explicit(&stats[k], v, memory_order_relaxed); }
+
+static void stat_call(int calls, int ns, long long t0)
+{
+    stat_add(calls, 1);
+    stat_add(ns, now_ns() - t0);
+}
+
+void p2_gpu_stats_take(double out[P2_GPU_STATS_N])
+{
+    long long v[ST_N];
+    for (int k = 0; k < ST_N; k++) v[k] = atomic_exchange_explicit(&stats[k], 0, memory_order_relaxed);
+    out[0] = (double)v[ST_FVB_CALLS]; out[1] = v[ST_FVB_NS] * 1e-6;
+    out[2] = (double)v[ST_Q8B_CALLS]; out[3] = v[ST_Q8B_NS] * 1e-6;
+    out[4] = (double)v[ST_SG_CALLS];  out[5] = v[ST_SG_NS] * 1e-6;
+    out[6] = v[ST_UPLOAD_NS] * 1e-6;
+    out[7] = v[ST_H2D] * 1e-6;        out[8] = v[ST_D2H] * 1e-6;
 }
 
 /* ── device start-up ───────────────────────────────────────────────────────────────────────────────────────── */
@@ -150,6 +185,7 @@ static void *hgrow(Ctx *c, size_t need, const char *who)
  * hundred rows) */
 static void h2d_rows(Ctx *c, void *d, const void *h, size_t width, size_t pitch, size_t rows, const char *who)
 {
+    stat_add(ST_H2D, (long long)(rows * width));
     if (pitch == width) {
         check(p2h_memcpy_h2d(d, h, rows * width, c->stream), who);
         return;
@@ -335,8 +371,10 @@ static Entry *fv_weight(const FiveValueB *B, int K, int N)
     e = entry_new_locked(h, 0, B->signs, B->flags, B->lo, B->hi, K, N, 0, fp, "p2_sgemm_fvb");
     pthread_mutex_unlock(&cache_mu);
     free_list(to_free);
+    const long long t0 = now_ns();
     e->w = p2h_fv_weight_upload(B->signs, B->flags, B->lo, B->hi, K, N);
     if (!e->w) die("p2_sgemm_fvb: weight upload", p2h_last_error());
+    stat_add(ST_UPLOAD_NS, now_ns() - t0);
     entry_publish(e);
     return e;
 }
@@ -359,12 +397,14 @@ static Entry *q8_weight(const signed char *B, const float *scales, int ldb, int 
     e = entry_new_locked(h, 1, B, NULL, scales, NULL, K, N, ldb, fp, "p2_sgemm_q8b");
     pthread_mutex_unlock(&cache_mu);
     free_list(to_free);
+    const long long t0 = now_ns();
     e->dq8 = p2h_malloc((size_t)K * N + 16);
     e->dsc = (float *)p2h_malloc((size_t)N * sizeof(float));
     if (!e->dq8 || !e->dsc) die("p2_sgemm_q8b: weight upload", p2h_last_error());
     check(p2h_memcpy2d_h2d(e->dq8, (size_t)N, B, (size_t)ldb, (size_t)N, (size_t)K, stream), "p2_sgemm_q8b");
     check(p2h_memcpy_h2d(e->dsc, scales, (size_t)N * sizeof(float), stream), "p2_sgemm_q8b");
     check(p2h_stream_sync(stream), "p2_sgemm_q8b");
+    stat_add(ST_UPLOAD_NS, now_ns() - t0);
     entry_publish(e);
     return e;
 }
@@ -409,6 +449,7 @@ static float *stage_c(Ctx *c, const float *C, int M, int N, int ldc, int need_ol
 static void finish_c(Ctx *c, float *C, const float *dC, int M, int N, int ldc, const char *who)
 {
     const size_t width = (size_t)N * 4, rows = (size_t)M;
+    stat_add(ST_D2H, (long long)(rows * width));
     if (ldc == N) {
         check(p2h_memcpy_d2h(C, dC, rows * width, c->stream), who);
         check(p2h_stream_sync(c->stream), who);
@@ -449,7 +490,7 @@ static void int8_empty_k(Ctx *c, float *C, int M, int N, int ldc, float beta, co
 
 /* ── the five-value GEMMs ──────────────────────────────────────────────────────────────────────────────────── */
 
-void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, const FiveValueB *B, float beta,
+static void p2_sgemm_fvb_body(int M, int N, int K, float alpha, const float *A, int lda, const FiveValueB *B, float beta,
                   float *C, int ldc)
 {
     static const char who[] = "p2_sgemm_fvb";
@@ -467,6 +508,14 @@ void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, con
     check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, e->w, beta, dC, N, ws, wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
     entry_put(e);
+}
+
+void p2_sgemm_fvb(int M, int N, int K, float alpha, const float *A, int lda, const FiveValueB *B, float beta,
+                  float *C, int ldc)
+{
+    const long long t0 = now_ns();
+    p2_sgemm_fvb_body(M, N, K, alpha, A, lda, B, beta, C, ldc);
+    stat_call(ST_FVB_CALLS, ST_FVB_NS, t0);
 }
 
 int p2_quant_prepare(QuantA *qa, int M, int K)
@@ -499,7 +548,7 @@ void p2_quant_row(const QuantA *qa, int m, const float *row)
     memcpy((float *)(void *)qa->q + (size_t)m * qa->K, row, (size_t)qa->K * sizeof(float));
 }
 
-void p2_sgemm_fvb_q8a(int M, int N, int K, float alpha, const QuantA *A, const FiveValueB *B, float beta, float *C,
+static void p2_sgemm_fvb_q8a_body(int M, int N, int K, float alpha, const QuantA *A, const FiveValueB *B, float beta, float *C,
                       int ldc)
 {
     static const char who[] = "p2_sgemm_fvb_q8a";
@@ -519,6 +568,14 @@ void p2_sgemm_fvb_q8a(int M, int N, int K, float alpha, const QuantA *A, const F
     check(p2h_fvb_gemm(mode, M, N, K, alpha, dA, K, e->w, beta, dC, N, ws, wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
     entry_put(e);
+}
+
+void p2_sgemm_fvb_q8a(int M, int N, int K, float alpha, const QuantA *A, const FiveValueB *B, float beta, float *C,
+                      int ldc)
+{
+    const long long t0 = now_ns();
+    p2_sgemm_fvb_q8a_body(M, N, K, alpha, A, B, beta, C, ldc);
+    stat_call(ST_FVB_CALLS, ST_FVB_NS, t0);
 }
 
 signed char *p2_fv_pack_codes(const FiveValueB *b, int K, int N)
@@ -549,7 +606,7 @@ signed char *p2_fv_pack_codes(const FiveValueB *b, int K, int N)
 
 /* ── int8-table GEMMs ──────────────────────────────────────────────────────────────────────────────────────── */
 
-void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, const signed char *B,
+static void p2_sgemm_q8b_body(int M, int N, int K, float alpha, const float *A, int lda, const signed char *B,
                   const float *scales, int ldb, float beta, float *C, int ldc)
 {
     static const char who[] = "p2_sgemm_q8b";
@@ -570,7 +627,15 @@ void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, con
     entry_put(e);
 }
 
-void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const signed char *B, const float *scales,
+void p2_sgemm_q8b(int M, int N, int K, float alpha, const float *A, int lda, const signed char *B,
+                  const float *scales, int ldb, float beta, float *C, int ldc)
+{
+    const long long t0 = now_ns();
+    p2_sgemm_q8b_body(M, N, K, alpha, A, lda, B, scales, ldb, beta, C, ldc);
+    stat_call(ST_Q8B_CALLS, ST_Q8B_NS, t0);
+}
+
+static void p2_sgemm_q8b_q8a_body(int M, int N, int K, float alpha, const QuantA *A, const signed char *B, const float *scales,
                       int ldb, float beta, float *C, int ldc)
 {
     static const char who[] = "p2_sgemm_q8b_q8a";
@@ -591,10 +656,18 @@ void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const s
     entry_put(e);
 }
 
+void p2_sgemm_q8b_q8a(int M, int N, int K, float alpha, const QuantA *A, const signed char *B, const float *scales,
+                      int ldb, float beta, float *C, int ldc)
+{
+    const long long t0 = now_ns();
+    p2_sgemm_q8b_q8a_body(M, N, K, alpha, A, B, scales, ldb, beta, C, ldc);
+    stat_call(ST_Q8B_CALLS, ST_Q8B_NS, t0);
+}
+
 /* ── fp32 GEMM ─────────────────────────────────────────────────────────────────────────────────────────────── */
 
-static void sgemm_any(const char *who, P2Trans transA, P2Trans transB, int M, int N, int K, float alpha,
-                      const float *A, int lda, const float *B, int ldb, float beta, float *C, int ldc)
+static void sgemm_body(const char *who, P2Trans transA, P2Trans transB, int M, int N, int K, float alpha,
+                       const float *A, int lda, const float *B, int ldb, float beta, float *C, int ldc)
 {
     Ctx *c = ctx();
     if (M <= 0 || N <= 0) return;
@@ -607,6 +680,14 @@ static void sgemm_any(const char *who, P2Trans transA, P2Trans transB, int M, in
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     check(p2h_sgemm(tA, tB, M, N, K, alpha, dA, tA ? M : K, dB, tB ? K : N, beta, dC, N, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
+}
+
+static void sgemm_any(const char *who, P2Trans transA, P2Trans transB, int M, int N, int K, float alpha,
+                      const float *A, int lda, const float *B, int ldb, float beta, float *C, int ldc)
+{
+    const long long t0 = now_ns();
+    sgemm_body(who, transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    stat_call(ST_SG_CALLS, ST_SG_NS, t0);
 }
 
 void p2_sgemm(P2Trans transA, P2Trans transB, int M, int N, int K, float alpha, const float *A, int lda,

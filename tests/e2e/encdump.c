@@ -9,13 +9,18 @@
  *  token ids of p2_greedy_decode (phonon2.h:407) on stdout.
  *  ENCDUMP_REPEAT=n (default 1) runs p2_encoder n times on the same log-mel (the last run's frames are written) and
  *  prints the wall time of each run on stderr as "encoder_ms <ms>"; the first run of a GPU-linked build includes
- *  moving the weights to the device.
+ *  moving the weights to the device (unless P2_CACHE_CODES=1 moved them at load, weights.c:525-529). A GPU-linked
+ *  build also prints, per run, "gpu_stats ..." from the library's call accounting: the time inside its GEMM entries
+ *  (PCIe copies and kernels), the uploads among it, and the bytes copied each way.
  */
 #include "phonon2.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 #include <time.h>
+
+/* The GPU GEMM library's call accounting (include/p2_blas.h), present only in the GPU-linked builds. */
+void p2_gpu_stats_take(double out[9]) __attribute__((weak));
 
 static double now_ms(void)
 {
@@ -46,12 +51,24 @@ int main(int argc, char **argv)
     int T = 0;
     const char *rep = getenv("ENCDUMP_REPEAT");
     const int repeat = rep && atoi(rep) > 0 ? atoi(rep) : 1;
+    if (p2_gpu_stats_take) {   /* what loading did (the uploads of P2_CACHE_CODES=1) is not a run's */
+        double st[9];
+        p2_gpu_stats_take(st);
+        fprintf(stderr, "gpu_stats_load upload_ms %.3f\n", st[6]);
+    }
     for (int r = 0; r < repeat; r++) {
         free(enc);
         enc = NULL;
         const double t0 = now_ms();
         if (p2_encoder(m, mel, frames, &enc, &T) != 0) return 1;
         fprintf(stderr, "encoder_ms %.3f\n", now_ms() - t0);
+        if (p2_gpu_stats_take) {
+            double st[9];
+            p2_gpu_stats_take(st);
+            fprintf(stderr, "gpu_stats fvb_calls %.0f fvb_ms %.3f q8b_calls %.0f q8b_ms %.3f sgemm_calls %.0f "
+                            "sgemm_ms %.3f upload_ms %.3f h2d_mb %.3f d2h_mb %.3f\n",
+                    st[0], st[1], st[2], st[3], st[4], st[5], st[6], st[7], st[8]);
+        }
     }
     FILE *f = fopen(argv[3], "wb");
     if (!f || fwrite(enc, sizeof(float), (size_t)T * P2_JOINT_DIM, f) != (size_t)T * P2_JOINT_DIM) return 1;
