@@ -44,8 +44,8 @@ const char *p2h_last_error(void);
 const char *p2h_device_name(void);          /* gcnArchName of the device in use */
 int         p2h_device_cu_count(void);
 /* Re-read the tuning and comparison switches (P2H_TILE, P2H_SPLIT_ROWS, P2H_EXACT_CHAIN, P2H_XF_STAGED, P2H_XF_TILE,
- * P2H_SGEMM_ANY, P2H_ATTENTION_FUSED, P2H_SILU_EPILOGUE, P2H_EXACT_EPILOGUE, P2H_STACK_NORM_PAIRS) from the
- * environment. They are read once at initialisation; no launch reads the environment. No reference counterpart:
+ * P2H_SGEMM_ANY, P2H_ATTENTION_FUSED, P2H_SILU_EPILOGUE, P2H_EXACT_EPILOGUE, P2H_STACK_NORM_PAIRS,
+ * P2H_CONV_QUANT) from the environment. They are read once at initialisation; no launch reads the environment. No reference counterpart:
  * for tests and tuning runs that change a switch within one process. */
 int         p2h_reload_switches(void);
 
@@ -280,6 +280,13 @@ int p2h_glu_depthwise_conv_silu(int T, const float *dPW1, const float *dW, const
  * (encoder.c:554-568) would make for the pw2 linear; the same bits. */
 int p2h_glu_depthwise_conv_silu_rows(int T, const float *dPW1, const float *dW, const float *dB, float *dOut,
                                      void *stream);
+/* The int8 modes' form of the convolution module's middle (encoder.c:594-597 with channel_major_to_rows' QuantA
+ * branch, encoder.c:554-568): GLU, depthwise convolution and SiLU of pw1's rows [T][2048], quantised per output row
+ * into Q [roundup(T, 16)][ldq] (tiled as p2h_quant_rows stores it, pad rows and columns zero) and scales [T]: the
+ * bits of p2h_glu_depthwise_conv_silu_rows followed by p2h_quant_rows, in one kernel, with no fp32 rows written.
+ * No separate reference function: the reference runs these steps on the CPU between its linears. */
+int p2h_glu_depthwise_conv_silu_quant_rows(int T, const float *dPW1, const float *dW, const float *dB,
+                                           signed char *dQ, int ldq, float *dScales, void *stream);
 int p2h_silu(size_t n, float *dX, void *stream);
 int p2h_add_residual(int T, float *dX, const float *dY, float alpha, void *stream);
 int p2h_layer_norm_rows(int M, int D, const float *dX, int ldx, const float *dGamma, const float *dBeta, float *dY,

@@ -144,6 +144,8 @@ struct Switches {
     std::atomic<int> silu_epilogue{1};      /* P2H_SILU_EPILOGUE: 0 uses the SiLU→int8 producer in the block */
     std::atomic<int> exact_epilogue{1};     /* P2H_EXACT_EPILOGUE: 0 runs exact mode's residuals and SiLU apart */
     std::atomic<int> stack_norm_pairs{1};   /* P2H_STACK_NORM_PAIRS: 0 keeps the stack's LayerNorms unpaired */
+    std::atomic<int> conv_quant{1};         /* P2H_CONV_QUANT: 0 quantises the convolution's rows apart */
+    std::atomic<int> conv_tt{2};            /* P2H_CONV_TT: frames per workgroup of the quantising convolution */
 };
 Switches g_sw;
 
@@ -160,6 +162,8 @@ void load_switches()
     g_sw.silu_epilogue.store(env_int("P2H_SILU_EPILOGUE", 1), r);
     g_sw.exact_epilogue.store(env_int("P2H_EXACT_EPILOGUE", 1), r);
     g_sw.stack_norm_pairs.store(env_int("P2H_STACK_NORM_PAIRS", 1), r);
+    g_sw.conv_quant.store(env_int("P2H_CONV_QUANT", 1), r);
+    g_sw.conv_tt.store(env_int("P2H_CONV_TT", 2), r);
 }
 
 inline int switch_of(const std::atomic<int> &v) { return v.load(std::memory_order_relaxed); }
@@ -959,6 +963,31 @@ int p2h_glu_depthwise_conv_silu_rows(int T, const float *dPW1, const float *dW, 
     if (!dPW1 || !dW || !dB || !dOut) return fail(P2H_E_ARG, "p2h_glu_depthwise_conv_silu_rows: null pointer");
     hipLaunchKernelGGL(p2k::glu_dwconv_silu<true>, dim3((unsigned)((T + 31) / 32), p2k::kD / 16), dim3(256), 0,
                        stream_of(stream), T, dPW1, dW, dB, dOut);
+    HIPCHK(hipGetLastError());
+    return P2H_OK;
+}
+
+int p2h_glu_depthwise_conv_silu_quant_rows(int T, const float *dPW1, const float *dW, const float *dB,
+                                           signed char *dQ, int ldq, float *dScales, void *stream)
+{
+    if (int rc = ensure_init()) return rc;
+    const char *name = "p2h_glu_depthwise_conv_silu_quant_rows";
+    if (T < 0) return fail(P2H_E_ARG, "%s: T = %d", name, T);
+    if (T == 0) return P2H_OK;
+    if (!dPW1 || !dW || !dB || !dQ || !dScales) return fail(P2H_E_ARG, "%s: null pointer", name);
+    if (ldq < p2h_q_ld(p2k::kD) || ldq % P2H_Q_KALIGN != 0 || !aligned(dQ, 16))
+        return fail(P2H_E_ARG, "%s: ldq = %d must be >= %d and a multiple of %d, Q 16-byte aligned", name, ldq,
+                    p2h_q_ld(p2k::kD), P2H_Q_KALIGN);
+    const int tt = switch_of(g_sw.conv_tt);
+    hipStream_t s = stream_of(stream);
+    auto go = [&](auto kern, int TT) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)((T + TT - 1) / TT)), dim3(1024), 0, s, T, dPW1, dW, dB, (int8_t *)dQ,
+                           ldq, dScales);
+    };
+    if (tt == 1) go(p2k::glu_dwconv_silu_quant<1>, 1);
+    else if (tt == 2) go(p2k::glu_dwconv_silu_quant<2>, 2);
+    else if (tt == 4) go(p2k::glu_dwconv_silu_quant<4>, 4);
+    else go(p2k::glu_dwconv_silu_quant<8>, 8);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
@@ -1878,8 +1907,13 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
     /* conv_module (encoder.c:573-613) */
     P2H_TRY(layer_norm(blk->norm_conv_w, blk->norm_conv_b));
     P2H_TRY(linear(blk->pw1, D, 2 * D, 1.0f, 0.0f, w.ln, w.h));
-    /* the convolution's output as rows [T][1024] (channel_major_to_rows' transpose made by the kernel's stores) */
-    P2H_TRY(p2h_glu_depthwise_conv_silu_rows(T, w.h, blk->dw_w, blk->dw_b, w.dw, s));
+    /* the convolution's output as rows [T][1024] (channel_major_to_rows' transpose made by the kernel's stores); in
+     * the int8 modes quantised in the same kernel, with no fp32 rows written */
+    const bool conv_quant = mode != P2H_EXACT && switch_of(g_sw.conv_quant) != 0;
+    if (conv_quant)
+        P2H_TRY(p2h_glu_depthwise_conv_silu_quant_rows(T, w.h, blk->dw_w, blk->dw_b, w.q, ldD, w.sc, s));
+    else
+        P2H_TRY(p2h_glu_depthwise_conv_silu_rows(T, w.h, blk->dw_w, blk->dw_b, w.dw, s));
     if (mode == P2H_EXACT) {
         if (res_epilogue) {
             P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, w.dw, dX));
@@ -1888,7 +1922,7 @@ int run_block(int mode, const P2hBlock *blk, int T, const float *dPE, const floa
             P2H_TRY(p2h_add_residual(T, dX, w.out, 1.0f, s));
         }
     } else {
-        P2H_TRY(p2h_quant_rows(T, D, w.dw, D, w.q, ldD, w.sc, s));
+        if (!conv_quant) P2H_TRY(p2h_quant_rows(T, D, w.dw, D, w.q, ldD, w.sc, s));
         P2H_TRY(linear(blk->pw2, D, D, 1.0f, 1.0f, nullptr, dX));
     }
     P2H_TRY(feed_forward(blk->norm_ff2_w, blk->norm_ff2_b, blk->ff2_l1, blk->ff2_l2, false));

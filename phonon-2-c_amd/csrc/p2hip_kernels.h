@@ -1095,6 +1095,86 @@ __global__ __launch_bounds__(256) void glu_dwconv_silu(int T, const float *__res
     }
 }
 
+/* The convolution module's int8 form in one pass (encoder.c:594-597 and the QuantA branch of
+ * channel_major_to_rows, encoder.c:554-568): GLU, depthwise convolution, SiLU and the per-row quantisation of the
+ * output rows for pw2. A workgroup owns TT frames and all 1024 channels, one thread per channel: it makes the GLU of
+ * its channel for frames t0 − 4 .. t0 + TT + 3 in registers, runs dwconv_silu's fmadd chain for its TT outputs and
+ * writes them as rows to LDS; then one wave per row quantises it as quant_rows does (the row's 1024 values, 16 per
+ * lane, its maximum across the wave, the same rounding), into the tiled layout with its scale. Every value is made
+ * by the same operations as glu_dwconv_silu<true> followed by quant_rows, so the bits are theirs; neither the
+ * fp32 rows nor the gated buffer reach memory. The workgroup with the last frames also writes the zero rows up to
+ * the next multiple of 16. Grid ceil(T / TT). */
+template <int TT>
+__global__ __launch_bounds__(1024) void glu_dwconv_silu_quant(int T, const float *__restrict__ pw1,
+                                                              const float *__restrict__ w,
+                                                              const float *__restrict__ bias, int8_t *__restrict__ Q,
+                                                              int ldq, float *__restrict__ scales)
+{
+    constexpr int HALO = kConvK / 2, TW = TT + 2 * HALO;
+    static_assert(TT <= 16, "one wave per row: at most 16 rows per workgroup");
+    __shared__ __attribute__((aligned(16))) float y[TT][kD + 4];
+    const int d = threadIdx.x, t0 = blockIdx.x * TT;
+    float gv[TW];
+#pragma unroll
+    for (int i = 0; i < TW; i++) {
+        const int t = t0 - HALO + i;
+        float v = 0.0f;
+        if (t >= 0 && t < T) {
+            const float *row = pw1 + (size_t)t * 2 * kD;
+            const float g = row[kD + d];
+            v = __fdiv_rn(row[d], __fadd_rn(1.0f, expf(g < -87.0f ? 87.0f : -g)));
+        }
+        gv[i] = v;
+    }
+    float taps[kConvK];
+#pragma unroll
+    for (int k = 0; k < kConvK; k++) taps[k] = w[d * kConvK + k];
+    const float b = bias[d];
+#pragma unroll
+    for (int tl = 0; tl < TT; tl++) {
+        const int t = t0 + tl;
+        float v = b;
+#pragma unroll
+        for (int k = 0; k < kConvK; k++) {
+            const int src = t - HALO + k;
+            if (src >= 0 && src < T) v = __builtin_fmaf(gv[tl + k], taps[k], v);
+        }
+        y[tl][d] = silu_p2(v);
+    }
+    __syncthreads();
+    const int lane = d & 63, wave = d >> 6;
+    const int kst = ldq / 64;
+    if (wave < TT) {
+        const int m = t0 + wave;
+        if (m < T) {
+            float x[16];
+            const float4 *src = reinterpret_cast<const float4 *>(&y[wave][16 * lane]);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 v = src[c];
+                x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[e]));
+            amax = wave_max_dpp(amax);
+            const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / scale;
+            *reinterpret_cast<uint4 *>(Q + q_index(m, 16 * lane, kst)) = quant16(x, 16 * lane, kD, kD, scale, inv);
+            for (int k0 = kD + 16 * lane; k0 < ldq; k0 += 1024)   /* columns beyond the row: zeros */
+                *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
+            if (lane == 0) scales[m] = scale;
+        }
+    }
+    /* the pad rows T .. roundup(T, 16) − 1 of the last row group, by the workgroup holding frame T − 1 */
+    const int Mp = (T + 15) / 16 * 16;
+    if (t0 <= T - 1 && T - 1 < t0 + TT)
+        for (int i = d; i < (Mp - T) * (ldq / 16); i += 1024) {
+            const int m = T + i / (ldq / 16), k0 = 16 * (i % (ldq / 16));
+            *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
+        }
+}
+
 /* p2_swish on a flat array in place (tensor_ops.c:437-491): elements below the last multiple of eight as silu_p2,
  * the tail as x · p2_sigmoid(x) (expf clamped at 87, phonon2.h:38-46). */
 __global__ __launch_bounds__(256) void silu_flat(size_t n, float *__restrict__ x)

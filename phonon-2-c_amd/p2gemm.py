@@ -95,6 +95,7 @@ _HIP_SIG = {
     "p2h_attention_rows": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "p2h_glu_depthwise_conv_silu": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
     "p2h_glu_depthwise_conv_silu_rows": (_i, [_i, _vp, _vp, _vp, _vp, _vp]),
+    "p2h_glu_depthwise_conv_silu_quant_rows": (_i, [_i, _vp, _vp, _vp, _vp, _i, _vp, _vp]),
     "p2h_conformer_stack_workspace_bytes": (_sz, [_i, _i, _i]),
     "p2h_conformer_stack": (_i, [_i, _vp, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "p2h_glu_channel_major": (_i, [_i, _vp, _vp, _vp]),
@@ -693,6 +694,22 @@ def glu_depthwise_conv_silu(pw1, w, b, rows=False):
         return dO.download((T, D_MODEL), np.float32)
     _ok(hip().p2h_glu_depthwise_conv_silu(T, dP.ptr, dW.ptr, dB.ptr, dO.ptr, None), "p2h_glu_depthwise_conv_silu")
     return dO.download((D_MODEL, T), np.float32)
+
+
+def glu_depthwise_conv_silu_quant_rows(pw1, w, b, ldq=None):
+    """pw1 [T, 2048] → SiLU(depthwise conv(GLU(pw1))) rows quantised in the same kernel: (q untiled
+    [roundup(T, 16), ldq], scales [T]). Every byte of Q is preset, so its pads must be written."""
+    pw1 = _f32(pw1)
+    T = pw1.shape[0]
+    ldq = q_ld(D_MODEL) if ldq is None else ldq
+    nbytes = (T + 15) // 16 * 16 * ldq
+    dP, dW, dB = to_device(pw1), to_device(_f32(w)), to_device(_f32(b))
+    dQ = DeviceBuffer(max(nbytes, 16))
+    dQ.upload(np.full(max(nbytes, 16), 0x5A, np.uint8))
+    dS = DeviceBuffer(max(T, 1) * 4)
+    _ok(hip().p2h_glu_depthwise_conv_silu_quant_rows(T, dP.ptr, dW.ptr, dB.ptr, dQ.ptr, ldq, dS.ptr, None),
+        "p2h_glu_depthwise_conv_silu_quant_rows")
+    return q_untile(dQ.download((nbytes,), np.int8), T, ldq), dS.download((T,), np.float32)
 
 
 def silu(x):

@@ -197,6 +197,45 @@ def test_glu_depthwise_conv_silu_fused(T):
     assert np.array_equal(got.view(np.uint32), two.view(np.uint32))
 
 
+@pytest.mark.parametrize("T,ldq", [(375, 1024), (1, 1024), (4, 1024), (9, 1152), (17, 1024), (300, 1024),
+                                   (760, 1152)])
+def test_glu_depthwise_conv_silu_quant_rows(T, ldq):
+    """The int8 modes' convolution kernel (GLU, convolution, SiLU and the rows' quantisation in one pass) equals the
+    rows kernel followed by the plain quantiser bit for bit: codes, scales, zero pad rows up to the next multiple of
+    16 and zero columns beyond 1024; with the GLU's clamp values and a zero frame."""
+    print(f"glu_depthwise_conv_silu_quant_rows T={T} ldq={ldq}", flush=True)
+    rng = np.random.default_rng(SEED + 29 * T)
+    pw1 = (rng.standard_normal((T, 2 * D)) * 2).astype(np.float32)
+    pw1[0, D:D + 4] = [-100.0, 100.0, -87.5, 88.0]
+    if T > 3:
+        pw1[2] = 0.0
+    w = (rng.standard_normal((D, 9)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    q, s = P.glu_depthwise_conv_silu_quant_rows(pw1, w, b, ldq)
+    q_ref, s_ref = P.quant_rows(P.glu_depthwise_conv_silu(pw1, w, b, rows=True))
+    Mp = (T + 15) // 16 * 16
+    assert q.shape == (Mp, ldq)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q[:, :D], q_ref[:, :D])
+    assert not q[:, D:].any() and not q[T:].any()
+
+
+@pytest.mark.parametrize("mode", ["int8w", "int8"])
+def test_conv_quant_same_bits(monkeypatch, mode):
+    """The block with the convolution's rows quantised in the convolution kernel equals the block with the rows
+    kernel and the plain quantiser (P2H_CONV_QUANT=0) bit for bit."""
+    print(f"conv quant mode={mode}", flush=True)
+    sys.path.insert(0, HERE)
+    import refblock_child as RC
+    x, pe = RC.block_input(SEED, 375)
+    blk = _device_block(SEED)
+    fused = blk.run(mode, x, pe)
+    monkeypatch.setenv("P2H_CONV_QUANT", "0")
+    separate = blk.run(mode, x, pe)
+    assert np.isfinite(fused).all()
+    assert np.array_equal(fused.view(np.uint32), separate.view(np.uint32))
+
+
 @pytest.mark.parametrize("T", [375, 33, 32, 31, 1])
 def test_glu_depthwise_conv_silu_rows(T):
     """The row-major variant is the transpose of the channel-major output bit for bit, and its rows quantised by
