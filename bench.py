@@ -516,7 +516,11 @@ def gemm_roofline(M, K, N, ms, plan, a_bytes=1, kernel=None):
     mfma = {"achieved": round(tops, 1), "peak": PEAK_INT8_TOPS, "unit": "TOPS", "frac": round(tops / PEAK_INT8_TOPS, 4)}
     hbm = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}
     r = dict(hbm if bound == "hbm" else mfma)
-    r.update({"bound": bound, "traffic": measured_traffic(fake, plan) if a_bytes == 1 else None,
+    traffic = measured_traffic(fake, plan)
+    if a_bytes == 4 and traffic is not None:
+        q = measured_traffic(fake, "quant_rows")
+        traffic = traffic + q if q is not None else None
+    r.update({"bound": bound, "traffic": traffic,
               "kernel": kernel or f"{kernel_name(plan)}<int8w> M={M} K={K} N={N} ({plan})", "avg_ms": round(ms, 6),
               "ops": int(ops), "algorithmic_bytes": int(alg), "us_at_hbm_peak": round(t_hbm * 1e6, 2),
               "us_at_int8_peak": round(t_mfma * 1e6, 2), "pct_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
@@ -731,7 +735,8 @@ def sweep_kernels_eager(stream, reps=20):
 
 def measured_traffic(L, plan):
     """HBM bytes per launch of this GEMM from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    (profiles/gemm_fv_traffic.json), when they were taken for the same shape and plan; otherwise None."""
+    (profiles/gemm_fv_traffic.json), when they were taken for the same shape and plan; otherwise None. The plan
+    "quant_rows" names the row quantiser that feeds the GEMM on the fp32-input route (M rows of K)."""
     path = os.path.join(ROOT, "profiles", "gemm_fv_traffic.json")
     if not os.path.exists(path):
         return None

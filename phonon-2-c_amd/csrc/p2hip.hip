@@ -1061,15 +1061,33 @@ using FvWK = p2k::FvGeo<6, 2, 4, 2>;  /*  96 × 128, 2 stages: K > 1024, unsplit
 using SmS = p2k::SmGeo<2, 2>;         /*  32 ×  32 */
 using SmW = p2k::SmGeo<3, 4>;         /*  48 ×  64 (int8w) */
 using SmD = p2k::SmGeo<2, 4, 2, 8>;   /*  32 ×  64, eight waves of four units each, all in flight: K > 1024 (int8w) */
+/* Eight waves, one 128-row unit per load batch (int8w), for K > 1024: each wave's segment is four units, loaded one
+ * unit ahead of the MFMAs, and a wave holds a quarter of the operand registers of SmS/SmD's two-unit batches */
+using SmS8 = p2k::SmGeo<2, 2, 1, 8>;     /* 32 × 32 */
+using SmW8 = p2k::SmGeo<3, 2, 1, 8>;     /* 48 × 32 */
 enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_WK = 9,
-       FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_COUNT = 13 };
+       FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_SS8 = 13, FV_SW8 = 14, FV_COUNT = 15 };
+/* calls f(G{}) with the small-M geometry of an int8w-only configuration; false for any other configuration */
+template <class F>
+bool with_small_geo(int cfg, F &&f)
+{
+    switch (cfg) {
+    case FV_SW: f(SmW{}); return true;
+    case FV_SD: f(SmD{}); return true;
+    case FV_SS8: f(SmS8{}); return true;
+    case FV_SW8: f(SmW8{}); return true;
+    default: return false;
+    }
+}
 const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
-                             FvWK::BM, SmS::BM, SmW::BM, SmD::BM};
+                             FvWK::BM, SmS::BM, SmW::BM, SmD::BM, SmS8::BM, SmW8::BM};
 const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN, FvW6::BN,
-                             FvWK::BN, SmS::BN, SmW::BN, SmD::BN};
-/* gemm_fvs splits K among the four waves of a workgroup: at most four K segments, so K <= 4096 */
+                             FvWK::BN, SmS::BN, SmW::BN, SmD::BN, SmS8::BN, SmW8::BN};
+/* gemm_fvs splits K among the waves of a workgroup, one 1024-row fold block at most per segment, so K <= 4096 */
 inline bool small_ok(int K) { return K <= 4 * p2k::kFoldRows; }
-inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW || cfg == FV_SD; }
+inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW || cfg == FV_SD || cfg == FV_SS8 || cfg == FV_SW8; }
+/* the small tiles that exist for int8w only (the two-plane mode runs SmS in their place) */
+inline bool int8w_only(int cfg) { return cfg == FV_SW || cfg == FV_SD || cfg == FV_SS8 || cfg == FV_SW8; }
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -1095,9 +1113,17 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
          * CU, so only where those tiles fill the CUs in one round without leaving most of them idle */
         const int cus_ = g_cus > 0 ? g_cus : 256;
         const int sd_tiles = ((M + SmD::BM - 1) / SmD::BM) * ((N + SmD::BN - 1) / SmD::BN);
+        /* K > 1024 (int8w), measured at N = 1024, K = 4096 with the weights streamed from HBM: eight waves of one
+         * unit per batch win wherever their tiles fit the CUs in one round, 32 x 32 up to 256 rows (14 % faster at
+         * M = 250), 48 x 32 up to 384 (6 % at M = 375); beyond, 32 x 64 or 32 x 32 with four waves */
+        const int ss8_tiles = ((M + SmS8::BM - 1) / SmS8::BM) * ((N + SmS8::BN - 1) / SmS8::BN);
+        const int sw8_tiles = ((M + SmW8::BM - 1) / SmW8::BM) * ((N + SmW8::BN - 1) / SmW8::BN);
+        const bool deep = K > p2k::kFoldRows && mode == P2H_INT8W;
         cfg = !small_ok(K) ? FV_T
               : (K <= p2k::kFoldRows && N >= 3072 && M >= 256) ? FV_SW   /* measured: 32 x 32 wins up to N = 2048 */
-              : (K > p2k::kFoldRows && mode == P2H_INT8W && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
+              : (deep && ss8_tiles <= cus_) ? FV_SS8
+              : (deep && sw8_tiles <= cus_) ? FV_SW8
+              : (deep && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
               : FV_SS;
     }
     else
@@ -1105,7 +1131,7 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
     if (switch_of(g_sw.tile) != kUnset) cfg = switch_of(g_sw.tile);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
     if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_WK)) cfg = FV_L;
-    if (mode == P2H_INT8 && (cfg == FV_SW || cfg == FV_SD)) cfg = FV_SS;
+    if (mode == P2H_INT8 && int8w_only(cfg)) cfg = FV_SS;
     if (is_small(cfg) && !small_ok(K)) cfg = FV_T;
     /* these never split K across workgroups: the fold stays in the kernel */
     const bool large = cfg == FV_W6 || cfg == FV_WK || is_small(cfg);
@@ -1191,10 +1217,10 @@ void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     switch (p.cfg) {
     case FV_SS: launch_fvs<SmS, MODE>(g, p, s); break;
-    case FV_SW: if (MODE == p2k::MODE_INT8W) { launch_fvs<SmW, p2k::MODE_INT8W>(g, p, s); break; }
-                launch_fvs<SmS, MODE>(g, p, s); break;
-    case FV_SD: if (MODE == p2k::MODE_INT8W) { launch_fvs<SmD, p2k::MODE_INT8W>(g, p, s); break; }
-                launch_fvs<SmS, MODE>(g, p, s); break;
+    case FV_SW: case FV_SD: case FV_SS8: case FV_SW8:
+        if (MODE != p2k::MODE_INT8W) { launch_fvs<SmS, MODE>(g, p, s); break; }   /* make_plan maps int8 away */
+        with_small_geo(p.cfg, [&](auto geo) { launch_fvs<decltype(geo), p2k::MODE_INT8W>(g, p, s); });
+        break;
     case FV_T: launch_fv<FvT, MODE>(g, p, s); break;
     case FV_S: launch_fv<FvS, MODE>(g, p, s); break;
     case FV_M: launch_fv<FvM, MODE>(g, p, s); break;
@@ -1377,11 +1403,10 @@ int p2h_fvb_gemm_q8a_grouped(int mode, int M, int N, int K, float alpha, const s
         hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8>), grid, dim3(SmS::NT), 0, s, g, ga);
     else if (p.cfg == FV_SS)
         hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmS, p2k::MODE_INT8W>), grid, dim3(SmS::NT), 0, s, g, ga);
-    else if (p.cfg == FV_SW)
-        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmW, p2k::MODE_INT8W>), grid, dim3(SmW::NT), 0, s, g, ga);
-    else if (p.cfg == FV_SD)
-        hipLaunchKernelGGL((p2k::gemm_fvs_grouped<SmD, p2k::MODE_INT8W>), grid, dim3(SmD::NT), 0, s, g, ga);
-    else
+    else if (!with_small_geo(p.cfg, [&](auto geo) {
+                 using G = decltype(geo);
+                 hipLaunchKernelGGL((p2k::gemm_fvs_grouped<G, p2k::MODE_INT8W>), grid, dim3(G::NT), 0, s, g, ga);
+             }))
         return fail(P2H_E_ARG, "p2h_fvb_gemm_q8a_grouped: no grouped kernel for tile %d", p.cfg);
     HIPCHK(hipGetLastError());
     return P2H_OK;
