@@ -757,13 +757,15 @@ def exact_config(stream):
         w = P.FvWeight(signs, flags, lo, hi, K, N)
         dA = P.to_device(P.gen_activations(SEED, 78, M, K))
         dC = P.DeviceBuffer(M * N * 4)
-        if chain:
+        if chain:   # the library reads its switches once: reload them around the capture
             os.environ["P2H_EXACT_CHAIN"] = "1"
+            P.reload_switches()
         try:
             sg = StepGraphs(stream, lambda: P.fvb_gemm_dev("exact", M, N, K, 1.0, dA.ptr, K, w, 0.0, dC.ptr, N, None,
                                                            0, stream.ptr), STEPS_PER_REPLAY, reps)
         finally:
             os.environ.pop("P2H_EXACT_CHAIN", None)
+            P.reload_switches()
         ms, _ = sg.time(reps, 3)
         del sg
         tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
@@ -843,8 +845,9 @@ def ffn_module_config(stream, M=375, steps=2000, warmup=100, reps=200, graph=Tru
 def m38_rotated_config(stream, pairs=188, steps=20, warmup=3):
     """The 3 s utterance's FFN pair (M = 38: 1024 -> 4096, then 4096 -> 1024, int8w) over `pairs` independently seeded
     weight pairs chained one after another (pair r's up-projection reads pair r - 1's output): 188 pairs hold 602 MB
-    of packed planes (the reference's format) and 1.4 GB of device copies (planes, 4-bit records, column tables), far
-    beyond the 256 MB Infinity Cache, so the weights stream from HBM: the weight-streaming bound of the small-M path.
+    of packed planes (the reference's format) and 797 MB of device copies (4-bit records, lo, hi and the lo codes),
+    far beyond the 256 MB Infinity Cache, so the weights stream from HBM: the weight-streaming bound of the small-M
+    path.
     One graph replay runs all pairs; reported per pair,
     with GB/s on the packed planes (K·N·3/8 + 8N, the bytes the reference's format holds) and on the 4-bit operand
     records the kernels read (K·N/2 + 8N), against 8 TB/s."""
