@@ -22,39 +22,46 @@ D, FF, C, H, E, J = 1024, 4096, 256, 640, 640, 640
 N_BLOCKS, VOCAB, N_LOGITS, N_MELS, SUB = 24, 8193, 8198, 128, 8
 
 
-class _Writer:
-    def __init__(self, path):
-        self.f = open(path, "wb")
-        self.off = 0
-        self.entries = {}
+class _Container:
+    """The tensors of weights.bin and the manifest that locates them. Tensors are laid out first (each at the next
+    ALIGN boundary, the gaps zero) and written in one pass by save(); manifest entries carry the format's field
+    names (weights.c:433-511), so the reference's loader reads them unchanged."""
 
-    def _put(self, arr):
-        pad = (-self.off) % ALIGN
-        self.f.write(b"\0" * pad)
-        self.off += pad
-        off = self.off
-        data = np.ascontiguousarray(arr).tobytes()
-        self.f.write(data)
-        self.off += len(data)
-        return off
+    def __init__(self):
+        self.parts = []        # (offset, contiguous array) in file order
+        self.end = 0
+        self.manifest = {}
+
+    def _place(self, arr, dtype):
+        arr = np.ascontiguousarray(arr, dtype=dtype)
+        at = (self.end + ALIGN - 1) // ALIGN * ALIGN
+        self.parts.append((at, arr))
+        self.end = at + arr.nbytes
+        return at
+
+    def tensor(self, name, kind, shape, fields=(), **extra):
+        """One manifest entry: `fields` are (key, array, dtype) triples, each array placed and its offset stored."""
+        entry = {"dtype": kind, "shape": [int(d) for d in shape], **extra}
+        for key, arr, dtype in fields:
+            entry[key] = self._place(arr, dtype)
+        self.manifest[name] = entry
 
     def f32(self, name, arr):
-        arr = np.ascontiguousarray(arr, dtype=np.float32)
-        self.entries[name] = {"dtype": "float32", "shape": list(arr.shape), "numel": int(arr.size),
-                              "offset": self._put(arr)}
+        arr = np.asarray(arr, np.float32)
+        self.tensor(name, "float32", arr.shape, [("offset", arr, np.float32)], numel=int(arr.size))
 
     def i8(self, name, q, scales):
-        rows, cols = q.shape
-        self.entries[name] = {"dtype": "int8", "shape": [rows, cols], "offset": self._put(q.astype(np.int8)),
-                              "scales_offset": self._put(scales.astype(np.float32))}
+        self.tensor(name, "int8", q.shape, [("offset", q, np.int8), ("scales_offset", scales, np.float32)])
 
     def fv(self, name, signs, flags, lo, hi, K, N):
-        self.entries[name] = {"dtype": "five_value", "shape": [K, N], "signs_offset": self._put(signs),
-                              "flags_offset": self._put(flags), "lo_offset": self._put(lo.astype(np.float32)),
-                              "hi_offset": self._put(hi.astype(np.float32))}
+        self.tensor(name, "five_value", (K, N), [("signs_offset", signs, np.uint8), ("flags_offset", flags, np.uint8),
+                                                 ("lo_offset", lo, np.float32), ("hi_offset", hi, np.float32)])
 
-    def close(self):
-        self.f.close()
+    def save(self, path):
+        with open(path, "wb") as f:
+            for at, arr in self.parts:
+                f.write(b"\0" * (at - f.tell()))
+                f.write(arr.tobytes())
 
 
 def _fp16(x):
@@ -89,7 +96,7 @@ def write_model(out_dir, seed=7, bias=0.0, joint_gain=3.0, attn_scale=0.05):
     frame-to-frame variation the decoder sees)."""
     os.makedirs(out_dir, exist_ok=True)
     rng = np.random.default_rng(seed)
-    w = _Writer(os.path.join(out_dir, "weights.bin"))
+    w = _Container()
     n = lambda *shape, s=1.0: (rng.standard_normal(shape) * s).astype(np.float32)
     for layer in (0, 2, 5):
         w.f32(f"subsampling.conv.{layer}.weight", n(C, 9, s=0.3))
@@ -128,10 +135,10 @@ def write_model(out_dir, seed=7, bias=0.0, joint_gain=3.0, attn_scale=0.05):
     w.f32("decoder.decoder_projector.bias", n(J, s=0.05))
     w.i8("joint.head.weight", *_i8(rng, N_LOGITS, J, True, joint_gain))
     w.f32("joint.head.bias", n(N_LOGITS, s=0.1))
-    w.close()
-    w.entries["_meta"] = {"format": FORMAT, "converter": "tests/e2e/model.py (synthetic)"}
+    w.save(os.path.join(out_dir, "weights.bin"))
+    w.manifest["_meta"] = {"format": FORMAT, "converter": "tests/e2e/model.py (synthetic)"}
     with open(os.path.join(out_dir, "weights.json"), "w") as f:
-        json.dump(w.entries, f, indent=1)
+        json.dump(w.manifest, f, indent=1)
         f.write("\n")
     with open(os.path.join(out_dir, "tokens.txt"), "w", encoding="utf-8") as f:
         f.write("\n".join([f"▁t{i}" for i in range(VOCAB - 1)] + ["<blank>"]) + "\n")
