@@ -1065,8 +1065,14 @@ using SmD = p2k::SmGeo<2, 4, 2, 8>;   /*  32 ×  64, eight waves of four units e
  * unit ahead of the MFMAs, and a wave holds a quarter of the operand registers of SmS/SmD's two-unit batches */
 using SmS8 = p2k::SmGeo<2, 2, 1, 8>;     /* 32 × 32 */
 using SmW8 = p2k::SmGeo<3, 2, 1, 8>;     /* 48 × 32 */
+/* Sixteen-row tiles (int8w) for a few dozen rows: a workgroup reads 16 activation rows instead of 32 or 48, so at
+ * these M the tiles spread the rows and the weight columns over up to three times as many CUs, each reading less */
+using SmQ = p2k::SmGeo<1, 1>;             /* 16 × 16, four waves (K <= 1024) */
+using SmQ8 = p2k::SmGeo<1, 1, 1, 8>;      /* 16 × 16, eight waves (K > 1024) */
+using SmR8 = p2k::SmGeo<1, 2, 1, 8>;      /* 16 × 32, eight waves (K > 1024) */
 enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_WK = 9,
-       FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_SS8 = 13, FV_SW8 = 14, FV_COUNT = 15 };
+       FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_SS8 = 13, FV_SW8 = 14, FV_SQ = 15, FV_SQ8 = 16, FV_SR8 = 17,
+       FV_COUNT = 18 };
 /* calls f(G{}) with the small-M geometry of an int8w-only configuration; false for any other configuration */
 template <class F>
 bool with_small_geo(int cfg, F &&f)
@@ -1076,18 +1082,21 @@ bool with_small_geo(int cfg, F &&f)
     case FV_SD: f(SmD{}); return true;
     case FV_SS8: f(SmS8{}); return true;
     case FV_SW8: f(SmW8{}); return true;
+    case FV_SQ: f(SmQ{}); return true;
+    case FV_SQ8: f(SmQ8{}); return true;
+    case FV_SR8: f(SmR8{}); return true;
     default: return false;
     }
 }
 const int kFvBM[FV_COUNT] = {FvT::BM, FvS::BM, FvM::BM, FvL::BM, FvX::BM, FvT8::BM, FvS8::BM, FvT6::BM, FvW6::BM,
-                             FvWK::BM, SmS::BM, SmW::BM, SmD::BM, SmS8::BM, SmW8::BM};
+                             FvWK::BM, SmS::BM, SmW::BM, SmD::BM, SmS8::BM, SmW8::BM, SmQ::BM, SmQ8::BM, SmR8::BM};
 const int kFvBN[FV_COUNT] = {FvT::BN, FvS::BN, FvM::BN, FvL::BN, FvX::BN, FvT8::BN, FvS8::BN, FvT6::BN, FvW6::BN,
-                             FvWK::BN, SmS::BN, SmW::BN, SmD::BN, SmS8::BN, SmW8::BN};
+                             FvWK::BN, SmS::BN, SmW::BN, SmD::BN, SmS8::BN, SmW8::BN, SmQ::BN, SmQ8::BN, SmR8::BN};
 /* gemm_fvs splits K among the waves of a workgroup, one 1024-row fold block at most per segment, so K <= 4096 */
 inline bool small_ok(int K) { return K <= 4 * p2k::kFoldRows; }
-inline bool is_small(int cfg) { return cfg == FV_SS || cfg == FV_SW || cfg == FV_SD || cfg == FV_SS8 || cfg == FV_SW8; }
+inline bool is_small(int cfg) { return cfg >= FV_SS && cfg < FV_COUNT; }
 /* the small tiles that exist for int8w only (the two-plane mode runs SmS in their place) */
-inline bool int8w_only(int cfg) { return cfg == FV_SW || cfg == FV_SD || cfg == FV_SS8 || cfg == FV_SW8; }
+inline bool int8w_only(int cfg) { return cfg > FV_SS && cfg < FV_COUNT; }
 
 /* int8-table tiles (gemm_i8): activation rows × table columns, waves (m × n), K rows per LDS stage */
 using G64 = p2k::Geo<64, 64, 2, 2, 256>;
@@ -1116,13 +1125,19 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
         /* K > 1024 (int8w), measured at N = 1024, K = 4096 with the weights streamed from HBM: eight waves of one
          * unit per batch win wherever their tiles fit the CUs in one round, 32 x 32 up to 256 rows (14 % faster at
          * M = 250), 48 x 32 up to 384 (6 % at M = 375); beyond, 32 x 64 or 32 x 32 with four waves */
-        const int ss8_tiles = ((M + SmS8::BM - 1) / SmS8::BM) * ((N + SmS8::BN - 1) / SmS8::BN);
-        const int sw8_tiles = ((M + SmW8::BM - 1) / SmW8::BM) * ((N + SmW8::BN - 1) / SmW8::BN);
+        auto tiles_of = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
         const bool deep = K > p2k::kFoldRows && mode == P2H_INT8W;
+        const bool w8 = mode == P2H_INT8W;
+        /* and the sixteen-row tiles where they fit the CUs in one round, the four-wave ones two workgroups per CU
+         * (measured at M = 1 to 160 with the weights from HBM: the down-projection at M = 38 4.28 against
+         * 5.13 µs, 1024 -> 1024 2.96 against 3.36 µs, 1024 -> 2048 3.20 against 3.42 µs) */
         cfg = !small_ok(K) ? FV_T
+              : (deep && tiles_of(16, 16) <= cus_) ? FV_SQ8
+              : (deep && tiles_of(16, 32) <= cus_) ? FV_SR8
+              : (w8 && !deep && tiles_of(16, 16) <= 2 * cus_) ? FV_SQ
               : (K <= p2k::kFoldRows && N >= 3072 && M >= 256) ? FV_SW   /* measured: 32 x 32 wins up to N = 2048 */
-              : (deep && ss8_tiles <= cus_) ? FV_SS8
-              : (deep && sw8_tiles <= cus_) ? FV_SW8
+              : (deep && tiles_of(SmS8::BM, SmS8::BN) <= cus_) ? FV_SS8
+              : (deep && tiles_of(SmW8::BM, SmW8::BN) <= cus_) ? FV_SW8
               : (deep && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
               : FV_SS;
     }
@@ -1217,7 +1232,7 @@ void launch_fv_cfg(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     switch (p.cfg) {
     case FV_SS: launch_fvs<SmS, MODE>(g, p, s); break;
-    case FV_SW: case FV_SD: case FV_SS8: case FV_SW8:
+    case FV_SW: case FV_SD: case FV_SS8: case FV_SW8: case FV_SQ: case FV_SQ8: case FV_SR8:
         if (MODE != p2k::MODE_INT8W) { launch_fvs<SmS, MODE>(g, p, s); break; }   /* make_plan maps int8 away */
         with_small_geo(p.cfg, [&](auto geo) { launch_fvs<decltype(geo), p2k::MODE_INT8W>(g, p, s); });
         break;

@@ -486,7 +486,7 @@ def test_exact_staged_rows_match_register_path(monkeypatch, M, K, N, lda, ldc, t
 _TILE_CASES = {}
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 8, 9, 10, 11, 12, 13, 14])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17])
 @pytest.mark.parametrize("split_rows", [-1, 0, 256, 512, 1024])
 @pytest.mark.parametrize("M,K,N", [(375, 4096, 1024), (130, 1028, 272), (38, 1024, 4096), (300, 2048, 512)])
 def test_tiles_and_splits_int8w(monkeypatch, tile, split_rows, M, K, N):
@@ -506,13 +506,18 @@ def test_tiles_and_splits_int8w(monkeypatch, tile, split_rows, M, K, N):
         _assert_fp32(got, ref)
 
 
-@pytest.mark.parametrize("M,K,N,plan", [(9, 4096, 1024, "32x32"), (38, 4096, 1024, "32x32"), (250, 4096, 1024, "32x32"),
+@pytest.mark.parametrize("M,K,N,plan", [(9, 4096, 1024, "16x16"), (38, 4096, 1024, "16x16"), (100, 4096, 1024, "16x32"),
+                                         (160, 4096, 1024, "32x32"), (250, 4096, 1024, "32x32"),
                                          (320, 4096, 1024, "48x32"), (375, 4096, 1024, "48x32"),
-                                         (500, 4096, 1024, "32x64"), (130, 1028, 272, "32x32")])
-def test_deep_small_m_plans(M, K, N, plan):
-    """K > 1024 at small M: the planner's eight-wave tiles (32 x 32 while they fit the CUs in one round, then 48 x 32,
-    then the four- or eight-wave 32 x 64) on the weights of a down-projection, bit-exact against the oracle, as the
-    four-wave kernel is on the same inputs."""
+                                         (500, 4096, 1024, "32x64"), (130, 1028, 272, "16x16"),
+                                         (9, 1024, 4096, "16x16"), (38, 1024, 1024, "16x16"), (38, 1024, 4096, "32x32"),
+                                         (1, 1024, 1024, "16x16"), (17, 256, 48, "16x16"), (100, 1024, 1024, "16x16"),
+                                         (38, 1024, 3072, "32x32")])
+def test_small_m_plans(M, K, N, plan):
+    """The planner's small-M tiles where they fit the CUs in one round: sixteen rows (16 x 16, then 16 x 32 with eight
+    waves for K > 1024; 16 x 16 with four waves, two workgroups per CU, for K <= 1024), then for K > 1024 the
+    eight-wave 32 x 32 and 48 x 32, then the four- or eight-wave 32 x 64; each bit-exact against the oracle on a
+    down- or up-projection's weights."""
     assert P.plan("int8w", M, N, K).startswith(f"tile {plan},")
     signs, flags, lo, hi = _weight(K, N, 960 + M)
     w = P.FvWeight(signs, flags, lo, hi, K, N)
@@ -523,7 +528,7 @@ def test_deep_small_m_plans(M, K, N, plan):
     _assert_fp32(P.fvb_gemm_q8a("int8w", q, sc, w, alpha=-0.5, beta=1.0, C0=C0), ref)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 10, 13, 14])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 10, 13, 14, 15, 16, 17])
 @pytest.mark.parametrize("split_rows", [0, 256, 1024])
 def test_tiles_and_splits_int8(monkeypatch, tile, split_rows):
     monkeypatch.setenv("P2H_TILE", str(tile))
