@@ -1068,7 +1068,7 @@ using SmW8 = p2k::SmGeo<3, 2, 1, 8>;     /* 48 × 32 */
 /* Sixteen-row tiles (int8w) for a few dozen rows: a workgroup reads 16 activation rows instead of 32 or 48, so at
  * these M the tiles spread the rows and the weight columns over up to three times as many CUs, each reading less */
 using SmQ = p2k::SmGeo<1, 1>;             /* 16 × 16, four waves (K <= 1024) */
-using SmQ8 = p2k::SmGeo<1, 1, 1, 8>;      /* 16 × 16, eight waves (K > 1024) */
+using SmQ8 = p2k::SmGeo<1, 1, 4, 8>;      /* 16 × 16, eight waves (K > 1024), a segment's four units in one batch */
 using SmR8 = p2k::SmGeo<1, 2, 1, 8>;      /* 16 × 32, eight waves (K > 1024) */
 enum { FV_T = 0, FV_S = 1, FV_M = 2, FV_L = 3, FV_X = 4, FV_T8 = 5, FV_S8 = 6, FV_T6 = 7, FV_W6 = 8, FV_WK = 9,
        FV_SS = 10, FV_SW = 11, FV_SD = 12, FV_SS8 = 13, FV_SW8 = 14, FV_SQ = 15, FV_SQ8 = 16, FV_SR8 = 17,
