@@ -129,12 +129,12 @@ __device__ __forceinline__ void load16(const float *__restrict__ row, int k0, in
  * 16·(l + 64c); with NCH > 0 the row (ldq <= 1024·NCH) stays in registers between the row maximum and the
  * quantisation, with NCH == 0 it is read twice. scale = amax/127 (1 for amax == 0), inv = 1/scale. Rows M..Mp−1 and
  * columns K..ldq−1 are written as zeros. VEC: lda % 4 == 0 and A 16-byte aligned. */
-template <int NCH, bool VEC>
-__global__ __launch_bounds__(256) void quant_rows(int M, int Mp, int K, const float *__restrict__ A, int lda,
-                                                  int8_t *__restrict__ Q, int ldq, float *__restrict__ scales)
+template <int NCH, bool VEC, int RPW = 4>
+__global__ __launch_bounds__(64 * RPW) void quant_rows(int M, int Mp, int K, const float *__restrict__ A, int lda,
+                                                       int8_t *__restrict__ Q, int ldq, float *__restrict__ scales)
 {
     const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);   /* four rows per 256-thread workgroup */
+    const int m = blockIdx.x * RPW + (threadIdx.x >> 6);   /* RPW rows per workgroup of RPW waves */
     if (m >= Mp) return;
     const int kst = ldq / 64, k16 = K / 16 * 16;
     if (m >= M) {

@@ -78,8 +78,12 @@ def _bits_equal(a, b):
 
 # ── activation quantisation ─────────────────────────────────────────────────────────────────────────────────────
 
-@pytest.mark.parametrize("M,K", [(64, 1024), (7, 20), (300, 4096), (5, 4), (129, 1028)])
-def test_quant_rows_bit_exact(M, K):
+@pytest.mark.parametrize("rpw", ["0", "1", "4"])
+@pytest.mark.parametrize("M,K", [(64, 1024), (7, 20), (300, 4096), (5, 4), (129, 1028), (38, 4096), (193, 5000)])
+def test_quant_rows_bit_exact(monkeypatch, rpw, M, K):
+    """Every row configuration of the quantiser (P2H_QUANT_RPW: 0 the planner's, 1 or 4 rows per workgroup), with
+    the padding rows and columns zeroed."""
+    monkeypatch.setenv("P2H_QUANT_RPW", rpw)
     A = P.gen_activations(SEED, 100 + K, M, K)
     if M > 3:
         A[2] = 0.0   # a zero row: scale 1, q 0
