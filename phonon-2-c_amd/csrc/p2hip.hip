@@ -996,9 +996,9 @@ int p2h_glu_depthwise_conv_silu_quant_rows(int T, const float *dPW1, const float
                            ldq, dScales);
     };
     if (tt == 1) go(p2k::glu_dwconv_silu_quant<1>, 1);
-    else if (tt == 2) go(p2k::glu_dwconv_silu_quant<2>, 2);
     else if (tt == 4) go(p2k::glu_dwconv_silu_quant<4>, 4);
-    else go(p2k::glu_dwconv_silu_quant<8>, 8);
+    else if (tt == 8) go(p2k::glu_dwconv_silu_quant<8>, 8);
+    else go(p2k::glu_dwconv_silu_quant<2>, 2);   /* 2, the measured best, for any other value */
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }
