@@ -197,13 +197,16 @@ def test_glu_depthwise_conv_silu_fused(T):
     assert np.array_equal(got.view(np.uint32), two.view(np.uint32))
 
 
+@pytest.mark.parametrize("tt", ["1", "2", "4", "8"])
 @pytest.mark.parametrize("T,ldq", [(375, 1024), (1, 1024), (4, 1024), (9, 1152), (17, 1024), (300, 1024),
                                    (760, 1152)])
-def test_glu_depthwise_conv_silu_quant_rows(T, ldq):
-    """The int8 modes' convolution kernel (GLU, convolution, SiLU and the rows' quantisation in one pass) equals the
-    rows kernel followed by the plain quantiser bit for bit: codes, scales, zero pad rows up to the next multiple of
-    16 and zero columns beyond 1024; with the GLU's clamp values and a zero frame."""
-    print(f"glu_depthwise_conv_silu_quant_rows T={T} ldq={ldq}", flush=True)
+def test_glu_depthwise_conv_silu_quant_rows(monkeypatch, tt, T, ldq):
+    """The int8 modes' convolution kernel (GLU, convolution, SiLU and the rows' quantisation in one pass), at every
+    frames-per-workgroup setting (P2H_CONV_TT), equals the rows kernel followed by the plain quantiser bit for bit:
+    codes, scales, zero pad rows up to the next multiple of 16 and zero columns beyond 1024; with the GLU's clamp
+    values and a zero frame."""
+    monkeypatch.setenv("P2H_CONV_TT", tt)
+    print(f"glu_depthwise_conv_silu_quant_rows T={T} ldq={ldq} frames per workgroup {tt}", flush=True)
     rng = np.random.default_rng(SEED + 29 * T)
     pw1 = (rng.standard_normal((T, 2 * D)) * 2).astype(np.float32)
     pw1[0, D:D + 4] = [-100.0, 100.0, -87.5, 88.0]
