@@ -137,7 +137,8 @@ struct Switches {
     std::atomic<int> tile{kUnset};          /* P2H_TILE: force a five-value tile */
     std::atomic<int> split_rows{0};         /* P2H_SPLIT_ROWS: force a K split (-1: never) */
     std::atomic<int> xf_staged{1};          /* P2H_XF_STAGED: 0 loads the exact route's rows into registers */
-    std::atomic<int> xf_tile{0};            /* P2H_XF_TILE: force the exact route's tile width */
+    std::atomic<int> xf_tile{0};            /* P2H_XF_TILE: force the exact route's tile: 32 or 64 columns of 32 rows,
+                                               or 1616, 1632, 1664 for 16 rows of 16, 32, 64 columns */
     std::atomic<int> exact_chain{0};        /* P2H_EXACT_CHAIN: the exact route's per-output fmaf chain */
     std::atomic<int> sgemm_any{0};          /* P2H_SGEMM_ANY: the fp32 GEMM's element loads */
     std::atomic<int> attention_fused{1};    /* P2H_ATTENTION_FUSED: 0 runs the attention as separate products */
@@ -1494,27 +1495,38 @@ static int launch_exact(int bkind, const p2k::ExactArgs &g0, hipStream_t s)
 
 namespace {
 
-template <int FN>
+template <int FM, int FN>
 void launch_xf_tile(const p2k::ExactArgs &g, hipStream_t s)
 {
-    const dim3 grid((unsigned)((size_t)g.tiles_n * ((g.M + 31) / 32))), block(256);
+    const dim3 grid((unsigned)((size_t)g.tiles_n * ((g.M + 16 * FM - 1) / (16 * FM)))), block(256);
     const bool vec = g.K % 4 == 0 && g.lda % 4 == 0 && aligned(g.A, 16);
     const bool staged = vec && g.K % 128 == 0 && switch_of(g_sw.xf_staged) != 0;
-    if (staged) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true, true>), grid, block, 0, s, g);
-    else if (vec) hipLaunchKernelGGL((p2k::gemm_xf<2, FN, true>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((p2k::gemm_xf<2, FN, false>), grid, block, 0, s, g);
+    if (staged) hipLaunchKernelGGL((p2k::gemm_xf<FM, FN, true, true>), grid, block, 0, s, g);
+    else if (vec) hipLaunchKernelGGL((p2k::gemm_xf<FM, FN, true>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((p2k::gemm_xf<FM, FN, false>), grid, block, 0, s, g);
 }
 
 int launch_xf(const p2k::ExactArgs &g0, hipStream_t s)
 {
     p2k::ExactArgs g = g0;
-    const int cus = g_cus > 0 ? g_cus : 256;
-    int bn = ((size_t)((g.N + 63) / 64) * ((g.M + 31) / 32) >= (size_t)2 * cus) ? 64 : 32;
+    const long long cus = g_cus > 0 ? g_cus : 256;
+    /* measured at M = 38 to 749 (the weights from HBM, the same bits for every tile): 16 × 16 tiles while they
+     * number at most six per CU (M = 38, 4096 -> 1024: 13.3 against 27.2 µs; M = 375, 4096 -> 1024: 41.4 against
+     * 44.9 µs), then 32 × 64 where those fill three workgroups per CU, else 32 × 32 (M = 375, 1024 -> 3072: 29.6
+     * against 33.3 µs for 32 × 64) */
+    const long long t16 = (long long)((g.N + 15) / 16) * ((g.M + 15) / 16);
+    const long long t64 = (long long)((g.N + 63) / 64) * ((g.M + 31) / 32);
+    int bm = t16 <= 6 * cus ? 16 : 32;
+    int bn = bm == 16 ? 16 : (t64 >= 3 * cus ? 64 : 32);
     const int forced = switch_of(g_sw.xf_tile);
-    if (forced == 32 || forced == 64) bn = forced;
+    if (forced == 32 || forced == 64) { bm = 32; bn = forced; }
+    if (forced == 1616 || forced == 1632 || forced == 1664) { bm = 16; bn = forced - 1600; }
     g.tiles_n = (g.N + bn - 1) / bn;
-    if (bn == 64) launch_xf_tile<4>(g, s);
-    else launch_xf_tile<2>(g, s);
+    if (bm == 16 && bn == 16) launch_xf_tile<1, 1>(g, s);
+    else if (bm == 16 && bn == 32) launch_xf_tile<1, 2>(g, s);
+    else if (bm == 16) launch_xf_tile<1, 4>(g, s);
+    else if (bn == 64) launch_xf_tile<2, 4>(g, s);
+    else launch_xf_tile<2, 2>(g, s);
     HIPCHK(hipGetLastError());
     return P2H_OK;
 }

@@ -455,14 +455,31 @@ def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
     assert _bits_equal(got4, (got * np.float32(4.0)).astype(np.float32))
 
 
+@pytest.mark.parametrize("M,K,N", [(375, 4096, 1024), (38, 1024, 4096), (130, 1024, 208), (9, 4096, 64)])
+def test_exact_tiles_same_bits(monkeypatch, M, K, N):
+    """Every output of the exact route's matrix-core kernel is summed in the same order whatever the tile (each MFMA
+    step covers the same four K rows, and the waves' K segments meet in wave order), so all five tiles give the same
+    bits; the planner's choice among them is a matter of speed only."""
+    signs, flags, lo, hi = _weight(K, N, 940 + M + N)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 941 + M, M, K)
+    C0 = np.random.default_rng(M).standard_normal((M, N)).astype(np.float32)
+    base = P.fvb_gemm("exact", A, w, alpha=0.7, beta=1.0, C0=C0)
+    for tile in (32, 64, 1616, 1632, 1664):
+        monkeypatch.setenv("P2H_XF_TILE", str(tile))
+        assert _bits_equal(P.fvb_gemm("exact", A, w, alpha=0.7, beta=1.0, C0=C0), base), f"tile {tile}"
+
+
 @pytest.mark.parametrize("M,K,N,lda,ldc,tile", [
     (375, 1024, 4096, 1024, 4096, 0), (375, 4096, 1024, 4096, 1024, 0), (375, 1024, 1024, 1028, 1030, 0),
-    (749, 1024, 1024, 1024, 1024, 64), (37, 256, 64, 260, 64, 32), (1, 128, 48, 128, 50, 0), (130, 384, 208, 388, 211, 64)])
+    (749, 1024, 1024, 1024, 1024, 64), (37, 256, 64, 260, 64, 32), (1, 128, 48, 128, 50, 0), (130, 384, 208, 388, 211, 64),
+    (38, 4096, 1024, 4096, 1024, 1616), (75, 1024, 208, 1028, 211, 1632), (130, 384, 208, 388, 211, 1664)])
 def test_exact_staged_rows_match_register_path(monkeypatch, M, K, N, lda, ldc, tile):
     """gemm_xf's two ways of bringing the fp32 rows to the matrix cores (staged through LDS by direct loads where
     K % 128 == 0 and the rows allow 16-byte loads; into registers otherwise, P2H_XF_STAGED=0) run the same MFMAs in
     the same order: the outputs are equal bit for bit, with beta = 0, 1 and 0.3, strided A and C, a last row tile cut
-    short, and both tile widths; and within 1e-4 of the oracle's exact route."""
+    short, and every tile (32 rows of 32 or 64 columns, 16 rows of 16, 32 or 64); and within 1e-4 of the oracle's
+    exact route."""
     print(f"exact staged M={M} K={K} N={N} lda={lda} ldc={ldc} tile={tile}", flush=True)
     signs, flags, lo, hi = _weight(K, N, 930 + K + N)
     w = P.FvWeight(signs, flags, lo, hi, K, N)
