@@ -1125,29 +1125,29 @@ struct Plan {
 Plan make_plan(int mode, int M, int N, int K, bool can_split)
 {
     Plan p;
-    /* measured on MI355X: 32 × 64 tiles are the fastest up to a thousand rows; beyond, the two-workgroups-per-CU
-     * tiles on 4-bit records (int8w) or 128 × 128 (the two-plane mode needs twice the accumulators) */
     int cfg;
-    if (M <= 1024)   /* small M: the register-streaming kernel, 48 × 64 for wide outputs at a few hundred rows */
-    {
-        /* K > 1024 (int8w): eight waves of a 32 × 64 tile keep a whole segment's loads in flight, one workgroup per
-         * CU, so only where those tiles fill the CUs in one round without leaving most of them idle */
+    if (M <= 1024) {
+        /* Small M: the register-streaming kernel (gemm_fvs). Measured on MI355X with the weights from HBM:
+         *  - sixteen-row tiles while they fit the CUs in one round (K > 1024: eight waves, 16 × 16, then 16 × 32;
+         *    K <= 1024: four waves, two workgroups per CU): a workgroup then reads 16 activation rows instead of 32
+         *    or 48 (M = 38, 4096 -> 1024: 4.28 against 5.13 µs; 1024 -> 1024: 2.96 against 3.36 µs);
+         *  - K > 1024: eight waves of one unit per batch while their tiles fit in one round, 32 × 32 up to 256 rows
+         *    (14 % faster at M = 250), 48 × 32 up to 384 (6 % at M = 375); then the eight-wave 32 × 64, whose
+         *    segments' loads are all in flight, where those tiles fill between half and all of the CUs;
+         *  - K <= 1024: 48 × 64 for wide outputs at a few hundred rows (N >= 3072, M >= 256; 32 × 32 wins up to
+         *    N = 2048), else 32 × 32.
+         * Beyond a thousand rows: the two-workgroups-per-CU tiles on 4-bit records (int8w) or 128 × 128 (the
+         * two-plane mode needs twice the accumulators). */
         const int cus_ = g_cus > 0 ? g_cus : 256;
-        const int sd_tiles = ((M + SmD::BM - 1) / SmD::BM) * ((N + SmD::BN - 1) / SmD::BN);
-        /* K > 1024 (int8w), measured at N = 1024, K = 4096 with the weights streamed from HBM: eight waves of one
-         * unit per batch win wherever their tiles fit the CUs in one round, 32 x 32 up to 256 rows (14 % faster at
-         * M = 250), 48 x 32 up to 384 (6 % at M = 375); beyond, 32 x 64 or 32 x 32 with four waves */
         auto tiles_of = [&](int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+        const long long sd_tiles = tiles_of(SmD::BM, SmD::BN);
         const bool deep = K > p2k::kFoldRows && mode == P2H_INT8W;
         const bool w8 = mode == P2H_INT8W;
-        /* and the sixteen-row tiles where they fit the CUs in one round, the four-wave ones two workgroups per CU
-         * (measured at M = 1 to 160 with the weights from HBM: the down-projection at M = 38 4.28 against
-         * 5.13 µs, 1024 -> 1024 2.96 against 3.36 µs, 1024 -> 2048 3.20 against 3.42 µs) */
         cfg = !small_ok(K) ? FV_T
               : (deep && tiles_of(16, 16) <= cus_) ? FV_SQ8
               : (deep && tiles_of(16, 32) <= cus_) ? FV_SR8
               : (w8 && !deep && tiles_of(16, 16) <= 2 * cus_) ? FV_SQ
-              : (K <= p2k::kFoldRows && N >= 3072 && M >= 256) ? FV_SW   /* measured: 32 x 32 wins up to N = 2048 */
+              : (K <= p2k::kFoldRows && N >= 3072 && M >= 256) ? FV_SW
               : (deep && tiles_of(SmS8::BM, SmS8::BN) <= cus_) ? FV_SS8
               : (deep && tiles_of(SmW8::BM, SmW8::BN) <= cus_) ? FV_SW8
               : (deep && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
