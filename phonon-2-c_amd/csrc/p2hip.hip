@@ -148,6 +148,8 @@ struct Switches {
     std::atomic<int> conv_quant{1};         /* P2H_CONV_QUANT: 0 quantises the convolution's rows apart */
     std::atomic<int> conv_tt{2};            /* P2H_CONV_TT: frames per workgroup of the quantising convolution */
     std::atomic<int> quant_rpw{0};          /* P2H_QUANT_RPW: rows per workgroup of quant_rows (1 or 4; 0: by M) */
+    std::atomic<int> dev_scope_stores{1};   /* P2H_DEVICE_SCOPE_STORES: 0 stores the five-value GEMMs' C plainly,
+                                               to be written back from the L2s when the kernel ends */
 };
 Switches g_sw;
 
@@ -167,6 +169,7 @@ void load_switches()
     g_sw.conv_quant.store(env_int("P2H_CONV_QUANT", 1), r);
     g_sw.conv_tt.store(env_int("P2H_CONV_TT", 2), r);
     g_sw.quant_rpw.store(env_int("P2H_QUANT_RPW", 0), r);
+    g_sw.dev_scope_stores.store(env_int("P2H_DEVICE_SCOPE_STORES", 1), r);
 }
 
 inline int switch_of(const std::atomic<int> &v) { return v.load(std::memory_order_relaxed); }
@@ -1197,6 +1200,7 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
     g.ng_last = N / 16 - 1;
     g.C = dC; g.ldc = ldc;
     g.c_vec4 = dC && (ldc % 4 == 0) && aligned(dC, 16);
+    g.c_wt = switch_of(g_sw.dev_scope_stores) ? 1 : 0;
     g.tiles_n = p.tiles_n; g.tiles_m = p.tiles_m;
     g.splits = p.splits; g.split_rows = p.split_rows;
     if (p.splits > 1) g.part = (int32_t *)split_ws;

@@ -436,6 +436,30 @@ def test_large_m_every_output(M, K, N):
         assert np.isnan(got[:, N:]).all()
 
 
+@pytest.mark.parametrize("M,K,N", [(1100, 1024, 4096), (4099, 900, 2064), (375, 1024, 4096), (38, 4096, 1024)])
+def test_device_scope_stores_same_bits(monkeypatch, M, K, N):
+    """C stored at device scope (buffer stores over the tile's rows) and plainly: the same bits, on the large-M and
+    small-M tiles, into a C wider than N (ldc = N + 8) that beta = 1 accumulates into; nothing past column N is
+    written."""
+    signs, flags, lo, hi = _weight(K, N, 970 + M)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 971 + M, M, K)
+    q, sc = O.quant_rows(A)
+    C0 = P.gen_activations(SEED, 972 + M, M, N + 8)
+    C0[:, N:] = np.nan
+    print(f"device-scope stores M={M} K={K} N={N} plan={P.plan('int8w', M, N, K)}", flush=True)
+    got = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("P2H_DEVICE_SCOPE_STORES", flag)
+        got[flag] = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=0.5, beta=1.0, C0=C0)
+        assert np.isnan(got[flag][:, N:]).all()
+    assert _bits_equal(got["0"], got["1"])
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, min(M, 16), replace=False)]))
+    ref = O.gemm_i8_run("int8w", q[rows], sc[rows], signs, flags, lo, hi, N, alpha=0.5, C0=C0[rows, :N],
+                        beta_zero=False)
+    _assert_fp32(got["1"][rows, :N], ref)
+
+
 @pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024)])
 def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
     """The exact route at the batched long-audio shapes (16 windows stacked, 12k+ workgroups on the fp32 matrix
