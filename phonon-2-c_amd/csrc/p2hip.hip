@@ -150,6 +150,8 @@ struct Switches {
     std::atomic<int> quant_rpw{0};          /* P2H_QUANT_RPW: rows per workgroup of quant_rows (1 or 4; 0: by M) */
     std::atomic<int> dev_scope_stores{1};   /* P2H_DEVICE_SCOPE_STORES: 0 stores the five-value GEMMs' C plainly,
                                                to be written back from the L2s when the kernel ends */
+    std::atomic<int> records_in_regs{1};    /* P2H_RECORDS_IN_REGISTERS: 0 streams the large-M tiles' weight records
+                                               through the LDS ring with the activation rows (gemm_fv) */
 };
 Switches g_sw;
 
@@ -170,6 +172,7 @@ void load_switches()
     g_sw.conv_tt.store(env_int("P2H_CONV_TT", 2), r);
     g_sw.quant_rpw.store(env_int("P2H_QUANT_RPW", 0), r);
     g_sw.dev_scope_stores.store(env_int("P2H_DEVICE_SCOPE_STORES", 1), r);
+    g_sw.records_in_regs.store(env_int("P2H_RECORDS_IN_REGISTERS", 1), r);
 }
 
 inline int switch_of(const std::atomic<int> &v) { return v.load(std::memory_order_relaxed); }
@@ -1207,11 +1210,17 @@ p2k::GemmArgs gemm_args(int M, int N, int K, float alpha, float beta, const sign
     return g;
 }
 
-/* the large-M tiles: unsplit, two workgroups per CU, 4-bit records, staged output rows */
+/* the large-M tiles: unsplit, two workgroups per CU, 4-bit records (in registers, or through the LDS ring with the
+ * activation rows), staged output rows */
 template <class G>
 void launch_fv_large(const p2k::GemmArgs &g, const Plan &p, hipStream_t s)
 {
     const dim3 grid((unsigned)((size_t)p.tiles_m * p.tiles_n)), block(G::NT);
+    if (switch_of(g_sw.records_in_regs)) {
+        if (g.K > p2k::kFoldRows) hipLaunchKernelGGL((p2k::gemm_fv_rb<G, true>), grid, block, 0, s, g);
+        else hipLaunchKernelGGL((p2k::gemm_fv_rb<G, false>), grid, block, 0, s, g);
+        return;
+    }
     if (g.K > p2k::kFoldRows)
         hipLaunchKernelGGL((p2k::gemm_fv<G, p2k::MODE_INT8W, p2k::OUT_F32, true, false, 2, true>), grid, block, 0,
                            s, g);

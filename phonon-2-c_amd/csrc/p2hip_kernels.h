@@ -742,6 +742,16 @@ __device__ __forceinline__ void wait_vm()
     asm volatile("" ::: "memory");
 }
 
+/* A 16-byte load into registers, issued from inline assembly as dma_16 is: the caller waits for it explicitly
+ * (wait_vm) and then passes the registers through pin16, after which the compiler may read them. */
+__device__ __forceinline__ v4u load16_async(const void *src)
+{
+    v4u r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(src) : "memory");
+    return r;
+}
+__device__ __forceinline__ void pin16(v4u &r) { asm volatile("" : "+v"(r)); }
+
 /* this wave's LDS reads complete, then the workgroup barrier; no wait on vector memory */
 __device__ __forceinline__ void lds_barrier()
 {
@@ -2096,6 +2106,249 @@ __device__ __forceinline__ void fv_tile(const GemmArgs &g)
                 }
             }
     }
+}
+
+/* The large-M int8w tiles with the weight records in registers (gemm_fv_rb, the production large-M kernel).
+ *  As fv_tile, except that each wave loads its own FN weight records of stage t + 1 straight into registers while
+ *  stage t is computed (a wave is the only reader of its columns' records, so they need no LDS and no barrier), and
+ *  decodes step 0 of stage t + 1 among stage t's step-1 MFMAs: a stage starts on MFMAs as soon as its first
+ *  activation operands are read from LDS. Only the activation operands go through the LDS ring (direct loads, one
+ *  barrier per stage). Against the records in LDS: M = 1500 11.3 against 12.4 µs, M = 4099 24.8 against 27.1,
+ *  M = 6000 32.5 against 33.7 (1024 → 4096). Two workgroups per CU; the output is folded and staged as in
+ *  fv_tile (per 1024-row block, in order; C staged through LDS as whole row segments at device scope). */
+template <class G, bool MULTI>
+__device__ __forceinline__ void fv_tile_rb(const GemmArgs &g)
+{
+    constexpr int FM = G::FM, FN = G::FN, NW = G::NW, D = G::D, A_STAGE = G::A_STAGE, A_DMA = G::A_DMA;
+    constexpr int UNITS_PER_FOLD = kFoldRows / 128;
+    constexpr int SROW = G::BN + 4;                    /* staged C rows, padded */
+    constexpr int CJ = FM < 3 ? FM : 3;                /* row groups per staging chunk */
+    constexpr int RING = D * A_STAGE, STG = 16 * CJ * SROW * 4;
+    __shared__ __attribute__((aligned(16))) int8_t ring[RING > STG ? RING : STG];
+    __shared__ __attribute__((aligned(16))) float f_c1[G::BN], f_as[G::BM];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tile_n, tile_m, split;
+    tile_of(g, tile_n, tile_m, split);
+    const int n0 = tile_n * G::BN, m0 = tile_m * G::BM;
+    const int M = g.M, N = g.N;
+    const int nst = g.units;
+
+    /* sources of this lane (row and column groups clamped into the padded operands; their outputs are masked) */
+    const int8_t *a_src[A_DMA];
+    int a_dst[A_DMA];
+#pragma unroll
+    for (int q = 0; q < A_DMA; q++) {
+        const int f = wave + q * NW;               /* operand f = 2·j + s of the stage */
+        const int mg = min((m0 >> 4) + (f >> 1), g.mg_last);
+        a_src[q] = g.Q + ((size_t)mg * g.kst + (f & 1)) * 1024 + lane * 16;
+        a_dst[q] = f * 1024;
+    }
+    const uint8_t *b_src[FN];
+    uint32_t lo_tab[FN];
+#pragma unroll
+    for (int i = 0; i < FN; i++) {
+        const int cg = min((n0 >> 4) + wave * FN + i, g.ng_last);
+        b_src[i] = g.rec + (size_t)cg * g.units * 1024 + lane * 16;
+        lo_tab[i] = i8w_lo_table(g.clo[16 * cg + (lane & 15)]);
+    }
+    auto issue_a = [&](int t) __attribute__((always_inline)) {   /* stage t's activation operands → slot t % D */
+        int8_t *slot = ring + (t % D) * A_STAGE;
+#pragma unroll
+        for (int q = 0; q < A_DMA; q++) dma_16(a_src[q] + (size_t)t * 2048, slot + a_dst[q]);
+    };
+
+    /* epilogue factors first (so that waiting for them waits for nothing else), then stage 0 */
+    float r_c1 = 0.0f, r_as = 0.0f;
+    if (tid < G::BN) r_c1 = c1_factor(g, min(n0 + tid, N - 1));
+    if (tid < G::BM) r_as = g.a_scales[min(m0 + tid, M - 1)];
+    v4u rb0[FN], rb1[FN];
+#pragma unroll
+    for (int i = 0; i < FN; i++) rb0[i] = load16_async(b_src[i]);
+    issue_a(0);
+    if (tid < G::BN) f_c1[tid] = r_c1;
+    if (tid < G::BM) f_as[tid] = r_as * g.alpha;
+
+    auto decode = [&](auto step_tag, const v4u(&rb)[FN], v4i(&bw)[FN]) __attribute__((always_inline)) {
+        constexpr int S = decltype(step_tag)::value;
+#pragma unroll
+        for (int i = 0; i < FN; i++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const uint32_t sel = (rb[i][2 * S + (d >> 1)] >> (4 * (d & 1))) & 0x07070707u;
+                bw[i][d] = (int)perm(kI8wHiTable, lo_tab[i], sel);
+            }
+    };
+
+    v4i acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; i++)
+#pragma unroll
+        for (int j = 0; j < FM; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    const int n_lane = n0 + wave * 16 * FN + 4 * (lane >> 4);   /* outputs (m_lane + 16 j, n_lane + 16 i + r) */
+    const int m_lane = m0 + (lane & 15);
+    const bool beta_zero = g.beta == 0.0f;
+    float run[FN][FM][4];
+    int block = 0;
+    /* CASE 0: block 0 with beta 0 (f·as); 1: block 0 with beta-scaled C (fmaf(f, as, β·C)); 2: a later block */
+    auto fold_case = [&](auto case_tag) __attribute__((always_inline)) {
+        constexpr int CASE = decltype(case_tag)::value;
+#pragma unroll
+        for (int i = 0; i < FN; i++) {
+            const int nl = wave * 16 * FN + 16 * i + 4 * (lane >> 4);
+            const v4f c1 = *reinterpret_cast<const v4f *>(f_c1 + nl);
+            float cold[CASE == 1 ? FM : 1][4];
+            if (CASE == 1) {
+#pragma unroll
+                for (int j = 0; j < FM; j++) {
+                    const int n = min(n_lane + 16 * i, N - 4), m = min(m_lane + 16 * j, M - 1);
+                    const float *cp = g.C + (size_t)m * g.ldc + n;
+                    if (g.c_vec4) {
+                        const v4f v = *reinterpret_cast<const v4f *>(cp);
+                        cold[CASE == 1 ? j : 0][0] = v[0]; cold[CASE == 1 ? j : 0][1] = v[1];
+                        cold[CASE == 1 ? j : 0][2] = v[2]; cold[CASE == 1 ? j : 0][3] = v[3];
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[CASE == 1 ? j : 0][r] = cp[r];
+                    }
+                }
+                if (g.beta != 1.0f) {
+#pragma unroll
+                    for (int j = 0; j < FM; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) cold[CASE == 1 ? j : 0][r] = cold[CASE == 1 ? j : 0][r] * g.beta;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < FM; j++) {
+                const float as = f_as[16 * j + (lane & 15)];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float f = (float)acc[i][j][r] * c1[r];
+                    float &out = run[i][j][r];
+                    if (CASE == 0) out = f * as;
+                    else if (CASE == 1) out = __builtin_fmaf(f, as, cold[CASE == 1 ? j : 0][r]);
+                    else out = __builtin_fmaf(f, as, out);
+                }
+                acc[i][j] = v4i{0, 0, 0, 0};
+            }
+        }
+    };
+    auto fold = [&](int blk) __attribute__((always_inline)) {
+        if (blk > 0) fold_case(std::integral_constant<int, 2>{});
+        else if (beta_zero) fold_case(std::integral_constant<int, 0>{});
+        else fold_case(std::integral_constant<int, 1>{});
+    };
+
+    v4i bw0[FN], bw1[FN];
+    wait_vm<0>();
+#pragma unroll
+    for (int i = 0; i < FN; i++) pin16(rb0[i]);
+    decode(std::integral_constant<int, 0>{}, rb0, bw0);
+
+    /* stage t: its records in rc (step 0 already decoded into bw0); the next stage's records into rn */
+    auto stage = [&](int t, v4u(&rc)[FN], v4u(&rn)[FN]) __attribute__((always_inline)) {
+        wait_vm<0>();    /* this wave's loads of stage t (and the records of t + 1 decoded last stage) landed ... */
+        lds_barrier();   /* ... every wave's; every wave is also done reading the slot stage t + 1 reuses */
+        /* stage t + 1's records and activation operands; after the last stage, the last stage's again (in bounds,
+         * unused), so that the stage is straight-line code */
+        const int tn = min(t + 1, nst - 1);
+#pragma unroll
+        for (int i = 0; i < FN; i++) rn[i] = load16_async(b_src[i] + (size_t)tn * 1024);
+        {
+            int8_t *slot = ring + ((t + 1) % D) * A_STAGE;
+#pragma unroll
+            for (int q = 0; q < A_DMA; q++) dma_16(a_src[q] + (size_t)tn * 2048, slot + a_dst[q]);
+        }
+        const int8_t *sa = ring + (t % D) * A_STAGE;
+        v4i av[2][FM];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int j = 0; j < FM; j++)
+                av[s2][j] = *reinterpret_cast<const v4i *>(sa + (2 * j + s2) * 1024 + lane * 16);
+        /* step 0's MFMAs with step 1's decode among them ... */
+        decode(std::integral_constant<int, 1>{}, rc, bw1);
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+            for (int i = 0; i < FN; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw0[i], av[0][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * FM, 0);
+#pragma unroll
+        for (int x = 0; x < FM * FN; x++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, (FN * 10 + FM * FN - 1) / (FM * FN), 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        /* ... then step 1's, with the next stage's step-0 decode among them (its records have landed) */
+        wait_vm<0>();
+#pragma unroll
+        for (int i = 0; i < FN; i++) pin16(rn[i]);
+        decode(std::integral_constant<int, 0>{}, rn, bw0);
+#pragma unroll
+        for (int j = 0; j < FM; j++)
+#pragma unroll
+            for (int i = 0; i < FN; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw1[i], av[1][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int x = 0; x < FM * FN; x++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, (FN * 10 + FM * FN - 1) / (FM * FN), 0);
+        }
+#pragma unroll
+        for (int i = 0; i < FN; i++) asm volatile("" : "+v"(bw0[i]));   /* made here, not after the loop's branch */
+        if (MULTI && t + 1 < nst && (t + 1) % UNITS_PER_FOLD == 0) {
+            fold(block);
+            block++;
+        }
+    };
+    for (int t = 0; t < nst; t += 2) {
+        stage(t, rb0, rb1);
+        if (t + 1 < nst) stage(t + 1, rb1, rb0);
+    }
+    fold(block);
+
+    /* C staged through LDS (idle once the last stage is read) and stored as whole row segments at device scope */
+    constexpr int LPR = G::BN / 4;   /* lanes per staged row */
+    constexpr int RPI = 64 / LPR;    /* rows per store instruction */
+    static_assert(64 % LPR == 0, "row segments per wave");
+    float *stg = reinterpret_cast<float *>(ring);
+    const int lr = lane / LPR, lc = lane % LPR;
+    const DevScopeOut cout(g.C + (size_t)m0 * g.ldc, (size_t)min(G::BM, M - m0) * g.ldc * 4, g.c_wt);
+    lds_barrier();
+#pragma unroll
+    for (int j0 = 0; j0 < FM; j0 += CJ) {
+#pragma unroll
+        for (int j = j0; j < j0 + CJ && j < FM; j++)
+#pragma unroll
+            for (int i = 0; i < FN; i++) {
+                const int nl = wave * 16 * FN + 16 * i + 4 * (lane >> 4);
+                *reinterpret_cast<v4f *>(stg + (16 * (j - j0) + (lane & 15)) * SROW + nl) =
+                    v4f{run[i][j][0], run[i][j][1], run[i][j][2], run[i][j][3]};
+            }
+        lds_barrier();
+        const int rows = 16 * (min(j0 + CJ, FM) - j0);
+        for (int r = wave * RPI + lr; r < rows; r += NW * RPI) {
+            const int m = m0 + 16 * j0 + r, n = n0 + 4 * lc;
+            if (m < M && n < N) {
+                const v4f v = *reinterpret_cast<const v4f *>(stg + r * SROW + 4 * lc);
+                if (g.c_vec4) {
+                    cout.st16(((size_t)(m - m0) * g.ldc + n) * 4, v);
+                } else {
+                    float *cp = g.C + (size_t)m * g.ldc + n;
+                    cp[0] = v[0]; cp[1] = v[1]; cp[2] = v[2]; cp[3] = v[3];
+                }
+            }
+        }
+        if (j0 + CJ < FM) lds_barrier();
+    }
+}
+
+template <class G, bool MULTI>
+__global__ __launch_bounds__(G::NT, 2) void gemm_fv_rb(GemmArgs g)
+{
+    fv_tile_rb<G, MULTI>(g);
 }
 
 template <class G, int MODE, int OUT, bool MULTI, bool SPLIT, int OCC = 1, bool CSHUF = false>

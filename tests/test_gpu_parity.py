@@ -460,6 +460,34 @@ def test_device_scope_stores_same_bits(monkeypatch, M, K, N):
     _assert_fp32(got["1"][rows, :N], ref)
 
 
+@pytest.mark.parametrize("M,K,N,tile", [(1100, 1024, 4096, None), (4099, 900, 2064, None), (6000, 4096, 1024, None),
+                                         (375, 4096, 1024, "8"), (130, 1028, 272, "9"), (200, 2048, 512, "8")])
+def test_records_in_registers_same_bits(monkeypatch, M, K, N, tile):
+    """The large-M tiles with each wave's weight records loaded into registers (gemm_fv_rb) and through the LDS ring
+    (gemm_fv): the same bits, K below, at and above one 1024-row fold block, ragged M and N, beta 1 into a C wider
+    than N (ldc = N + 4); checked against the oracle on sampled rows."""
+    if tile is not None:
+        monkeypatch.setenv("P2H_TILE", tile)
+    plan = P.plan("int8w", M, N, K)
+    assert plan.startswith("tile 96x"), plan
+    signs, flags, lo, hi = _weight(K, N, 980 + M)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 981 + M, M, K)
+    q, sc = O.quant_rows(A)
+    C0 = P.gen_activations(SEED, 982 + M, M, N + 4)
+    print(f"records in registers M={M} K={K} N={N} plan={plan}", flush=True)
+    got = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("P2H_RECORDS_IN_REGISTERS", flag)
+        got[flag] = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=-0.75, beta=1.0, C0=C0)
+    assert _bits_equal(got["0"], got["1"])
+    assert _bits_equal(got["1"][:, N:], C0[:, N:])
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, min(M, 12), replace=False)]))
+    ref = O.gemm_i8_run("int8w", q[rows], sc[rows], signs, flags, lo, hi, N, alpha=-0.75, C0=C0[rows, :N],
+                        beta_zero=False)
+    _assert_fp32(got["1"][rows, :N], ref)
+
+
 @pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024)])
 def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
     """The exact route at the batched long-audio shapes (16 windows stacked, 12k+ workgroups on the fp32 matrix
