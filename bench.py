@@ -143,7 +143,7 @@ def time_launches(launch, stream, reps):
 
 
 def kernel_name(plan):
-    return "gemm_fvs" if "waves" in plan else "gemm_fv"
+    return "gemm_fvs" if "waves" in plan else "gemm_fv_rb" if "records in registers" in plan else "gemm_fv"
 
 
 # ── workloads ──────────────────────────────────────────────────────────────────────────────────────────────────
@@ -631,7 +631,8 @@ def main():
         # the p2_sgemm_fvb route the reference's bench_gemm and sgemm_i8 run: fp32 rows in, quantised per call
         roofline["fp32_in_route"] = gemm_roofline(
             M, K, N, ms_f, plan, a_bytes=4,
-            kernel=f"quant_rows + gemm_fv<int8w> M={M} K={K} N={N} (p2h_fvb_gemm: fp32 rows quantised in the step)")
+            kernel=f"quant_rows + {kernel_name(plan)}<int8w> M={M} K={K} N={N} "
+                   "(p2h_fvb_gemm: fp32 rows quantised in the step)")
         print(f"# gemm6000 fp32 in: {ms_f * 1e3:.2f} us/GEMM, "
               f"{roofline['fp32_in_route']['pct_int8_peak']:.1f} % of int8 peak", file=sys.stderr, flush=True)
         del gs

@@ -1295,9 +1295,11 @@ const char *p2h_fvb_plan(int mode, int M, int N, int K, int with_workspace)
         snprintf(buf, sizeof buf, "tile %dx%d, K split across the workgroup's waves, fold in LDS", kFvBM[p.cfg],
                  kFvBN[p.cfg]);
     else
-        snprintf(buf, sizeof buf, "tile %dx%d, %d split%s of %d rows%s", kFvBM[p.cfg], kFvBN[p.cfg], p.splits,
+        snprintf(buf, sizeof buf, "tile %dx%d, %d split%s of %d rows%s%s", kFvBM[p.cfg], kFvBN[p.cfg], p.splits,
                  p.splits > 1 ? "s" : "", p.split_rows,
-                 p.splits > 1 ? " + fold" : (K > p2k::kFoldRows ? ", folds in registers" : ""));
+                 p.splits > 1 ? " + fold" : (K > p2k::kFoldRows ? ", folds in registers" : ""),
+                 (p.cfg == FV_W6 || p.cfg == FV_WK) && mode != P2H_INT8 && switch_of(g_sw.records_in_regs)
+                     ? ", weight records in registers" : "");
     return buf;
 }
 

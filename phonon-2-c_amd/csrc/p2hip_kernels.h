@@ -47,14 +47,19 @@ struct DevScopeOut {
     {
         r = __builtin_amdgcn_make_buffer_rsrc(base_, 0, on ? (int)bytes : 0, 0x00020000);
     }
+    /* The whole offset is kept in the VGPR operand (soffset 0): a buffer store whose offset the compiler had split
+     * into an SGPR soffset missed its store-data hazard wait on gfx950 and wrote the next store's data. */
     template <class V>
     __device__ __forceinline__ void st16(size_t off, V v) const
     {
         static_assert(sizeof(V) == 16, "16-byte stores");
-        if (on)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, (int)off, 0, kStoreSc1);
-        else
+        if (on) {
+            int o = (int)off;
+            asm volatile("" : "+v"(o));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, o, 0, kStoreSc1);
+        } else {
             *reinterpret_cast<V *>(base + off) = v;
+        }
     }
 };
 
