@@ -1159,8 +1159,16 @@ Plan make_plan(int mode, int M, int N, int K, bool can_split)
               : (deep && 2 * sd_tiles >= cus_ && sd_tiles <= cus_) ? FV_SD
               : FV_SS;
     }
-    else
-        cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows ? FV_WK : FV_W6) : FV_L;
+    else {
+        /* int8w: 96 × 256 for K <= 1024 unless its tiles leave every CU one workgroup at most (a lone workgroup's K
+         * loop is no faster than a pair's), then 96 × 128, twice the workgroups: 1024 → 1024 at M = 6000 11.2–11.6
+         * against 12.3 µs, at M = 3000 7.8 against 11.0; 1024 → 4096 at M = 1500 10.8 against 12.1; 1024 → 3072 at
+         * M = 2000 11.0 against 12.2. With more tiles than CUs 96 × 256 wins or ties (M = 4099: 26.6 against 27.8 µs;
+         * 1024 → 2048 at M = 6000: 19.3 against 21.4; 1024 → 3072 at M = 4000: 18.7 against 20.6). */
+        const int cus_ = g_cus > 0 ? g_cus : 256;
+        const long long w6_tiles = (long long)((M + 95) / 96) * ((N + 255) / 256);
+        cfg = mode == P2H_INT8W ? (K > p2k::kFoldRows || w6_tiles <= cus_ ? FV_WK : FV_W6) : FV_L;
+    }
     if (switch_of(g_sw.tile) != kUnset) cfg = switch_of(g_sw.tile);
     if (cfg < 0 || cfg >= FV_COUNT) cfg = FV_S;
     if (mode == P2H_INT8 && (cfg == FV_X || cfg == FV_W6 || cfg == FV_WK)) cfg = FV_L;

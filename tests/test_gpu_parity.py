@@ -460,6 +460,26 @@ def test_device_scope_stores_same_bits(monkeypatch, M, K, N):
     _assert_fp32(got["1"][rows, :N], ref)
 
 
+@pytest.mark.parametrize("M,K,N,plan", [(6000, 1024, 4096, "96x256"), (3000, 1024, 4096, "96x256"),
+                                         (6000, 1024, 2048, "96x256"), (4099, 1024, 4096, "96x256"),
+                                         (6000, 1024, 1024, "96x128"), (3000, 1024, 1024, "96x128"),
+                                         (1500, 1024, 4096, "96x128"), (2000, 1024, 3072, "96x128"),
+                                         (6000, 4096, 1024, "96x128")])
+def test_large_m_plans(M, K, N, plan):
+    """The large-M tile: 96 × 256 for K <= 1024 while its tiles outnumber the CUs, else 96 × 128 (twice the
+    workgroups, so that no CU is left with one); 96 × 128 with the fold in registers for K > 1024. Where the plan is
+    96 × 128 at K <= 1024, sampled rows are checked against the oracle."""
+    assert P.plan("int8w", M, N, K).startswith(f"tile {plan},")
+    if plan == "96x128" and K <= 1024 and M * N <= 3000 * 1024:
+        signs, flags, lo, hi = _weight(K, N, 990 + M)
+        w = P.FvWeight(signs, flags, lo, hi, K, N)
+        A = P.gen_activations(SEED, 991 + M, M, K)
+        q, sc = O.quant_rows(A)
+        got = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=1.25)
+        rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 12, replace=False)]))
+        _assert_fp32(got[rows], O.gemm_i8_run("int8w", q[rows], sc[rows], signs, flags, lo, hi, N, alpha=1.25))
+
+
 @pytest.mark.parametrize("M,K,N,tile", [(1100, 1024, 4096, None), (4099, 900, 2064, None), (6000, 4096, 1024, None),
                                          (375, 4096, 1024, "8"), (130, 1028, 272, "9"), (200, 2048, 512, "8")])
 def test_records_in_registers_same_bits(monkeypatch, M, K, N, tile):
