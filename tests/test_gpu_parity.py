@@ -481,11 +481,17 @@ def test_large_m_plans(M, K, N, plan):
 
 
 @pytest.mark.parametrize("M,K,N,tile", [(1100, 1024, 4096, None), (4099, 900, 2064, None), (6000, 4096, 1024, None),
-                                         (375, 4096, 1024, "8"), (130, 1028, 272, "9"), (200, 2048, 512, "8")])
+                                         (375, 4096, 1024, "8"), (130, 1028, 272, "9"), (200, 2048, 512, "8"),
+                                         (1100, 640, 512, None), (2000, 384, 1040, "8"),
+                                         (1500, 1024, 1024, "8-odd-ldc")])
 def test_records_in_registers_same_bits(monkeypatch, M, K, N, tile):
     """The large-M tiles with each wave's weight records loaded into registers (gemm_fv_rb) and through the LDS ring
-    (gemm_fv): the same bits, K below, at and above one 1024-row fold block, ragged M and N, beta 1 into a C wider
-    than N (ldc = N + 4); checked against the oracle on sampled rows."""
+    (gemm_fv): the same bits, K below, at and above one 1024-row fold block, odd numbers of 128-row stages (K = 640,
+    384, 1028), ragged M and N, beta 1 into a C wider than N (ldc = N + 4); checked against the oracle on sampled
+    rows."""
+    pad = 4
+    if tile is not None and tile.endswith("-odd-ldc"):   # ldc = N + 3: rows not 16-byte aligned, element stores
+        tile, pad = tile[:-8], 3
     if tile is not None:
         monkeypatch.setenv("P2H_TILE", tile)
     plan = P.plan("int8w", M, N, K)
@@ -494,8 +500,8 @@ def test_records_in_registers_same_bits(monkeypatch, M, K, N, tile):
     w = P.FvWeight(signs, flags, lo, hi, K, N)
     A = P.gen_activations(SEED, 981 + M, M, K)
     q, sc = O.quant_rows(A)
-    C0 = P.gen_activations(SEED, 982 + M, M, N + 4)
-    print(f"records in registers M={M} K={K} N={N} plan={plan}", flush=True)
+    C0 = P.gen_activations(SEED, 982 + M, M, N + pad)
+    print(f"records in registers M={M} K={K} N={N} ldc={N + pad} plan={plan}", flush=True)
     got = {}
     for flag in ("0", "1"):
         monkeypatch.setenv("P2H_RECORDS_IN_REGISTERS", flag)
