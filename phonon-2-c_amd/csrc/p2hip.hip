@@ -147,7 +147,8 @@ struct Switches {
     std::atomic<int> stack_norm_pairs{1};   /* P2H_STACK_NORM_PAIRS: 0 keeps the stack's LayerNorms unpaired */
     std::atomic<int> conv_quant{1};         /* P2H_CONV_QUANT: 0 quantises the convolution's rows apart */
     std::atomic<int> conv_tt{2};            /* P2H_CONV_TT: frames per workgroup of the quantising convolution */
-    std::atomic<int> quant_rpw{0};          /* P2H_QUANT_RPW: rows per workgroup of quant_rows (1 or 4; 0: by M) */
+    std::atomic<int> quant_rpw{0};          /* P2H_QUANT_RPW: rows per workgroup of quant_rows (1 or 4), or −4 for
+                                               four waves per row (quant_rows_w4); 0: by M and K */
     std::atomic<int> dev_scope_stores{1};   /* P2H_DEVICE_SCOPE_STORES: 0 stores the five-value GEMMs' C plainly,
                                                to be written back from the L2s when the kernel ends */
     std::atomic<int> records_in_regs{1};    /* P2H_RECORDS_IN_REGISTERS: 0 streams the large-M tiles' weight records
@@ -616,6 +617,24 @@ int p2h_quant_rows(int M, int K, const float *dA, int lda, signed char *dQ, int 
     const int rpw = forced_rpw == 1 || forced_rpw == 4 ? forced_rpw : (Mp <= 192 ? 1 : 4);
     const dim3 grid((unsigned)((Mp + rpw - 1) / rpw)), block(64 * rpw);
     hipStream_t s = stream_of(stream);
+    /* four waves per row for a few long rows (K = 4096: M = 38 2.56 against 2.94 µs, M = 9 2.43 against 2.86, M = 250
+     * 3.38 against 3.62; at M = 375 one wave per row wins, 3.69 against 4.01, and at K = 1024 for every M); forced with
+     * P2H_QUANT_RPW = -4 */
+    const bool w4 = forced_rpw == -4 || (forced_rpw == 0 && Mp <= 256 && ldq >= 4096);
+    if (w4 && ldq <= 8192) {
+        auto launch4 = [&](auto nch_tag, auto vec_tag) {
+            hipLaunchKernelGGL((p2k::quant_rows_w4<decltype(nch_tag)::value, decltype(vec_tag)::value>),
+                               dim3((unsigned)Mp), dim3(256), 0, s, M, Mp, K, dA, lda, (int8_t *)dQ, ldq, dScales);
+        };
+        auto by_width4 = [&](auto vec_tag) {
+            if (ldq <= 4096) launch4(std::integral_constant<int, 1>{}, vec_tag);
+            else launch4(std::integral_constant<int, 2>{}, vec_tag);
+        };
+        if (vec_ok) by_width4(std::true_type{});
+        else by_width4(std::false_type{});
+        HIPCHK(hipGetLastError());
+        return P2H_OK;
+    }
     auto launch = [&](auto nch_tag, auto vec_tag) {
         constexpr int NCH = decltype(nch_tag)::value;
         constexpr bool VEC = decltype(vec_tag)::value;

@@ -215,6 +215,46 @@ __global__ __launch_bounds__(64 * RPW) void quant_rows(int M, int Mp, int K, con
     if (lane == 0) scales[m] = scale;
 }
 
+/* quant_rows with a workgroup of four waves per row, for a few long rows: each lane holds 16 · NCH values of
+ * K ≤ 4096·NCH (four times fewer than one wave per row would), the waves' maxima meet in LDS. The maximum is exact
+ * in any order, so the bits are quant_rows' own. */
+template <int NCH, bool VEC>
+__global__ __launch_bounds__(256) void quant_rows_w4(int M, int Mp, int K, const float *__restrict__ A, int lda,
+                                                     int8_t *__restrict__ Q, int ldq, float *__restrict__ scales)
+{
+    __shared__ float wmax[4];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int m = blockIdx.x;
+    if (m >= Mp) return;
+    const int kst = ldq / 64, k16 = K / 16 * 16;
+    if (m >= M) {
+        for (int k0 = 16 * t; k0 < ldq; k0 += 4096)
+            *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = make_uint4(0u, 0u, 0u, 0u);
+        return;
+    }
+    const float *row = A + (size_t)m * lda;
+    float x[NCH][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        load16<VEC>(row, 16 * (t + 256 * c), K, x[c]);
+#pragma unroll
+        for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(x[c][e]));
+    }
+    amax = wave_max_dpp(amax);
+    if (lane == 0) wmax[w] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / scale;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int k0 = 16 * (t + 256 * c);
+        if (k0 < ldq) *reinterpret_cast<uint4 *>(Q + q_index(m, k0, kst)) = quant16(x[c], k0, K, k16, scale, inv);
+    }
+    if (t == 0) scales[m] = scale;
+}
+
 /* ── producers: make a quantised linear's input rows and quantise them in one pass ────────────────────────────── */
 
 enum { PROD_SILU = 1, PROD_HEADS = 2, PROD_CMAJOR = 3, PROD_LN = 4 };

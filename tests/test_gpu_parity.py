@@ -78,11 +78,12 @@ def _bits_equal(a, b):
 
 # ── activation quantisation ─────────────────────────────────────────────────────────────────────────────────────
 
-@pytest.mark.parametrize("rpw", ["0", "1", "4"])
-@pytest.mark.parametrize("M,K", [(64, 1024), (7, 20), (300, 4096), (5, 4), (129, 1028), (38, 4096), (193, 5000)])
+@pytest.mark.parametrize("rpw", ["0", "1", "4", "-4"])
+@pytest.mark.parametrize("M,K", [(64, 1024), (7, 20), (300, 4096), (5, 4), (129, 1028), (38, 4096), (193, 5000),
+                                 (17, 8188)])
 def test_quant_rows_bit_exact(monkeypatch, rpw, M, K):
-    """Every row configuration of the quantiser (P2H_QUANT_RPW: 0 the planner's, 1 or 4 rows per workgroup), with
-    the padding rows and columns zeroed."""
+    """Every row configuration of the quantiser (P2H_QUANT_RPW: 0 the planner's, 1 or 4 rows per workgroup, −4 four
+    waves per row), with the padding rows and columns zeroed."""
     monkeypatch.setenv("P2H_QUANT_RPW", rpw)
     A = P.gen_activations(SEED, 100 + K, M, K)
     if M > 3:
