@@ -2197,10 +2197,11 @@ __device__ __forceinline__ void fv_tile_rb(const GemmArgs &g)
         b_src[i] = g.rec + (size_t)cg * g.units * 1024 + lane * 16;
         lo_tab[i] = i8w_lo_table(g.clo[16 * cg + (lane & 15)]);
     }
-    auto issue_a = [&](int t) __attribute__((always_inline)) {   /* stage t's activation operands → slot t % D */
+    /* stage t's slot (t % D) filled with stage ts's activation operands (ts = t but past the last stage) */
+    auto issue_a = [&](int t, int ts) __attribute__((always_inline)) {
         int8_t *slot = ring + (t % D) * A_STAGE;
 #pragma unroll
-        for (int q = 0; q < A_DMA; q++) dma_16(a_src[q] + (size_t)t * 2048, slot + a_dst[q]);
+        for (int q = 0; q < A_DMA; q++) dma_16(a_src[q] + (size_t)ts * 2048, slot + a_dst[q]);
     };
 
     /* epilogue factors first (so that waiting for them waits for nothing else), then stage 0 */
@@ -2210,7 +2211,8 @@ __device__ __forceinline__ void fv_tile_rb(const GemmArgs &g)
     v4u rb0[FN], rb1[FN];
 #pragma unroll
     for (int i = 0; i < FN; i++) rb0[i] = load16_async(b_src[i]);
-    issue_a(0);
+#pragma unroll
+    for (int t = 0; t < D - 1; t++) issue_a(t, min(t, nst - 1));
     if (tid < G::BN) f_c1[tid] = r_c1;
     if (tid < G::BM) f_as[tid] = r_as * g.alpha;
 
@@ -2292,19 +2294,17 @@ __device__ __forceinline__ void fv_tile_rb(const GemmArgs &g)
     decode(std::integral_constant<int, 0>{}, rb0, bw0);
 
     /* stage t: its records in rc (step 0 already decoded into bw0); the next stage's records into rn */
+    /* Loads retire in order: waiting until at most the youngest (D − 2) stages of activation loads are in flight
+     * leaves every older load landed. */
     auto stage = [&](int t, v4u(&rc)[FN], v4u(&rn)[FN]) __attribute__((always_inline)) {
-        wait_vm<0>();    /* this wave's loads of stage t (and the records of t + 1 decoded last stage) landed ... */
-        lds_barrier();   /* ... every wave's; every wave is also done reading the slot stage t + 1 reuses */
-        /* stage t + 1's records and activation operands; after the last stage, the last stage's again (in bounds,
-         * unused), so that the stage is straight-line code */
-        const int tn = min(t + 1, nst - 1);
+        wait_vm<(D - 2) * A_DMA>();   /* this wave's loads of stage t landed (the records of t + 1 too) ... */
+        lds_barrier();   /* ... every wave's; every wave is also done reading the slot stage t + D − 1 reuses */
+        /* stage t + 1's records and stage t + D − 1's activation operands; past the last stage, the last stage's
+         * again (in bounds, unused), so that the stage is straight-line code */
+        const int tn = min(t + 1, nst - 1), ta = min(t + D - 1, nst - 1);
 #pragma unroll
         for (int i = 0; i < FN; i++) rn[i] = load16_async(b_src[i] + (size_t)tn * 1024);
-        {
-            int8_t *slot = ring + ((t + 1) % D) * A_STAGE;
-#pragma unroll
-            for (int q = 0; q < A_DMA; q++) dma_16(a_src[q] + (size_t)tn * 2048, slot + a_dst[q]);
-        }
+        issue_a(t + D - 1, ta);
         const int8_t *sa = ring + (t % D) * A_STAGE;
         v4i av[2][FM];
 #pragma unroll
@@ -2327,7 +2327,7 @@ __device__ __forceinline__ void fv_tile_rb(const GemmArgs &g)
         }
         __builtin_amdgcn_sched_barrier(0);
         /* ... then step 1's, with the next stage's step-0 decode among them (its records have landed) */
-        wait_vm<0>();
+        wait_vm<(D - 2) * A_DMA>();
 #pragma unroll
         for (int i = 0; i < FN; i++) pin16(rn[i]);
         decode(std::integral_constant<int, 0>{}, rn, bw0);
