@@ -872,11 +872,13 @@ def m38_rotated_config(stream, pairs=188, steps=20, warmup=3):
 def block_config(stream, T=375, steps=500, warmup=50):
     """One conformer block's nine five-value linears as the encoder runs them in the int8 modes (encoder.c:333-613),
     every input made by its producer and every residual added in a GEMM epilogue, on the device and replayed from
-    one graph: LN→int8, ff1.linear1, SiLU→int8, ff1.linear2 (x += ½·), LN→int8, qkv, the positional projection
-    (its rows quantised once per window, so not in the block), heads→int8, out (x += ), LN→int8, pw1,
-    channel-major→int8, pw2 (x += ), LN→int8, ff2.linear1, SiLU→int8, ff2.linear2 (x += ½·). What lies between the
-    linears and is not on this path (attention scores and softmax, GLU, the depthwise convolution) is replaced by
-    fixed buffers of the right shapes: the heads [8, T, 128] and the channel-major conv output [1024, T]."""
+    one graph: LN→int8, ff1.linear1 with SiLU, int8, ff1.linear2 (x += ½·), LN→int8, qkv, the positional
+    projection (its rows quantised once per window, so not in the block), heads→int8, out (x += ), LN→int8, pw1,
+    channel-major→int8, pw2 (x += ), LN→int8, ff2.linear1 with SiLU, int8, ff2.linear2 (x += ½·). The feed-forward's
+    SiLU is applied as the up-projection stores its output and a plain quantiser follows, as p2h_conformer_block runs
+    it (the same bits as the SiLU→int8 producer after a plain GEMM). What lies between the linears and is not on this
+    path (attention scores and softmax, GLU, the depthwise convolution) is replaced by fixed buffers of the right
+    shapes: the heads [8, T, 128] and the channel-major conv output [1024, T]."""
     D, FF, H, Dh = 1024, 4096, 8, 128
     rng = np.random.default_rng(SEED + 9)
     x = P.to_device(P.gen_activations(SEED, 10_000 + D + T, T, D))
@@ -902,26 +904,27 @@ def block_config(stream, T=375, steps=500, warmup=50):
     def ln(i):
         P.layer_norm_quant_rows_dev(T, D, x.ptr, D, gb[i][0].ptr, gb[i][1].ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)
 
-    def silu(l):
-        P.silu_quant_rows_dev(T, FF, l.out.ptr, FF, ws.q.ptr, ldF, ws.s.ptr, stream.ptr)
+    def up_silu(l):   # SiLU as the up-projection stores, then the plain quantiser of its rows
+        P.fvb_gemm_q8a_silu_dev("int8w", T, l.N, l.K, 1.0, ws.q.ptr, ldD, ws.s.ptr, l.w, l.out.ptr, ws.ws.ptr,
+                                ws.ws.nbytes, stream.ptr)
+        P.quant_rows_dev(T, FF, l.out.ptr, FF, ws.q.ptr, ldF, ws.s.ptr, stream.ptr)
 
     def block():
-        ln(0); gemm(lin["ff1_l1"], ldD, 1.0, 0.0, lin["ff1_l1"].out.ptr)
-        silu(lin["ff1_l1"]); gemm(lin["ff1_l2"], ldF, 0.5, 1.0, x.ptr)
+        ln(0); up_silu(lin["ff1_l1"]); gemm(lin["ff1_l2"], ldF, 0.5, 1.0, x.ptr)
         ln(1); gemm(lin["qkv"], ldD, 1.0, 0.0, lin["qkv"].out.ptr)
         P.concat_heads_quant_rows_dev(H, T, Dh, heads.ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)
         gemm(lin["out"], ldD, 1.0, 1.0, x.ptr)
         ln(2); gemm(lin["pw1"], ldD, 1.0, 0.0, lin["pw1"].out.ptr)
         P.channel_major_quant_rows_dev(D, T, cm.ptr, ws.q.ptr, ldD, ws.s.ptr, stream.ptr)
         gemm(lin["pw2"], ldD, 1.0, 1.0, x.ptr)
-        ln(3); gemm(lin["ff2_l1"], ldD, 1.0, 0.0, lin["ff2_l1"].out.ptr)
-        silu(lin["ff2_l1"]); gemm(lin["ff2_l2"], ldF, 0.5, 1.0, x.ptr)
+        ln(3); up_silu(lin["ff2_l1"]); gemm(lin["ff2_l2"], ldF, 0.5, 1.0, x.ptr)
 
     ms, _ = StepGraphs(stream, block, STEPS_PER_REPLAY, steps).time(steps, warmup)
     ops = sum(gemm_ops(T, l.N, l.K) for l in lin.values())
     return {"ms_per_block": round(ms, 6), "ms_per_30s_window_24_blocks": round(24 * ms, 4),
             "tops": round(ops / (ms * 1e-3) / 1e12, 2), "kernels_per_block": 16,
-            "what": f"T={T}: 8 producers + 8 five-value GEMMs (int8w), residuals in the epilogues"}
+            "what": f"T={T}: 8 producers + 8 five-value GEMMs (int8w), residuals and the feed-forward's SiLU in the "
+                    "epilogues"}
 
 
 def conformer_block_config(stream, T=375, steps=200, warmup=20, graph=True):

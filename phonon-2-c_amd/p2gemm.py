@@ -411,6 +411,12 @@ def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=Non
                                ws_bytes, stream), "p2h_fvb_gemm_q8a")
 
 
+def fvb_gemm_q8a_silu_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, dC, ws=None, ws_bytes=0, stream=None):
+    """SiLU(alpha·A·W) into dC [M, N] (ldc = N): the feed-forward up-projection with SiLU applied as C is stored."""
+    _ok(hip().p2h_fvb_gemm_q8a_silu(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, dC, ws, ws_bytes,
+                                    stream), "p2h_fvb_gemm_q8a_silu")
+
+
 def fvb_gemm_q8a_next_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=None, ws_bytes=0, next_w=None,
                           stream=None):
     """fvb_gemm_q8a_dev that also reads the records of `next_w` (the next weight the caller runs) ahead."""
