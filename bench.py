@@ -675,6 +675,7 @@ def main():
             _, rr = run(name, specs[name](), steps, 20, kreps)
             extra[name] = rr
         extra["exact375"] = exact_config(stream)
+        extra["q8b375"] = q8b_config(stream)
         if not args.no_sweep:
             extra["sweep_exact"] = exact_sweep_config(stream)
         extra["attention375"] = attention_config(stream)
@@ -771,6 +772,36 @@ def exact_config(stream):
         del sg
         tf = gemm_ops(M, N, K) / (ms * 1e-3) / 1e12
         out[name] = {"ms": round(ms, 5), "tflops": round(tf, 2), "pct_fp32_peak": round(100 * tf / PEAK_FP32_TFLOPS, 2)}
+    return out
+
+
+def q8b_config(stream, T=375, reps=500):
+    """The encoder's two int8-table linears (p2_sgemm_q8b: one int8 plane with a per-column fp32 scale) at a 30 s
+    window's T = 375 frames: the subsampling output linear 4096 -> 1024 (encoder.c:219) and the projector
+    1024 -> 640 (encoder.c:744), each timed by time_launches as p2_wmatmul calls it: p2h_q8b_gemm on fp32 rows
+    (quantise, GEMM, and for the subsampling K split at its four 1024-row blocks plus the fold), beside the
+    quantiser alone and p2h_q8b_gemm_q8a (rows already quantised; no workspace, so never split). Algorithmic bytes
+    of the fp32-row route: the fp32 rows 4·M·K, the int8 plane K·N, its scales 4N, fp32 C 4·M·N."""
+    rng = np.random.default_rng(SEED + 11)
+    out = {}
+    for name, K, N in (("subsampling_4096x1024", 4096, 1024), ("projector_1024x640", 1024, 640)):
+        B = P.to_device(rng.integers(-127, 128, (K, N), dtype=np.int8))
+        bs = P.to_device(rng.uniform(0.5, 1.5, N).astype(np.float32) / 127.0)
+        dA = P.to_device(P.gen_activations(SEED, 20_100 + K, T, K))
+        ldq = P.q_ld(K)
+        dQ, dS = P.DeviceBuffer(P.q_bytes(T, K)), P.DeviceBuffer(4 * T)
+        dC = P.DeviceBuffer(T * N * 4)
+        ws = P.Workspace(P.q8b_workspace_bytes("int8w", T, N, K))
+        quant = time_launches(lambda: P.quant_rows_dev(T, K, dA.ptr, K, dQ.ptr, ldq, dS.ptr, stream.ptr), stream, reps)
+        route = time_launches(lambda: P.q8b_gemm_dev("int8w", T, N, K, 1.0, dA.ptr, K, B.ptr, N, bs.ptr, 0.0, dC.ptr, N,
+                                                     ws.ptr, ws.nbytes, stream.ptr), stream, reps)
+        q8a = time_launches(lambda: P.q8b_gemm_q8a_dev(T, N, K, 1.0, dQ.ptr, ldq, dS.ptr, B.ptr, N, bs.ptr, 0.0, dC.ptr,
+                                                       N, stream.ptr), stream, reps)
+        alg = 4 * T * K + K * N + 4 * N + 4 * T * N
+        out[name] = {"fp32_rows_us": round(route * 1e3, 3), "quant_us": round(quant * 1e3, 3),
+                     "q8a_entry_us": round(q8a * 1e3, 3),
+                     "gbs": round(alg / (route * 1e-3) / 1e9, 1),
+                     "tops": round(gemm_ops(T, N, K) / (route * 1e-3) / 1e12, 1)}
     return out
 
 

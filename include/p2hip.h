@@ -231,9 +231,16 @@ int p2h_scale_c(int M, int N, float beta, float *dC, int ldc, void *stream);
 int p2h_q8b_gemm_q8a(int M, int N, int K, float alpha, const signed char *dQ, int ldq, const float *dScales,
                      const signed char *dB, int ldb, const float *dBscales, float beta, float *dC, int ldc,
                      void *stream);
+/* p2_sgemm_q8b (blas.c:1439-1446): fp32 rows A quantised into the workspace (int8 modes), then the GEMM; P2H_EXACT
+ * (or K % 4 != 0) runs the fp32 expansion. The workspace holds the quantised rows (it must have at least that many
+ * bytes); with p2h_q8b_workspace_bytes bytes, a call with few rows and K beyond 1024 also splits K across workgroups
+ * at the 1024-row blocks (int32 partial sums folded in order by a second kernel: the same bits). Stream-ordered. */
 int p2h_q8b_gemm(int mode, int M, int N, int K, float alpha, const float *dA, int lda, const signed char *dB,
                  int ldb, const float *dBscales, float beta, float *dC, int ldc, void *workspace,
                  size_t workspace_bytes, void *stream);
+/* Workspace bytes for p2h_q8b_gemm with room to split K (0 in P2H_EXACT or when K % 4 != 0). No counterpart in the
+ * reference, which needs no device workspace. */
+size_t p2h_q8b_workspace_bytes(int mode, int M, int N, int K);
 
 /* ── fp32 GEMM (p2_sgemm, blas.h:25-29): C = alpha · op(A) · op(B) + beta · C, row-major, trans 0/1 ──────── *
  *  On the fp32 matrix cores: sums in their order, within fp32 rounding of the reference's. */

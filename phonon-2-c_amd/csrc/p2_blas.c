@@ -462,14 +462,25 @@ static void finish_c(Ctx *c, float *C, const float *dC, int M, int N, int ldc, c
     for (size_t r = 0; r < rows; r++) memcpy((char *)C + r * (size_t)ldc * 4, hp + r * width, width);
 }
 
-static void *workspace(Ctx *c, int mode, int M, int N, int K, size_t *bytes, const char *who)
+static void *workspace_of(Ctx *c, size_t need, size_t *bytes, const char *who)
 {
-    size_t need = p2h_fvb_workspace_bytes(mode, M, N, K);
     *bytes = need;
     if (need == 0) return NULL;
     dgrow(&c->dW, &c->capW, need, who);
     *bytes = c->capW;
     return c->dW;
+}
+
+/* the five-value entries' workspace (quantised rows, split partials) */
+static void *workspace(Ctx *c, int mode, int M, int N, int K, size_t *bytes, const char *who)
+{
+    return workspace_of(c, p2h_fvb_workspace_bytes(mode, M, N, K), bytes, who);
+}
+
+/* the int8-table entries' workspace (quantised rows, and room to split K) */
+static void *workspace_q8b(Ctx *c, int mode, int M, int N, int K, size_t *bytes, const char *who)
+{
+    return workspace_of(c, p2h_q8b_workspace_bytes(mode, M, N, K), bytes, who);
 }
 
 /* C = beta · C for alpha == 0 (blas.c:1434-1435, 1488 and 748-749). */
@@ -620,7 +631,7 @@ static void p2_sgemm_q8b_body(int M, int N, int K, float alpha, const float *A, 
     float *dA = upload_f32(c, &c->dA, &c->capA, A, M, K, lda, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
-    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace(c, P2H_INT8W, M, N, K, &wsb, who) : NULL;
+    void *ws = (mode != P2H_EXACT && K % 4 == 0) ? workspace_q8b(c, P2H_INT8W, M, N, K, &wsb, who) : NULL;
     check(p2h_q8b_gemm(mode, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws, wsb,
                        c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);
@@ -649,7 +660,7 @@ static void p2_sgemm_q8b_q8a_body(int M, int N, int K, float alpha, const QuantA
     float *dA = upload_f32(c, &c->dA, &c->capA, (const float *)(const void *)A->q, M, K, K, who);
     float *dC = stage_c(c, C, M, N, ldc, beta != 0.0f, who);
     size_t wsb = 0;
-    void *ws = workspace(c, P2H_INT8W, M, N, K, &wsb, who);
+    void *ws = workspace_q8b(c, P2H_INT8W, M, N, K, &wsb, who);
     check(p2h_q8b_gemm(P2H_INT8W, M, N, K, alpha, dA, K, (const signed char *)e->dq8, N, e->dsc, beta, dC, N, ws,
                        wsb, c->stream), who);
     finish_c(c, C, dC, M, N, ldc, who);

@@ -85,6 +85,7 @@ _HIP_SIG = {
     "p2h_scale_c": (_i, [_i, _i, _f, _vp, _i, _vp]),
     "p2h_q8b_gemm_q8a": (_i, [_i, _i, _i, _f, _vp, _i, _vp, _vp, _i, _vp, _f, _vp, _i, _vp]),
     "p2h_q8b_gemm": (_i, [_i, _i, _i, _i, _f, _vp, _i, _vp, _i, _vp, _f, _vp, _i, _vp, _sz, _vp]),
+    "p2h_q8b_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "p2h_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
     "p2h_sgemm_batched": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, C.c_longlong, _vp, _i, C.c_longlong, _f, _vp, _i,
                                C.c_longlong, _i, _vp]),
@@ -411,6 +412,18 @@ def fvb_gemm_q8a_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, beta, dC, ldc, ws=Non
                                ws_bytes, stream), "p2h_fvb_gemm_q8a")
 
 
+def q8b_gemm_dev(mode, M, N, K, alpha, dA, lda, dB, ldb, dBs, beta, dC, ldc, ws=None, ws_bytes=0, stream=None):
+    """p2h_q8b_gemm on device pointers: fp32 rows A [M][lda] (quantised in the call in the int8 modes)."""
+    _ok(hip().p2h_q8b_gemm(MODES.get(mode, mode), M, N, K, alpha, dA, lda, dB, ldb, dBs, beta, dC, ldc, ws,
+                           ws_bytes, stream), "p2h_q8b_gemm")
+
+
+def q8b_gemm_q8a_dev(M, N, K, alpha, dQ, ldq, dS, dB, ldb, dBs, beta, dC, ldc, stream=None):
+    """p2h_q8b_gemm_q8a on device pointers: rows already quantised (tiled, pitch ldq) with their scales."""
+    _ok(hip().p2h_q8b_gemm_q8a(M, N, K, alpha, dQ, ldq, dS, dB, ldb, dBs, beta, dC, ldc, stream),
+        "p2h_q8b_gemm_q8a")
+
+
 def fvb_gemm_q8a_silu_dev(mode, M, N, K, alpha, dQ, ldq, dS, w, dC, ws=None, ws_bytes=0, stream=None):
     """SiLU(alpha·A·W) into dC [M, N] (ldc = N): the feed-forward up-projection with SiLU applied as C is stored."""
     _ok(hip().p2h_fvb_gemm_q8a_silu(MODES.get(mode, mode), M, N, K, alpha, dQ, ldq, dS, w.ptr, dC, ws, ws_bytes,
@@ -574,14 +587,19 @@ def fv_pack_codes(w):
     return d.download((w.K * w.N,), np.int8)
 
 
-def q8b_gemm(mode, A, B, scales, alpha=1.0, beta=0.0, C0=None):
+def q8b_workspace_bytes(mode, M, N, K):
+    return hip().p2h_q8b_workspace_bytes(MODES.get(mode, mode), M, N, K)
+
+
+def q8b_gemm(mode, A, B, scales, alpha=1.0, beta=0.0, C0=None, ws_bytes=None):
+    """p2h_q8b_gemm on host arrays; ws_bytes overrides the workspace size (default: room to split K)."""
     A = np.ascontiguousarray(A, np.float32)
     B = np.ascontiguousarray(B, np.int8)
     M, K = A.shape
     N = B.shape[1]
     C0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
     dA, dB, dS, dC = to_device(A), to_device(B), to_device(np.ascontiguousarray(scales, np.float32)), to_device(C0)
-    ws = Workspace(workspace_bytes("int8w", M, N, K))
+    ws = Workspace(q8b_workspace_bytes(mode, M, N, K) if ws_bytes is None else ws_bytes)
     _ok(hip().p2h_q8b_gemm(MODES.get(mode, mode), M, N, K, alpha, dA.ptr, K, dB.ptr, N, dS.ptr, beta, dC.ptr,
                            C0.shape[1], ws.ptr, ws.nbytes, None), "p2h_q8b_gemm")
     return dC.download(C0.shape, np.float32)

@@ -242,14 +242,34 @@ def test_weight_records_only(monkeypatch, K, N):
 
 
 @pytest.mark.parametrize("mode", ["int8w", "exact"])
-@pytest.mark.parametrize("M,K,N,beta", [(11, 96, 32, 0.0), (375, 4096, 1024, 1.0), (3, 1030, 48, 0.0)])
+@pytest.mark.parametrize("M,K,N,beta", [(11, 96, 32, 0.0), (375, 4096, 1024, 1.0), (3, 1030, 48, 0.0),
+                                        (375, 1024, 640, 0.0), (200, 2100, 48, 1.0)])
 def test_q8b_parity(mode, M, K, N, beta):
+    """The int8-table GEMM (p2_sgemm_q8b) against the oracle, with the workspace that lets it split K: the encoder's
+    subsampling output (4096 -> 1024, split at the 1024-row blocks) and projector (1024 -> 640, 32 x 64 tiles) at
+    T = 375, a ragged K beyond two blocks, and small shapes."""
     B, sc = P.gen_i8_weight(SEED, 51, K, N)
     A = P.gen_activations(SEED, 52, M, K)
     C0 = P.gen_activations(SEED, 53, M, N)
     got = P.q8b_gemm(mode, A, B, sc, alpha=0.75, beta=beta, C0=C0)
     ref = O.sgemm_q8b(mode, A, B, sc, N, alpha=0.75, beta=beta, C0=C0)
     _assert_fp32(got, ref)
+
+
+@pytest.mark.parametrize("M,K,N,beta", [(375, 4096, 1024, 0.0), (375, 4096, 1024, 1.0), (200, 2100, 48, 0.5),
+                                        (1024, 3072, 512, 1.0)])
+def test_q8b_split_same_bits(M, K, N, beta):
+    """p2h_q8b_gemm splits K at the 1024-row blocks when its workspace has room (p2h_q8b_workspace_bytes) and runs
+    unsplit with only the quantised rows' room: the same bits either way."""
+    B, sc = P.gen_i8_weight(SEED, 54, K, N)
+    A = P.gen_activations(SEED, 55, M, K)
+    C0 = P.gen_activations(SEED, 56, M, N)
+    full = P.q8b_workspace_bytes("int8w", M, N, K)
+    rows_only = P.q_bytes(M, K) + 4 * M + 512
+    assert full > rows_only, "the shape must be one that splits"
+    split = P.q8b_gemm("int8w", A, B, sc, alpha=-0.5, beta=beta, C0=C0)
+    unsplit = P.q8b_gemm("int8w", A, B, sc, alpha=-0.5, beta=beta, C0=C0, ws_bytes=rows_only)
+    assert _bits_equal(split, unsplit)
 
 
 @pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
