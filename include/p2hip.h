@@ -45,8 +45,9 @@ const char *p2h_device_name(void);          /* gcnArchName of the device in use 
 int         p2h_device_cu_count(void);
 /* Re-read the tuning and comparison switches (P2H_TILE, P2H_SPLIT_ROWS, P2H_EXACT_CHAIN, P2H_XF_STAGED, P2H_XF_TILE,
  * P2H_SGEMM_ANY, P2H_ATTENTION_FUSED, P2H_SILU_EPILOGUE, P2H_EXACT_EPILOGUE, P2H_STACK_NORM_PAIRS, P2H_CONV_QUANT,
- * P2H_CONV_TT, P2H_QUANT_RPW, P2H_DEVICE_SCOPE_STORES, P2H_RECORDS_IN_REGISTERS) from the environment. They are read once at initialisation; no launch reads the
- * environment. No reference counterpart: for tests and tuning runs that change a switch within one process. */
+ * P2H_CONV_TT, P2H_QUANT_RPW, P2H_DEVICE_SCOPE_STORES, P2H_RECORDS_IN_REGISTERS, P2H_XCD_ROWS) from the
+ * environment. They are read once at initialisation; no launch reads the environment. No reference counterpart: for
+ * tests and tuning runs that change a switch within one process. */
 int         p2h_reload_switches(void);
 
 void *p2h_stream_create(void);              /* a default-priority stream; NULL on failure */

@@ -1301,6 +1301,7 @@ struct GemmArgs {
     int mg_last, ng_last;                                 /* last 16-row group of Q, last 16-column group of C */
     const uint8_t *warm; int warm_lines;                  /* 128-byte lines a later kernel reads, loaded meanwhile */
     int act;                                              /* small-M tiles: 1 stores silu_p2 of each output */
+    int xcd_rows;                                         /* small-M tiles: 0, or the rows of an XCD grid (below) */
 };
 
 /* The fold's per-column factors (blas.c:1316-1336), made from the weight's lo and hi as the reference makes them:
@@ -2476,7 +2477,17 @@ __device__ __forceinline__ void fvs_tile(const GemmArgs &g)
     __shared__ __attribute__((aligned(16))) int32_t part[(TWO ? 2 : 1) * G::MAXSEG * TILE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
+    /* Workgroup b runs on XCD b % 8. By default consecutive workgroups take consecutive column tiles, so each XCD's
+     * L2 fetches all the rows and an eighth of the weight records. With xcd_rows = a the XCDs form an a × (8 / a)
+     * grid over the tiles: XCD x takes row block x / (8 / a) and column block x % (8 / a), its L2 fetching 1 / a of
+     * the rows and a / 8 of the records. */
+    int tile_n = blockIdx.x % g.tiles_n, tile_m = blockIdx.x / g.tiles_n;
+    if (g.xcd_rows > 0) {
+        const int a = g.xcd_rows, cb = 8 / a, x = (int)blockIdx.x & 7, l = (int)blockIdx.x >> 3;
+        const int RB = g.tiles_m / a, CB = g.tiles_n / cb;
+        tile_m = (x / cb) * RB + l / CB;
+        tile_n = (x % cb) * CB + l % CB;
+    }
     const int n0 = tile_n * BN, m0 = tile_m * BM;
     const int M = g.M, N = g.N, units = g.units;
     /* one 128-byte line per thread of the range a later kernel reads (the records of the caller's next weight),

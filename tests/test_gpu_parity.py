@@ -535,6 +535,27 @@ def test_records_in_registers_same_bits(monkeypatch, M, K, N, tile):
     _assert_fp32(got["1"][rows, :N], ref)
 
 
+@pytest.mark.parametrize("M,K,N", [(375, 4096, 1024), (375, 1024, 1024), (749, 1024, 1024), (375, 1024, 4096),
+                                   (38, 4096, 1024), (256, 2048, 512)])
+def test_xcd_grid_same_bits(monkeypatch, M, K, N):
+    """The small-M tiles' XCD grid (P2H_XCD_ROWS: the default -4 takes four rows of XCDs where N < 4·M; 0, 2 and 4
+    everywhere the tiles divide) is a permutation of the tiles: the same bits as the plain order, beta 1."""
+    signs, flags, lo, hi = _weight(K, N, 970 + M)
+    w = P.FvWeight(signs, flags, lo, hi, K, N)
+    A = P.gen_activations(SEED, 971 + M, M, K)
+    q, sc = O.quant_rows(A)
+    C0 = P.gen_activations(SEED, 972 + M, M, N)
+    got = {}
+    for flag in ("0", "-4", "4", "2"):
+        monkeypatch.setenv("P2H_XCD_ROWS", flag)
+        got[flag] = P.fvb_gemm_q8a("int8w", q, sc, w, alpha=0.5, beta=1.0, C0=C0)
+    for flag in ("-4", "4", "2"):
+        assert _bits_equal(got["0"], got[flag]), flag
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, min(M, 8), replace=False)]))
+    ref = O.gemm_i8_run("int8w", q[rows], sc[rows], signs, flags, lo, hi, N, alpha=0.5, C0=C0[rows], beta_zero=False)
+    _assert_fp32(got["-4"][rows], ref)
+
+
 @pytest.mark.parametrize("M,K,N", [(6000, 1024, 4096), (6000, 4096, 1024)])
 def test_exact_full_size_sampled_rows(monkeypatch, M, K, N):
     """The exact route at the batched long-audio shapes (16 windows stacked, 12k+ workgroups on the fp32 matrix
